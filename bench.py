@@ -1,0 +1,287 @@
+"""Benchmark of the MI355X routed-expert (MoE) path.
+
+Headline workload: one MoE-layer decode step at batch 1 -- router softmax/top-8
+over 128 expert logits, then the FP8 W8A8 routed experts (hidden 2048, expert
+intermediate 768, per-output-channel E4M3 weight scales, bf16 activations) with
+the slot-order weighted combine.  A step is one layer for one token; steps
+rotate over LAYERS distinct layer banks (16 x 606 MB, far above the 256 MB
+Infinity Cache) with fresh seeded logits per step, all inputs resident in HBM,
+and are replayed from hipGraphs.
+
+Reported: value = microseconds per layer decode step (lower is better); the
+dominant kernel's roofline (gate/up GEMV, HBM-bound) from HIP events around a
+graph of back-to-back launches of that kernel alone; the reference's own CPU
+expert executor (compiled from its sources into oracle/_ref) timed on this
+host's cores on a bounded sample of the same layer shape.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "drama3-studio_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HIDDEN, INTER, EXPERTS, TOP_K = 2048, 768, 128, 8
+LAYERS = 16
+HBM_PEAK_GBS = 8000.0
+SEED = 20261202  # 20261201 + config index 1
+
+
+def log(*parts):
+    print("[bench]", *parts, file=sys.stderr, flush=True)
+
+
+def make_layer_bank(layer: int, device):
+    """One layer of 128 experts: N(0, 0.02) weights, per-channel E4M3 scales."""
+    import torch
+
+    from drama_moe.formats import StagedExperts, quantize_fp8_weights
+
+    g = torch.Generator(device=device).manual_seed(SEED * 100 + layer)
+    parts = []
+    for rows, cols in ((2 * INTER, HIDDEN), (HIDDEN, INTER)):
+        w = torch.empty(EXPERTS, rows, cols, device=device)
+        for e0 in range(0, EXPERTS, 32):
+            w[e0:e0 + 32].normal_(0.0, 0.02, generator=g)
+        q, s = quantize_fp8_weights(w, "channel")
+        del w
+        parts += [q, s]
+    return StagedExperts(*parts)
+
+
+def unique_experts(ids) -> list[int]:
+    return [len(set(row)) for row in ids]
+
+
+def run_gpu(steps: int, warmup: int):
+    import torch
+
+    from drama_moe import _lib, router
+    from drama_moe.formats import fp8_bank_struct
+    from drama_moe.offload import HipExpertBackend, device_state
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    log("device", torch.cuda.get_device_name(device))
+    banks = [make_layer_bank(layer, device) for layer in range(LAYERS)]
+    torch.cuda.synchronize()
+    log("banks ready:", LAYERS, "layers x", round(banks[0].nbytes / 1e6, 1), "MB")
+
+    g = torch.Generator(device=device).manual_seed(SEED)
+    backend = HipExpertBackend()
+    stream = torch.cuda.Stream(device)
+    # per-step inputs, resident in HBM
+    xs = torch.randn(LAYERS, 1, HIDDEN, device=device, generator=g).bfloat16()
+    logits = torch.randn(LAYERS, 1, EXPERTS, device=device, generator=g)
+    outs = torch.empty(LAYERS, 1, HIDDEN, device=device, dtype=torch.bfloat16)
+
+    def step(i):
+        weights, ids = router.route_topk(logits[i], TOP_K)
+        outs[i].copy_(backend.forward(xs[i], ids, weights, banks[i]))
+
+    # warm up the workspace and descriptor caches outside capture
+    with torch.cuda.stream(stream):
+        for i in range(LAYERS):
+            step(i)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(LAYERS):
+            step(i)
+    remainder = steps % LAYERS
+    tail = None
+    if remainder:
+        tail = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(tail, stream=stream):
+            for i in range(remainder):
+                step(i)
+    full = steps // LAYERS
+
+    for _ in range(max(1, warmup // LAYERS)):
+        graph.replay()
+    torch.cuda.synchronize()
+
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(full):
+            graph.replay()
+        if tail is not None:
+            tail.replay()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+    us_per_step = total_ms * 1e3 / steps
+
+    # routing of the timed steps (same logits every replay): distinct experts
+    with torch.no_grad():
+        ids_all = torch.stack([router.route_topk(logits[i], TOP_K)[1][0] for i in range(LAYERS)])
+    uniq = unique_experts(ids_all.cpu().tolist())
+    per_expert = 2 * INTER * HIDDEN + HIDDEN * INTER + (2 * INTER + HIDDEN) * 4
+    step_bytes = [u * per_expert + 2 * HIDDEN * 2 + EXPERTS * 4 for u in uniq]
+    alg_bytes_step = sum(step_bytes) / len(step_bytes)
+    step_gbs = alg_bytes_step / (us_per_step * 1e-6) / 1e9
+
+    # dominant kernel: gate/up alone, back-to-back over the rotating layers
+    lib = _lib.library()
+    state = device_state(device)
+    ids_dev = ids_all.contiguous()
+    w_dev = torch.full((LAYERS, TOP_K), 1.0 / TOP_K, device=device)
+    gu_bytes = [u * (2 * INTER * HIDDEN + 2 * INTER * 4) + HIDDEN * 2 + TOP_K * INTER + TOP_K * (INTER // 128) * 4
+                for u in uniq]
+    kstream = torch.cuda.Stream(device)
+    hq = torch.empty(TOP_K, INTER, dtype=torch.uint8, device=device)
+    hs = torch.empty(TOP_K, INTER // 128, device=device)
+
+    def gateup_only(i):
+        bank = fp8_bank_struct(banks[i])
+        ws = state.workspace_for(lib.dmoe_fp8_workspace_bytes(bank, TOP_K))
+        _lib.check(lib.dmoe_fp8_gate_up(
+            bank, _lib.ptr(xs[i]), _lib.BF16, HIDDEN, 1, TOP_K, _lib.ptr(ids_dev[i]), _lib.I64, TOP_K,
+            128, _lib.BF16, _lib.ptr(hq), _lib.ptr(hs), _lib.ptr(ws), ws.numel(), _lib.ptr(state.status),
+            _lib.stream_handle(device)))
+
+    kgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(kstream):
+        for i in range(LAYERS):
+            gateup_only(i)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(kgraph, stream=kstream):
+        for i in range(LAYERS):
+            gateup_only(i)
+    reps = max(1, steps // LAYERS)
+    kgraph.replay()
+    torch.cuda.synchronize()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(kstream):
+        k0.record(kstream)
+        for _ in range(reps):
+            kgraph.replay()
+        k1.record(kstream)
+    torch.cuda.synchronize()
+    k_us = k0.elapsed_time(k1) * 1e3 / (reps * LAYERS)
+    k_bytes = sum(gu_bytes) / len(gu_bytes)
+    k_gbs = k_bytes / (k_us * 1e-6) / 1e9
+    return {
+        "us_per_step": us_per_step, "total_ms": total_ms, "alg_bytes_step": alg_bytes_step,
+        "step_gbs": step_gbs, "unique_experts_mean": sum(uniq) / len(uniq),
+        "kernel_us": k_us, "kernel_bytes": k_bytes, "kernel_gbs": k_gbs,
+        "device": torch.cuda.get_device_name(device),
+    }
+
+
+def cpu_baseline(budget_s: float = 12.0):
+    """The reference CPU expert executor (oracle/_ref), one token per call with
+    8 route slots over 8 worker threads, block-128 FP8 banks of the same layer
+    shape.  Falls back to the scalar C oracle port if _ref is absent."""
+    import numpy as np
+
+    from oracle import ref_native
+
+    rng = np.random.default_rng(SEED)
+
+    def fp8_bytes(shape):
+        b = rng.integers(0, 256, size=shape, dtype=np.uint8)
+        b[(b & 0x7F) == 0x7F] = 0x3F  # no NaN codes
+        return b
+
+    w13 = fp8_bytes((EXPERTS, 2 * INTER, HIDDEN))
+    w2 = fp8_bytes((EXPERTS, HIDDEN, INTER))
+    s13 = rng.uniform(1e-4, 2e-4, (EXPERTS, 2 * INTER // 128, HIDDEN // 128)).astype(np.float32)
+    s2 = rng.uniform(1e-4, 2e-4, (EXPERTS, HIDDEN // 128, INTER // 128)).astype(np.float32)
+    x = (rng.standard_normal(HIDDEN).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    weights = np.full(TOP_K, 1.0 / TOP_K, np.float32)
+    threads = 8
+    if ref_native.available():
+        lib = ref_native.RefLibrary()
+        kind = "reference"
+        with ref_native.RefExecutor(lib, HIDDEN, INTER, capacity=TOP_K, threads=threads) as ex:
+            out = np.empty((TOP_K, HIDDEN), np.float32)
+            ex.forward(w13, s13, w2, s2, x, rng.choice(EXPERTS, TOP_K, replace=False), weights, out)
+            calls, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < budget_s or calls < 3:
+                ids = rng.choice(EXPERTS, TOP_K, replace=False).astype(np.int64)
+                ex.forward(w13, s13, w2, s2, x, ids, weights, out)
+                calls += 1
+            elapsed = time.perf_counter() - t0
+        sample = (f"{calls} layer decodes (1 token, 8 distinct random experts of 128, H 2048, I 768, "
+                  f"block-128 FP8 scales) on the reference's drama_native executor, {threads} threads")
+    else:
+        from oracle import oracle as orc
+
+        threads, kind = 1, "port"
+        b13, b2 = orc.Fp8Bank(w13, s13), orc.Fp8Bank(w2, s2)
+        xf = (x.astype(np.uint32) << 16).view(np.float32)
+        calls, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s or calls < 1:
+            ids = rng.choice(EXPERTS, TOP_K, replace=False)
+            orc.fp8_expert_pairs(b13, b2, xf, ids, weights)
+            calls += 1
+        elapsed = time.perf_counter() - t0
+        sample = f"{calls} layer decodes on the scalar C oracle port, 1 thread"
+    return {"value": elapsed * 1e6 / calls, "unit": "us", "cores": threads, "kind": kind,
+            "sample": sample}
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=4096)
+    parser.add_argument("--warmup", type=int, default=256)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path is built and "
+              "measured on a single MI355X, multi-GPU sharding is design-only.", file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs as a single process on one GPU", file=sys.stderr)
+        sys.exit(2)
+    steps = max(1, args.steps)
+    gpu = run_gpu(steps, args.warmup)
+    log("gpu", json.dumps(gpu))
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+    if cpu:
+        log("cpu", json.dumps(cpu))
+    frac = gpu["kernel_gbs"] / HBM_PEAK_GBS
+    line = {
+        "metric": "MoE-layer decode us + % peak HBM GB/s (B=1); FP8 prefill TFLOPS @2048 tok",
+        "value": round(gpu["us_per_step"], 3),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["us_per_step"] / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (W8A8, fp32 accumulate)",
+        "data": "synthetic: N(0,0.02) weights -> per-channel E4M3, N(0,1) bf16 activations and fp32 logits, seeded",
+        "config": {"workload": "MoE layer decode B=1: router top-8 of 128 + FP8 experts H2048 I768, "
+                               f"{LAYERS} rotating layer banks, hipGraph",
+                   "tokens": 1, "experts": EXPERTS, "hidden": HIDDEN, "intermediate": INTER,
+                   "top_k": TOP_K, "layers_rotated": LAYERS},
+        "hbm_gbs_step": round(gpu["step_gbs"], 1),
+        "pct_peak_hbm_step": round(100 * gpu["step_gbs"] / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gpu["kernel_gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(frac, 4), "traffic": None,
+                     "kernel": "fp8_gateup_decode_kernel", "kernel_us": round(gpu["kernel_us"], 3),
+                     "alg_bytes_per_launch": round(gpu["kernel_bytes"])},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

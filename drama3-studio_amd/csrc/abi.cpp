@@ -1,0 +1,402 @@
+// C ABI of the MoE expert path (include/drama_moe.h): argument validation,
+// workspace layout and kernel dispatch.  All validation precedes any enqueued
+// work; nothing here synchronizes the host or allocates device memory.
+#include "drama_moe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct AbiError : std::invalid_argument {
+    using std::invalid_argument::invalid_argument;
+};
+
+void require(bool ok, const char* message) {
+    if (!ok) throw AbiError(message);
+}
+
+template <class F>
+int checked(F&& body) {
+    g_last_error.clear();
+    try {
+        body();
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) throw std::runtime_error(std::string("HIP launch failed: ") + hipGetErrorString(err));
+        return 0;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+    } catch (...) {
+        g_last_error = "unknown native exception";
+    }
+    return -1;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+bool is_float_dtype(int d) { return d == DMOE_F32 || d == DMOE_BF16 || d == DMOE_F16; }
+bool is_id_dtype(int d) { return d == DMOE_I32 || d == DMOE_I64; }
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+dmoe::Fp8Proj to_kernel(const DmoeFp8Proj& p) {
+    require(p.weight && p.scale, "FP8 projection weight and scale pointers are required");
+    require(p.k >= 128 && p.k % 128 == 0, "FP8 projection K must be a positive multiple of 128");
+    require(p.n >= 16 && p.n % 8 == 0, "FP8 projection N must be a multiple of 8 and at least 16");
+    require(p.weight_stride_n >= p.k && p.weight_stride_n % 16 == 0,
+            "FP8 weight rows must be contiguous in K and 16-byte aligned");
+    require(p.weight_stride_e >= 0 && p.weight_stride_e % 16 == 0,
+            "FP8 weight expert stride must keep rows 16-byte aligned");
+    require(reinterpret_cast<uintptr_t>(p.weight) % 16 == 0, "FP8 weight base must be 16-byte aligned");
+    require((p.scale_rows == p.n) || (p.n % 128 == 0 && p.scale_rows == p.n / 128),
+            "FP8 scale rows must be N (per channel) or N/128 (128x128 blocks)");
+    require(p.scale_cols == 1 || p.scale_cols == p.k / 128,
+            "FP8 scale columns must be 1 (per channel) or K/128 (128x128 blocks)");
+    dmoe::Fp8Proj k{};
+    k.w = p.weight;
+    k.s = p.scale;
+    k.w_se = p.weight_stride_e;
+    k.w_sn = p.weight_stride_n;
+    k.s_se = p.scale_stride_e;
+    k.s_sn = p.scale_stride_n;
+    k.s_sk = p.scale_stride_k;
+    k.n_div = p.n / p.scale_rows;
+    k.kb_div = (p.k / 128) / p.scale_cols;
+    k.N = p.n;
+    k.K = p.k;
+    return k;
+}
+
+struct BankGeom {
+    dmoe::Fp8Proj w13, w2;
+    int experts, H, I;
+};
+
+BankGeom check_bank(const DmoeFp8Bank* bank) {
+    require(bank != nullptr, "FP8 bank descriptor is required");
+    BankGeom g{to_kernel(bank->w13), to_kernel(bank->w2), bank->experts, bank->w13.k,
+               bank->w13.n / 2};
+    require(g.experts >= 1 && g.experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+    require(bank->w13.n % 2 == 0 && g.I % 128 == 0, "gate/up rows must be 2 * I with I a multiple of 128");
+    require(bank->w2.n == g.H && bank->w2.k == g.I, "w2 must be [E, H, I] for w13 [E, 2I, H]");
+    require(g.H <= dmoe::kMaxHidden && g.I <= dmoe::kMaxInter, "hidden or intermediate size too large");
+    require(g.H % 8 == 0, "hidden size must be a multiple of 8");
+    return g;
+}
+
+struct Fp8Workspace {
+    float* h32;
+    uint8_t* hq;
+    float* hs;
+    int* counters;
+};
+
+// Workspace: the arrival counters come first at a fixed size, so one
+// zero-filled workspace serves calls of any pair count and bank geometry;
+// the per-pair regions follow.
+constexpr size_t kCounterBytes = (size_t)dmoe::kMaxDecodePairs * (dmoe::kMaxInter / 128) * 4;
+
+size_t fp8_workspace_layout(int pairs, int I, char* base, Fp8Workspace* ws) {
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        size_t o = off;
+        off = align256(off + n);
+        return base ? base + o : nullptr;
+    };
+    char* counters = take(kCounterBytes);
+    char* h32 = take((size_t)pairs * I * 4);
+    char* hq = take((size_t)pairs * I);
+    char* hs = take((size_t)pairs * (I / 128) * 4);
+    if (ws) {
+        ws->h32 = reinterpret_cast<float*>(h32);
+        ws->hq = reinterpret_cast<uint8_t*>(hq);
+        ws->hs = reinterpret_cast<float*>(hs);
+        ws->counters = reinterpret_cast<int*>(counters);
+    }
+    return off;
+}
+
+struct Activations {
+    const void* x;
+    int x_dtype;
+    int64_t x_row_stride;
+    const uint8_t* xq;
+    const float* xs;
+    int64_t xq_row_stride, xs_row_stride;
+    int rows, row_div, x_group;
+};
+
+void check_activations(const BankGeom& g, const Activations& a, int pairs) {
+    require(pairs >= 1, "at least one route pair is required");
+    require(pairs <= dmoe::kMaxDecodePairs,
+            "more than 256 route pairs per call: split the rows (the decode kernels take <= 256 pairs)");
+    require(a.row_div >= 1 && (int64_t)(pairs - 1) / a.row_div < a.rows, "pairs read past the activation rows");
+    require(a.x_group == 128 || a.x_group == g.H, "activation group must be 128 or the hidden size");
+    if (a.xq) {
+        require(a.xs != nullptr, "quantized activations need their scales");
+        require(a.xq_row_stride >= g.H && a.xq_row_stride % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(a.xq) % 16 == 0,
+                "quantized activation rows must be 16-byte aligned");
+        require(a.xs_row_stride >= g.H / a.x_group, "activation scale row stride too small");
+    } else {
+        require(a.x != nullptr && is_float_dtype(a.x_dtype), "activations must be fp32, bf16 or fp16");
+        require(a.x_row_stride >= g.H, "activation row stride smaller than the hidden size");
+    }
+}
+
+// Stage 1: gate/up projection, SiLU(gate) * up, FP8 128-group quantization of
+// the hidden activation into hq [pairs, I] / hs [pairs, I/128].
+void launch_gate_up(const BankGeom& g, const Activations& a, const void* ids, int ids_dtype, int pairs,
+                    int gu_dtype, uint8_t* hq, float* hs, const Fp8Workspace& ws, int* status,
+                    hipStream_t stream) {
+    dmoe::GateUpArgs ga{};
+    ga.w13 = g.w13;
+    ga.experts = g.experts;
+    ga.x = a.x;
+    ga.x_dtype = a.x_dtype;
+    ga.x_row_stride = a.x_row_stride;
+    ga.xq = a.xq;
+    ga.xs = a.xs;
+    ga.xq_row_stride = a.xq_row_stride;
+    ga.xs_row_stride = a.xs_row_stride;
+    ga.x_group = a.x_group;
+    ga.ids = ids;
+    ga.ids_dtype = ids_dtype;
+    ga.pairs = pairs;
+    ga.row_div = a.row_div;
+    ga.gu_dtype = gu_dtype;
+    ga.h32 = ws.h32;
+    ga.hq = hq;
+    ga.hs = hs;
+    ga.counters = ws.counters;
+    ga.status = status;
+    dmoe::launch_fp8_gateup_decode(ga, std::min(pairs, g.experts), stream);
+}
+
+// Stage 2: down projection of the FP8 hidden activation, route weight, and
+// either the slot-order layer combine (out) or ordered fp32 partials.
+void launch_down(const BankGeom& g, const uint8_t* hq, const float* hs, const void* ids, int ids_dtype,
+                 const void* weights, int weights_dtype, int pairs, int top_k, void* out, int out_dtype,
+                 int64_t out_row_stride, float* out_pairs, int* status, hipStream_t stream) {
+    dmoe::DownArgs da{};
+    da.w2 = g.w2;
+    da.experts = g.experts;
+    da.hq = hq;
+    da.hs = hs;
+    da.ids = ids;
+    da.ids_dtype = ids_dtype;
+    da.weights = weights;
+    da.w_dtype = weights_dtype;
+    da.pairs = pairs;
+    da.top_k = top_k;
+    da.out = out;
+    da.out_dtype = out_dtype;
+    da.out_row_stride = out_row_stride;
+    da.out_pairs = out_pairs;
+    da.status = status;
+    dmoe::launch_fp8_down_decode(da, stream);
+}
+
+Fp8Workspace take_workspace(const BankGeom& g, int pairs, void* workspace, size_t workspace_bytes) {
+    const size_t need = fp8_workspace_layout(pairs, g.I, nullptr, nullptr);
+    require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+    require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+    Fp8Workspace ws{};
+    fp8_workspace_layout(pairs, g.I, static_cast<char*>(workspace), &ws);
+    return ws;
+}
+
+void check_routes(const void* ids, int ids_dtype, const void* weights, int weights_dtype) {
+    require(ids && weights, "route ids and weights are required");
+    require(is_id_dtype(ids_dtype), "route ids must be int32 or int64");
+    require(is_float_dtype(weights_dtype), "route weights must be fp32, bf16 or fp16");
+}
+
+void check_gu_dtype(int gu_dtype) {
+    require(gu_dtype == DMOE_F32 || gu_dtype == DMOE_BF16 || gu_dtype == DMOE_F16, "bad gate/up dtype");
+}
+
+// Shared body of the three whole-path grouped FP8 entry points.
+void fp8_grouped(const BankGeom& g, const Activations& a, const void* ids, int ids_dtype,
+                 const void* weights, int weights_dtype, int pairs, int top_k, int gu_dtype,
+                 void* out, int out_dtype, int64_t out_row_stride, float* out_pairs,
+                 void* workspace, size_t workspace_bytes, int* status, hipStream_t stream) {
+    check_activations(g, a, pairs);
+    check_routes(ids, ids_dtype, weights, weights_dtype);
+    check_gu_dtype(gu_dtype);
+    if (out_pairs == nullptr) {
+        require(out != nullptr && is_float_dtype(out_dtype), "output must be fp32, bf16 or fp16");
+        require(out_row_stride >= g.H, "output row stride smaller than the hidden size");
+        require(top_k >= 1 && pairs % top_k == 0, "pairs must be tokens * top_k");
+    }
+    const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
+    launch_gate_up(g, a, ids, ids_dtype, pairs, gu_dtype, ws.hq, ws.hs, ws, status, stream);
+    launch_down(g, ws.hq, ws.hs, ids, ids_dtype, weights, weights_dtype, pairs, top_k, out, out_dtype,
+                out_row_stride, out_pairs, status, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dmoe_abi_version(void) { return DMOE_ABI_VERSION; }
+
+const char* dmoe_last_error(void) { return g_last_error.c_str(); }
+
+int dmoe_decode_fp8(const uint8_t* values, float* out, int64_t count, void* stream) {
+    return checked([&] {
+        require(count >= 0, "negative count");
+        require(count == 0 || (values && out), "decode buffers are required");
+        if (count) dmoe::launch_fp8_decode(values, out, count, as_stream(stream));
+    });
+}
+
+int dmoe_fp8_quantize(const void* x, int x_dtype, int64_t x_row_stride, int rows, int cols,
+                      int group, uint8_t* q, float* scales, int* status, void* stream) {
+    return checked([&] {
+        require(x && q && scales, "quantization buffers are required");
+        require(is_float_dtype(x_dtype), "activations must be fp32, bf16 or fp16");
+        require(rows >= 0 && cols >= 128 && cols % 128 == 0, "columns must be whole 128-value groups");
+        require(group == 128 || group == cols, "group must be 128 or the row length");
+        require(x_row_stride >= cols, "row stride smaller than the row");
+        if (!rows) return;
+        dmoe::QuantArgs a{x, x_dtype, x_row_stride, rows, cols, group, 0, q, scales, status};
+        dmoe::launch_fp8_quantize(a, as_stream(stream));
+    });
+}
+
+int dmoe_silu_mul_quant(const void* gate_up, int dtype, int64_t row_stride, int rows, int inter,
+                        uint8_t* q, float* scales, int* status, void* stream) {
+    return checked([&] {
+        require(gate_up && q && scales, "quantization buffers are required");
+        require(is_float_dtype(dtype), "gate/up must be fp32, bf16 or fp16");
+        require(rows >= 0 && inter >= 128 && inter % 128 == 0, "intermediate size must be whole 128-value groups");
+        require(row_stride >= 2 * (int64_t)inter, "row stride smaller than gate|up");
+        if (!rows) return;
+        dmoe::QuantArgs a{gate_up, dtype, row_stride, rows, inter, 128, 1, q, scales, status};
+        dmoe::launch_fp8_quantize(a, as_stream(stream));
+    });
+}
+
+int dmoe_route_topk(const float* logits, int64_t row_stride, int tokens, int experts, int top_k,
+                    int renormalize, int64_t* ids, void* weights, int weights_dtype, void* stream) {
+    return checked([&] {
+        require(logits && ids && weights, "router buffers are required");
+        require(experts >= 1 && experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        require(top_k >= 1 && top_k <= experts && top_k <= 64, "top_k outside [1, min(experts, 64)]");
+        require(tokens >= 0 && row_stride >= experts, "bad router geometry");
+        require(is_float_dtype(weights_dtype), "router weights must be fp32, bf16 or fp16");
+        if (!tokens) return;
+        dmoe::RouteArgs a{logits, row_stride, tokens, experts, top_k, renormalize != 0, ids, weights,
+                          weights_dtype};
+        dmoe::launch_route_topk(a, as_stream(stream));
+    });
+}
+
+int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t* order,
+                 int32_t* counts, int32_t* offsets, int* status, void* stream) {
+    return checked([&] {
+        require(ids && order && counts && offsets, "permutation buffers are required");
+        require(is_id_dtype(ids_dtype), "route ids must be int32 or int64");
+        require(experts >= 1 && experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 16384]");
+        dmoe::PermuteArgs a{ids, ids_dtype, pairs, experts, order, counts, offsets, status};
+        dmoe::launch_permute(a, as_stream(stream));
+    });
+}
+
+size_t dmoe_fp8_workspace_bytes(const DmoeFp8Bank* bank, int pairs) {
+    if (!bank || pairs < 1) return 0;
+    return fp8_workspace_layout(pairs, bank->w13.n / 2, nullptr, nullptr);
+}
+
+int dmoe_fp8_moe_forward(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride,
+                         int tokens, const void* ids, int ids_dtype, const void* weights,
+                         int weights_dtype, int top_k, int x_group, int gu_dtype, void* out,
+                         int out_dtype, int64_t out_row_stride, void* workspace,
+                         size_t workspace_bytes, int* status, void* stream) {
+    return checked([&] {
+        const BankGeom g = check_bank(bank);
+        require(tokens >= 1 && top_k >= 1 && top_k <= g.experts, "bad token count or top_k");
+        const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, x_group};
+        fp8_grouped(g, a, ids, ids_dtype, weights, weights_dtype, tokens * top_k, top_k, gu_dtype, out,
+                    out_dtype, out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
+    });
+}
+
+int dmoe_fp8_moe_pairs(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride,
+                       int rows, int row_div, const void* ids, int ids_dtype, const void* weights,
+                       int weights_dtype, int pairs, int x_group, int gu_dtype, float* out,
+                       void* workspace, size_t workspace_bytes, int* status, void* stream) {
+    return checked([&] {
+        const BankGeom g = check_bank(bank);
+        require(out != nullptr, "output partials are required");
+        const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, rows, row_div, x_group};
+        fp8_grouped(g, a, ids, ids_dtype, weights, weights_dtype, pairs, 1, gu_dtype, nullptr, DMOE_F32, 0,
+                    out, workspace, workspace_bytes, status, as_stream(stream));
+    });
+}
+
+int dmoe_fp8_quantized_pairs(const DmoeFp8Bank* bank, const uint8_t* xq, const float* xs,
+                             int64_t xq_row_stride, int64_t xs_row_stride, int rows, int row_div,
+                             int x_group, const void* ids, int ids_dtype, const void* weights,
+                             int weights_dtype, int pairs, int gu_dtype, float* out,
+                             void* workspace, size_t workspace_bytes, int* status, void* stream) {
+    return checked([&] {
+        const BankGeom g = check_bank(bank);
+        require(xq != nullptr, "quantized activations are required");
+        require(out != nullptr, "output partials are required");
+        const Activations a{nullptr, DMOE_F32, 0, xq, xs, xq_row_stride, xs_row_stride, rows, row_div, x_group};
+        fp8_grouped(g, a, ids, ids_dtype, weights, weights_dtype, pairs, 1, gu_dtype, nullptr, DMOE_F32, 0,
+                    out, workspace, workspace_bytes, status, as_stream(stream));
+    });
+}
+
+int dmoe_fp8_gate_up(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride, int rows,
+                     int row_div, const void* ids, int ids_dtype, int pairs, int x_group, int gu_dtype,
+                     uint8_t* hidden_q, float* hidden_scales, void* workspace, size_t workspace_bytes,
+                     int* status, void* stream) {
+    return checked([&] {
+        const BankGeom g = check_bank(bank);
+        const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, rows, row_div, x_group};
+        check_activations(g, a, pairs);
+        require(ids != nullptr && is_id_dtype(ids_dtype), "route ids must be int32 or int64");
+        check_gu_dtype(gu_dtype);
+        require(hidden_q && hidden_scales, "hidden activation outputs are required");
+        require(reinterpret_cast<uintptr_t>(hidden_q) % 16 == 0, "hidden FP8 rows must be 16-byte aligned");
+        const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
+        launch_gate_up(g, a, ids, ids_dtype, pairs, gu_dtype, hidden_q, hidden_scales, ws, status,
+                       as_stream(stream));
+    });
+}
+
+int dmoe_fp8_down(const DmoeFp8Bank* bank, const uint8_t* hidden_q, const float* hidden_scales,
+                  const void* ids, int ids_dtype, const void* weights, int weights_dtype, int pairs,
+                  int top_k, void* out, int out_dtype, int64_t out_row_stride, float* out_pairs,
+                  int* status, void* stream) {
+    return checked([&] {
+        const BankGeom g = check_bank(bank);
+        require(pairs >= 1 && pairs <= dmoe::kMaxDecodePairs, "pair count outside [1, 256]");
+        check_routes(ids, ids_dtype, weights, weights_dtype);
+        require(hidden_q && hidden_scales, "hidden activation inputs are required");
+        require(reinterpret_cast<uintptr_t>(hidden_q) % 16 == 0, "hidden FP8 rows must be 16-byte aligned");
+        if (out_pairs == nullptr) {
+            require(out != nullptr && is_float_dtype(out_dtype), "output must be fp32, bf16 or fp16");
+            require(out_row_stride >= g.H, "output row stride smaller than the hidden size");
+            require(top_k >= 1 && pairs % top_k == 0, "pairs must be tokens * top_k");
+        }
+        launch_down(g, hidden_q, hidden_scales, ids, ids_dtype, weights, weights_dtype, pairs,
+                    out_pairs ? 1 : top_k, out, out_dtype, out_row_stride, out_pairs, status,
+                    as_stream(stream));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// Kernel argument blocks and launchers shared by the C ABI (abi.cpp) and the
+// kernel translation units.  Plain structs of pointers and sizes only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dmoe {
+
+constexpr int kMaxExperts = 512;      // routed experts per bank
+constexpr int kMaxDecodePairs = 256;  // tokens * top_k handled by the decode kernels
+constexpr int kMaxHidden = 8192;
+constexpr int kMaxInter = 4096;
+
+// One FP8 projection bank [E, N, K] (K contiguous) with fp32 scales addressed
+// as s[e*s_se + (n / n_div)*s_sn + (kb / kb_div)*s_sk] for 128-column block kb.
+struct Fp8Proj {
+    const uint8_t* w;
+    const float* s;
+    int64_t w_se, w_sn;
+    int64_t s_se, s_sn, s_sk;
+    int32_t n_div, kb_div;
+    int32_t N, K;
+};
+
+struct GateUpArgs {
+    Fp8Proj w13;
+    int experts;
+    // activations: either raw rows (x) or pre-quantized rows (xq, xs)
+    const void* x;
+    int x_dtype;
+    int64_t x_row_stride;
+    const uint8_t* xq;
+    const float* xs;
+    int64_t xq_row_stride, xs_row_stride;
+    int x_group;        // 128 or K (one scale per row)
+    const void* ids;
+    int ids_dtype;
+    int pairs;
+    int row_div;        // pair p reads activation row p / row_div
+    int gu_dtype;       // storage type gate/up are rounded through
+    float* h32;         // [pairs, I] silu(gate) * up
+    uint8_t* hq;        // [pairs, I] FP8 hidden
+    float* hs;          // [pairs, I/128]
+    int* counters;      // [min(pairs, experts), I/128], zero at first use
+    int* status;
+};
+
+struct DownArgs {
+    Fp8Proj w2;
+    int experts;
+    const uint8_t* hq;
+    const float* hs;
+    const void* ids;
+    int ids_dtype;
+    const void* weights;
+    int w_dtype;
+    int pairs;
+    int top_k;
+    void* out;              // [pairs / top_k, H] in out_dtype (layer output) ...
+    int out_dtype;
+    int64_t out_row_stride;
+    float* out_pairs;       // ... or [pairs, H] fp32 partials when non-null
+    int* status;
+};
+
+constexpr int kMaxPermutePairs = 16384;  // pairs one permutation workgroup sorts
+
+struct QuantArgs {
+    const void* x;          // [rows, cols] (or [rows, 2*cols] gate|up when silu_mul)
+    int x_dtype;
+    int64_t x_row_stride;
+    int rows, cols;
+    int group;              // 128 or cols
+    int silu_mul;           // quantize silu(gate) * up instead of x
+    uint8_t* q;             // [rows, cols]
+    float* scales;          // [rows, cols / group]
+    int* status;
+};
+
+struct RouteArgs {
+    const float* logits;    // [tokens, experts], row stride in elements
+    int64_t row_stride;
+    int tokens, experts, top_k, renormalize;
+    int64_t* ids;           // [tokens, top_k]
+    void* weights;          // [tokens, top_k] in w_dtype
+    int w_dtype;
+};
+
+struct PermuteArgs {
+    const void* ids;
+    int ids_dtype;
+    int pairs, experts;
+    int32_t* order;         // [pairs], -1 past the valid pairs
+    int32_t* counts;        // [experts]
+    int32_t* offsets;       // [experts + 1]
+    int* status;
+};
+
+void launch_fp8_gateup_decode(const GateUpArgs& a, int max_active, hipStream_t stream);
+void launch_fp8_down_decode(const DownArgs& a, hipStream_t stream);
+void launch_fp8_quantize(const QuantArgs& a, hipStream_t stream);
+void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stream);
+void launch_route_topk(const RouteArgs& a, hipStream_t stream);
+void launch_permute(const PermuteArgs& a, hipStream_t stream);
+
+}  // namespace dmoe

@@ -1,0 +1,278 @@
+"""HBM-resident routed-expert runtime: the gfx950 ``ExpertBackend`` and a
+resident manager that installs it on expert modules.
+
+Reference interface: ``ExpertBackend`` (src/drama_low_vram/offload.py:187-196)
+with ``forward`` / ``forward_pairs`` and the Triton backend's
+``forward_decode_pairs`` / ``_check`` / ``.kernel`` (offload.py:247-356); the
+manager contract of ``ExpertOffloadManager`` / ``install_expert_offload``
+(offload.py:903-1063, 1534).  All experts are resident, so the staging pool,
+hot cache and host residency tiers of the reference are absent: ``staged`` is
+the whole bank and local slot ids are global expert ids.
+
+Conventions kept from the reference: kernels run on the caller's current
+stream, outputs are freshly allocated, ``ValueError`` for geometry / dtype,
+``RuntimeError`` for an unsupported device.  The backend never synchronizes
+the host; bad expert ids are reported through a device status word
+(``status()`` reads and clears it) and contribute zero.
+"""
+from __future__ import annotations
+
+import types
+
+import torch
+from torch import Tensor, nn
+
+from . import _lib
+from .formats import EXPERT_BUFFER_NAMES, FP8_DTYPE, StagedExperts, fp8_bank_struct
+
+DECODE_PAIRS = 256  # route pairs one fused decode launch pair handles
+
+
+class _DeviceState:
+    """Per-device zero-initialised workspace and status word."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.workspace = torch.zeros(0, dtype=torch.uint8, device=device)
+        self.status = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def workspace_for(self, nbytes: int) -> Tensor:
+        if self.workspace.numel() < nbytes:
+            self.workspace = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+        return self.workspace
+
+
+_STATES: dict[torch.device, _DeviceState] = {}
+
+
+def device_state(device: torch.device) -> _DeviceState:
+    state = _STATES.get(device)
+    if state is None:
+        state = _STATES[device] = _DeviceState(device)
+    return state
+
+
+def _device_of(x: Tensor) -> torch.device:
+    if x.device.type != "cuda":
+        raise RuntimeError("The HIP expert backend requires tensors on a ROCm GPU (gfx950); "
+                           f"got device {x.device}")
+    return torch.device("cuda", x.device.index if x.device.index is not None else torch.cuda.current_device())
+
+
+class HipExpertBackend:
+    """FP8 W8A8 routed experts on gfx950 MFMA (drop-in for TritonExpertBackend).
+
+    ``x_group`` = 128 follows the reference contract (one activation scale per
+    128 values); ``"token"`` uses one scale per token row (dynamic per-token
+    quantization).  ``gu_dtype`` is the type gate/up are rounded through before
+    SiLU (the reference stores them in the compute dtype; ``None`` = x.dtype).
+    """
+
+    def __init__(self, *, decode_specialization: bool = True, x_group: int | str = 128,
+                 gu_dtype: torch.dtype | None = None) -> None:
+        from . import fp8_moe
+
+        if x_group not in (128, "token"):
+            raise ValueError("x_group must be 128 or 'token'")
+        self.kernel = fp8_moe
+        self.decode_specialization = decode_specialization
+        self.x_group = x_group
+        self.gu_dtype = gu_dtype
+        self._checked_devices: set[torch.device] = set()
+
+    # -- reference helpers -------------------------------------------------
+    def _check(self, x: Tensor) -> None:
+        device = _device_of(x)
+        if device not in self._checked_devices:
+            if not self.kernel.fp8_gemm_supported([device]):
+                raise RuntimeError("The HIP expert backend requires an MI355X-class gfx950 GPU")
+            _lib.library()
+            self._checked_devices.add(device)
+
+    def status(self, device=None, clear: bool = True) -> int:
+        """Read (and clear) the device status bits; synchronizes the stream."""
+        state = device_state(torch.device(device) if device is not None else
+                             torch.device("cuda", torch.cuda.current_device()))
+        value = int(state.status.item())
+        if clear:
+            state.status.zero_()
+        return value
+
+    # -- protocol ----------------------------------------------------------
+    def forward(self, x: Tensor, ids: Tensor, weights: Tensor, staged: StagedExperts) -> Tensor:
+        self._check(x)
+        if x.ndim != 2 or ids.ndim != 2 or ids.shape[0] != x.shape[0] or weights.shape != ids.shape:
+            raise ValueError("Expected x [T, H], ids and weights [T, top_k]")
+        tokens, top_k = ids.shape
+        out = torch.empty_like(x)
+        if tokens == 0:
+            return out
+        bank = fp8_bank_struct(staged)
+        self._validate(x, staged)
+        ids, weights = ids.contiguous(), weights.contiguous()
+        state = device_state(_device_of(x))
+        chunk = max(1, DECODE_PAIRS // top_k)
+        lib = _lib.library()
+        ws = state.workspace_for(lib.dmoe_fp8_workspace_bytes(bank, min(tokens, chunk) * top_k))
+        stream = _lib.stream_handle(x.device)
+        for start in range(0, tokens, chunk):
+            stop = min(tokens, start + chunk)
+            _lib.check(lib.dmoe_fp8_moe_forward(
+                bank, _lib.ptr(x[start:stop]), _lib.dtype_code(x.dtype), x.stride(0), stop - start,
+                _lib.ptr(ids[start:stop]), _lib.dtype_code(ids.dtype), _lib.ptr(weights[start:stop]),
+                _lib.dtype_code(weights.dtype), top_k, self._group(x), self._gu(x),
+                _lib.ptr(out[start:stop]), _lib.dtype_code(out.dtype), out.stride(0),
+                _lib.ptr(ws), ws.numel(), _lib.ptr(state.status), stream))
+        return out
+
+    def forward_pairs(self, x: Tensor, ids: Tensor, weights: Tensor, staged: StagedExperts) -> Tensor:
+        """Weighted [pairs, hidden] fp32 contributions, before summing."""
+        self._check(x)
+        if ids.shape != (x.shape[0], 1) or weights.shape != ids.shape:
+            raise ValueError("Pair backend expects one expert and weight per input row")
+        return self._pairs(x, ids.reshape(-1), weights.reshape(-1), staged, row_div=1)
+
+    def forward_decode_pairs(self, x: Tensor, ids: Tensor, weights: Tensor, staged: StagedExperts) -> Tensor:
+        """Small partition of decode rows; fp32 partials (offload.py:346-356)."""
+        return self.forward_pairs(x, ids, weights, staged)
+
+    # -- internals ---------------------------------------------------------
+    def _group(self, x: Tensor) -> int:
+        return 128 if self.x_group == 128 else x.shape[-1]
+
+    def _gu(self, x: Tensor) -> int:
+        return _lib.dtype_code(self.gu_dtype or x.dtype)
+
+    def _validate(self, x: Tensor, staged: StagedExperts) -> None:
+        if x.shape[-1] != staged.hidden:
+            raise ValueError(f"Expected hidden rows [N, {staged.hidden}], got {tuple(x.shape)}")
+        if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError("Expert compute dtype must be float16, bfloat16 or float32")
+        if x.stride(-1) != 1:
+            raise ValueError("Hidden rows must be contiguous")
+        if staged.device != x.device:
+            raise ValueError("Expert bank and activations must share a device")
+
+    def _pairs(self, x: Tensor, ids: Tensor, weights: Tensor, staged: StagedExperts, *,
+               row_div: int) -> Tensor:
+        pairs = ids.numel()
+        out = torch.empty((pairs, staged.hidden), dtype=torch.float32, device=x.device)
+        if pairs == 0:
+            return out
+        bank = fp8_bank_struct(staged)
+        self._validate(x, staged)
+        ids, weights = ids.contiguous(), weights.contiguous()
+        state = device_state(_device_of(x))
+        lib = _lib.library()
+        ws = state.workspace_for(lib.dmoe_fp8_workspace_bytes(bank, min(pairs, DECODE_PAIRS)))
+        stream = _lib.stream_handle(x.device)
+        shared = x.shape[0] > 1 and x.stride(0) == 0  # an expanded single row
+        for start in range(0, pairs, DECODE_PAIRS):
+            stop = min(pairs, start + DECODE_PAIRS)
+            if shared:
+                rows, div = x[:1], stop - start
+            else:
+                rows, div = (x if row_div != 1 else x[start:stop]), row_div
+            _lib.check(lib.dmoe_fp8_moe_pairs(
+                bank, _lib.ptr(rows), _lib.dtype_code(x.dtype), max(rows.stride(0), x.shape[-1]),
+                rows.shape[0], div,
+                _lib.ptr(ids[start:stop]), _lib.dtype_code(ids.dtype), _lib.ptr(weights[start:stop]),
+                _lib.dtype_code(weights.dtype), stop - start, self._group(x), self._gu(x),
+                _lib.ptr(out[start:stop]), _lib.ptr(ws), ws.numel(), _lib.ptr(state.status), stream))
+        return out
+
+
+def store_from_module(module: nn.Module) -> StagedExperts:
+    """The four FP8 buffers of an expert module (offload.py:107-118)."""
+    if not getattr(module, "fp8", False):
+        raise ValueError("Expert offload requires FP8 buffers, not dense BF16 weights")
+    store = StagedExperts(**{name: getattr(module, name) for name in EXPERT_BUFFER_NAMES})
+    store.validate()
+    return store
+
+
+class ResidentExpertManager:
+    """Routes ``experts(x, topk_ids, topk_weights)`` of attached modules to a
+    backend with the whole bank resident (the caller contract of
+    ExpertOffloadManager.forward, offload.py:1016-1063).
+
+    ``validate_ids=True`` keeps the reference's eager check that ids lie in
+    [0, E) before any expert runs (one host sync per call); ``False`` leaves it
+    to the device status word so a call can be captured in a hipGraph.
+    """
+
+    def __init__(self, *, backend=None, validate_ids: bool = True) -> None:
+        self.backend = backend if backend is not None else HipExpertBackend()
+        self.validate_ids = validate_ids
+        self.modules: dict[str, nn.Module] = {}
+        self.forward_calls = 0
+        self._closed = False
+
+    def attach(self, name: str, module: nn.Module) -> None:
+        if self._closed:
+            raise RuntimeError("This expert manager has been closed")
+        if hasattr(module, "_drama_offload_original_forward") or name in self.modules:
+            raise ValueError(f"Expert module {name!r} already has an offload manager")
+        store_from_module(module)
+        module._drama_offload_original_forward = module.forward
+        manager = self
+
+        def forward(experts: nn.Module, x: Tensor, topk_ids: Tensor, topk_weights: Tensor) -> Tensor:
+            return manager.forward(experts, x, topk_ids, topk_weights)
+
+        module.forward = types.MethodType(forward, module)
+        self.modules[name] = module
+
+    @torch.no_grad()
+    def forward(self, module: nn.Module, x: Tensor, topk_ids: Tensor, topk_weights: Tensor) -> Tensor:
+        if self._closed:
+            raise RuntimeError("This expert manager has been closed")
+        store = store_from_module(module)
+        if x.ndim != 2 or x.shape[-1] != store.hidden:
+            raise ValueError(f"Expected hidden rows [N, {store.hidden}], got {tuple(x.shape)}")
+        if topk_ids.ndim != 2 or topk_ids.shape[0] != x.shape[0]:
+            raise ValueError("Expert IDs must have shape [tokens, top_k]")
+        if topk_weights.shape != topk_ids.shape or topk_ids.shape[1] < 1:
+            raise ValueError("Routing weights must match IDs and top_k must be positive")
+        if topk_ids.dtype not in (torch.int32, torch.int64):
+            raise ValueError("Expert IDs must have an integer dtype")
+        if topk_ids.device != x.device or topk_weights.device != x.device:
+            raise ValueError("Hidden states, expert IDs and routing weights must share a device")
+        if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError("Expert compute dtype must be float16, bfloat16 or float32")
+        if not topk_weights.is_floating_point():
+            raise ValueError("Routing weights must be floating point")
+        self.forward_calls += 1
+        if x.shape[0] == 0:
+            return torch.zeros_like(x)
+        if self.validate_ids:
+            low, high = int(topk_ids.min()), int(topk_ids.max())
+            if low < 0 or high >= store.count:
+                raise ValueError(f"Expert IDs must be in [0, {store.count})")
+        return self.backend.forward(x, topk_ids, topk_weights, store)
+
+    def close(self) -> None:
+        for module in self.modules.values():
+            original = module.__dict__.pop("_drama_offload_original_forward", None)
+            if original is not None:
+                module.forward = original
+        self.modules.clear()
+        self._closed = True
+
+
+def install_expert_offload(backbone: nn.Module, *, backend=None, validate_ids: bool = True,
+                           **_ignored) -> ResidentExpertManager:
+    """Attach a resident manager to every FP8 expert module (offload.py:1534).
+    Staging / cache keywords of the reference are accepted and ignored: every
+    expert is HBM-resident."""
+    manager = ResidentExpertManager(backend=backend, validate_ids=validate_ids)
+    for name, module in backbone.named_modules():
+        if getattr(module, "fp8", False) and all(hasattr(module, n) for n in EXPERT_BUFFER_NAMES):
+            manager.attach(name, module)
+    if not manager.modules:
+        raise ValueError("No FP8 expert modules found")
+    return manager
+
+
+__all__ = ["HipExpertBackend", "ResidentExpertManager", "install_expert_offload",
+           "store_from_module", "StagedExperts", "FP8_DTYPE", "DECODE_PAIRS"]

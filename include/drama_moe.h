@@ -1,0 +1,182 @@
+/*
+ * drama_moe.h -- C ABI of the MI355X (gfx950) quantized MoE expert path.
+ *
+ * Conventions (kept from the reference's native ABI, native/include/drama_native.h:1-32
+ * and native/src/runtime.cpp:278-290):
+ *   - extern "C", default-visibility symbols, no C++ or tensor types;
+ *   - every call returns 0 on success or -1 with a thread-local message
+ *     readable through dmoe_last_error();
+ *   - every argument is validated before any work is enqueued;
+ *   - buffers are borrowed and caller-owned.  Unlike the reference's CPU ABI,
+ *     pointers are DEVICE pointers and calls are ASYNCHRONOUS: work is enqueued
+ *     on `stream` (a hipStream_t; NULL = the legacy default stream) and the
+ *     library never synchronizes the host, so every entry point may be
+ *     captured in a hipGraph;
+ *   - no entry point allocates device memory; scratch comes from the caller's
+ *     `workspace` (size from the matching *_workspace_bytes query), which must
+ *     be zero-filled once when first allocated -- the library leaves its
+ *     counter region zeroed after every call;
+ *   - `status` (optional, may be NULL) is a device int the kernels OR their
+ *     DMOE_STATUS_* bits into, so a caller can check data errors (bad expert
+ *     ids, non-finite activations) without a per-call host sync.
+ */
+#ifndef DRAMA_MOE_H
+#define DRAMA_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define DMOE_API __attribute__((visibility("default")))
+#define DMOE_ABI_VERSION 1
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element codes. */
+enum { DMOE_F32 = 0, DMOE_BF16 = 1, DMOE_F16 = 2, DMOE_I32 = 3, DMOE_I64 = 4 };
+
+/* Status bits written to the optional device status word. */
+enum {
+    DMOE_STATUS_BAD_EXPERT_ID = 1, /* route id outside [0, experts): that pair contributes 0 */
+    DMOE_STATUS_NON_FINITE = 2,    /* non-finite value met by an FP8 quantizer */
+    DMOE_STATUS_TOO_MANY_ROWS = 4
+};
+
+/* One FP8 E4M3 projection bank: weight [E, N, K] with K contiguous (row and
+ * expert strides in bytes, rows 16-byte aligned), fp32 scales of shape
+ * [E, scale_rows, scale_cols] with element strides.  scale_rows is N/128
+ * (the reference's 128x128 block scales, offload.py:44-56) or N (one scale per
+ * output channel); scale_cols is K/128 (block) or 1 (per channel).  The
+ * reference's StagedExperts fields map as w13_weight/w13_scale_inv ->
+ * DmoeFp8Bank.w13 and w2_weight/w2_scale_inv -> .w2 (offload.py:175-184). */
+typedef struct DmoeFp8Proj {
+    const uint8_t* weight;
+    const float* scale;
+    int64_t weight_stride_e, weight_stride_n;
+    int64_t scale_stride_e, scale_stride_n, scale_stride_k;
+    int32_t scale_rows, scale_cols;
+    int32_t n, k;
+} DmoeFp8Proj;
+
+typedef struct DmoeFp8Bank {
+    DmoeFp8Proj w13; /* [E, 2I, H] gate rows 0..I-1, up rows I..2I-1 */
+    DmoeFp8Proj w2;  /* [E, H, I] */
+    int32_t experts;
+} DmoeFp8Bank;
+
+/* ABI version (DMOE_ABI_VERSION).  Replaces drama_native_abi
+ * (native/include/drama_native.h:16; runtime.cpp:288). */
+DMOE_API int dmoe_abi_version(void);
+
+/* Last error message of the calling thread.  Replaces drama_native_error
+ * (native/include/drama_native.h:19; runtime.cpp:290). */
+DMOE_API const char* dmoe_last_error(void);
+
+/* E4M3 -> fp32 of `count` bytes on the device.  Replaces drama_decode_fp8
+ * (native/include/drama_native.h:37). */
+DMOE_API int dmoe_decode_fp8(const uint8_t* values, float* out, int64_t count, void* stream);
+
+/* Dynamic FP8 quantization of rows x[rows, cols] (dtype bf16/fp16/fp32, row
+ * stride in elements) in `group`-column groups, group = 128 or cols (one scale
+ * per row).  q [rows, cols] E4M3, scales [rows, cols/group] fp32.  Replaces the
+ * fish fp8_moe quantize_groups(quant_kernel, x, H) launch
+ * (src/drama_low_vram/fp8_decode.py:117; offload.py:308-310) and
+ * drama_quantize_bf16 (native/include/drama_native.h:38-39). */
+DMOE_API int dmoe_fp8_quantize(const void* x, int x_dtype, int64_t x_row_stride, int rows,
+                               int cols, int group, uint8_t* q, float* scales, int* status,
+                               void* stream);
+
+/* h = silu(gate) * up of gate_up[rows, 2*inter] (gate columns first), then FP8
+ * 128-group quantization into q [rows, inter], scales [rows, inter/128].
+ * Replaces quantize_groups(silu_mul_quant_kernel, gu, I)
+ * (src/drama_low_vram/fp8_decode.py:133-135; offload.py:326-328). */
+DMOE_API int dmoe_silu_mul_quant(const void* gate_up, int dtype, int64_t row_stride, int rows,
+                                 int inter, uint8_t* q, float* scales, int* status, void* stream);
+
+/* Router: p = softmax(logits), top_k experts in (logit desc, index asc)
+ * order, weights = p (renormalize: / slot-order sum) stored as weights_dtype.
+ * logits [tokens, experts] fp32 (row stride in elements); ids [tokens, top_k]
+ * int64.  Replaces the router of backbone_graph.py:317-323. */
+DMOE_API int dmoe_route_topk(const float* logits, int64_t row_stride, int tokens, int experts,
+                             int top_k, int renormalize, int64_t* ids, void* weights,
+                             int weights_dtype, void* stream);
+
+/* Stable expert-major permutation of pairs = tokens * top_k flattened route
+ * ids (int32 or int64): order [pairs] (-1 past the valid pairs), counts
+ * [experts], offsets [experts + 1].  Replaces the argsort(stable)/bincount/
+ * starts of ExpertOffloadManager._forward_partitioned (offload.py:1206-1210). */
+DMOE_API int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t* order,
+                          int32_t* counts, int32_t* offsets, int* status, void* stream);
+
+/* Workspace bytes for dmoe_fp8_moe_forward / _pairs / _quantized_pairs. */
+DMOE_API size_t dmoe_fp8_workspace_bytes(const DmoeFp8Bank* bank, int pairs);
+
+/* Whole routed-expert call: x [tokens, H] (bf16/fp16/fp32, row stride in
+ * elements), ids/weights [tokens, top_k] contiguous, out [tokens, H] in
+ * out_dtype = fp32 sum of the weighted expert partials in router slot order.
+ * x_group = 128 (reference contract) or H (one activation scale per token);
+ * gu_dtype = type the gate/up projection is stored in before SiLU (the
+ * reference uses the compute dtype).  Replaces ExpertBackend.forward
+ * (offload.py:187-196) of TritonExpertBackend (offload.py:269-287) and the
+ * direct decode fp8_decode.forward (fp8_decode.py:114-119). */
+DMOE_API int dmoe_fp8_moe_forward(const DmoeFp8Bank* bank, const void* x, int x_dtype,
+                                  int64_t x_row_stride, int tokens, const void* ids, int ids_dtype,
+                                  const void* weights, int weights_dtype, int top_k, int x_group,
+                                  int gu_dtype, void* out, int out_dtype, int64_t out_row_stride,
+                                  void* workspace, size_t workspace_bytes, int* status,
+                                  void* stream);
+
+/* Ordered weighted fp32 partials [pairs, H], one per route pair, before any
+ * summation; pair p reads activation row p / row_div (1: one row per pair,
+ * top_k: token-major pairs, pairs: one shared row).  Replaces
+ * ExpertBackend.forward_pairs (offload.py:289-344) and
+ * TritonExpertBackend.forward_decode_pairs (offload.py:346-356). */
+DMOE_API int dmoe_fp8_moe_pairs(const DmoeFp8Bank* bank, const void* x, int x_dtype,
+                                int64_t x_row_stride, int rows, int row_div, const void* ids,
+                                int ids_dtype, const void* weights, int weights_dtype, int pairs,
+                                int x_group, int gu_dtype, float* out, void* workspace,
+                                size_t workspace_bytes, int* status, void* stream);
+
+/* As dmoe_fp8_moe_pairs with an activation already quantized by the caller:
+ * xq [rows, H] E4M3 and xs [rows, H/x_group] fp32.  Replaces
+ * fp8_decode.quantized_pairs (fp8_decode.py:122-147) and the quantized handoff
+ * drama_executor_forward_quantized (native/include/drama_native.h:57-64). */
+DMOE_API int dmoe_fp8_quantized_pairs(const DmoeFp8Bank* bank, const uint8_t* xq, const float* xs,
+                                      int64_t xq_row_stride, int64_t xs_row_stride, int rows,
+                                      int row_div, int x_group, const void* ids, int ids_dtype,
+                                      const void* weights, int weights_dtype, int pairs,
+                                      int gu_dtype, float* out, void* workspace,
+                                      size_t workspace_bytes, int* status, void* stream);
+
+/* Decode stage 1 (gate/up): for the route pairs (pair p reads activation row
+ * p / row_div), gate/up = block-scaled FP8 projection of the FP8-quantized
+ * activation, rounded through gu_dtype, h = silu(gate) * up, then FP8
+ * 128-group quantization into hidden_q [pairs, I] E4M3 and hidden_scales
+ * [pairs, I/128] fp32.  Replaces the first decode_gemm launch plus
+ * quantize_groups(silu_mul_quant_kernel) of fp8_decode.quantized_pairs
+ * (fp8_decode.py:130-146) and runtime.cpp:184-225 of the CPU executor. */
+DMOE_API int dmoe_fp8_gate_up(const DmoeFp8Bank* bank, const void* x, int x_dtype,
+                              int64_t x_row_stride, int rows, int row_div, const void* ids,
+                              int ids_dtype, int pairs, int x_group, int gu_dtype,
+                              uint8_t* hidden_q, float* hidden_scales, void* workspace,
+                              size_t workspace_bytes, int* status, void* stream);
+
+/* Decode stage 2 (down + combine): partial_p = route_weight_p * (block-scaled
+ * FP8 down projection of hidden p).  With out_pairs == NULL the partials of
+ * each token (pairs = tokens * top_k, token-major) are summed in router slot
+ * order in fp32 and stored to out [tokens, H] in out_dtype; otherwise the
+ * ordered fp32 partials go to out_pairs [pairs, H].  Replaces the second
+ * decode_gemm launch (ROUTE_WEIGHT) and down.sum(0) of fp8_decode.py:54-55,
+ * 119, and the combine of offload.py:1242-1244. */
+DMOE_API int dmoe_fp8_down(const DmoeFp8Bank* bank, const uint8_t* hidden_q,
+                           const float* hidden_scales, const void* ids, int ids_dtype,
+                           const void* weights, int weights_dtype, int pairs, int top_k, void* out,
+                           int out_dtype, int64_t out_row_stride, float* out_pairs, int* status,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DRAMA_MOE_H */

@@ -1,0 +1,17 @@
+"""CPU oracle for the quantized MoE expert path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this package, and only as the checker.  The product
+(``drama3-studio_amd/drama_moe``) never imports it.
+
+Contents
+--------
+``moe_oracle.c``   scalar C restatement of the reference arithmetic
+                   (FP8 codec, dynamic FP8 quant, block-scaled W8A8 expert
+                   pairs, router top-k, stable permutation, packed W4A16 /
+                   INT8 / W6A8 / W4A8 projections, H256 rotation).
+``oracle.py``      ctypes + numpy wrapper of ``liboracle.so``.
+``ref_native.py``  ctypes binding of the reference's own CPU expert executor
+                   (``native/include/drama_native.h``), compiled from the
+                   reference sources into ``_ref/`` by ``make ref``.
+"""

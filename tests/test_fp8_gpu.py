@@ -1,0 +1,394 @@
+"""GPU parity of the FP8 W8A8 expert path against the CPU oracle.
+
+Bars (north-star): routing ids, top-k order and the permutation bit-exact;
+FP8 bytes and scales of the activation quantizer bit-exact; expert outputs
+within ||y - r||_inf / ||r||_inf <= 2e-2 of the contract oracle (activation
+quantization emulated, bf16 gate/up boundary), which also absorbs FP8 re-quant
+flips of the hidden activation caused by fp32 summation order.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import print_case
+from drama_moe import fp8_decode, fp8_moe, router
+from drama_moe.formats import StagedExperts, random_fp8_bank
+from drama_moe.offload import HipExpertBackend, ResidentExpertManager, install_expert_offload
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+TOL = 2e-2
+
+
+def rel_inf(actual, expected):
+    actual = np.asarray(actual, np.float64)
+    expected = np.asarray(expected, np.float64)
+    return float(np.max(np.abs(actual - expected)) / max(np.max(np.abs(expected)), 1e-30))
+
+
+def oracle_banks(staged: StagedExperts):
+    return (orc.Fp8Bank(staged.w13_weight.view(torch.uint8).cpu().numpy(), staged.w13_scale_inv.cpu().numpy()),
+            orc.Fp8Bank(staged.w2_weight.view(torch.uint8).cpu().numpy(), staged.w2_scale_inv.cpu().numpy()))
+
+
+def to_device(staged: StagedExperts, device) -> StagedExperts:
+    return StagedExperts(*(getattr(staged, n).to(device) for n in
+                           ("w13_weight", "w13_scale_inv", "w2_weight", "w2_scale_inv")))
+
+
+@pytest.fixture(scope="module", autouse=True)
+def built():
+    orc.build()
+
+
+# ----------------------------------------------------------------- codecs
+
+def test_device_fp8_decode_all_bytes(cuda):
+    print_case("decode_fp8 all bytes")
+    raw = torch.arange(256, dtype=torch.uint8, device=cuda)
+    actual = router.decode_fp8(raw).cpu()
+    expected = raw.cpu().view(torch.float8_e4m3fn).float()
+    torch.testing.assert_close(actual, expected, rtol=0, atol=0, equal_nan=True)
+    assert bool(torch.signbit(actual[128]))
+
+
+@pytest.mark.parametrize("kind", ["random", "zero", "tiny", "saturated"])
+def test_activation_quant_exact_bytes_and_scales(cuda, kind):
+    # test_native_backend.py:41-55 scenarios, against the reference executor's bytes
+    print_case("quantize", kind)
+    data = np.load(GOLDEN / "fp8_quant.npz")
+    x = torch.randn(16, 128, generator=torch.Generator().manual_seed(22))
+    if kind == "zero":
+        x.zero_()
+        x[0, :4] = torch.tensor([0.0, -0.0, 0.0, -0.0])
+    elif kind == "tiny":
+        x *= 1e-20
+    elif kind == "saturated":
+        x *= 1e20
+    x = x.to(torch.bfloat16).to(cuda)
+    q, s = fp8_moe.quantize_groups(fp8_moe.quant_kernel, x, 128)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy().reshape(-1), data[f"{kind}_q"])
+    np.testing.assert_array_equal(s.cpu().numpy().reshape(-1), data[f"{kind}_s"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("group", [128, "row"])
+def test_activation_quant_matches_oracle_on_wide_rows(cuda, dtype, group):
+    print_case("quantize wide", dtype, group)
+    from drama_moe import _lib
+    from drama_moe.offload import device_state
+
+    x = (torch.randn(37, 2048, generator=torch.Generator().manual_seed(3)) * 3).to(dtype)
+    g = 128 if group == 128 else 2048
+    q = torch.empty(37, 2048, dtype=torch.uint8, device=cuda)
+    s = torch.empty(37, 2048 // g, device=cuda)
+    xd = x.to(cuda)
+    _lib.check(_lib.library().dmoe_fp8_quantize(
+        _lib.ptr(xd), _lib.dtype_code(dtype), 2048, 37, 2048, g, _lib.ptr(q), _lib.ptr(s),
+        _lib.ptr(device_state(cuda).status), _lib.stream_handle(cuda)))
+    eq, es = orc.quantize_fp8(x.float().numpy(), g)
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+    np.testing.assert_array_equal(s.cpu().numpy(), es)
+
+
+def test_silu_mul_quant_matches_oracle_within_one_step(cuda):
+    print_case("silu_mul_quant")
+    gu = (torch.randn(9, 2 * 768, generator=torch.Generator().manual_seed(5)) * 4).bfloat16()
+    q, s = fp8_moe.quantize_groups(fp8_moe.silu_mul_quant_kernel, gu.to(cuda), 768)
+    g, u = gu.float().numpy()[:, :768], gu.float().numpy()[:, 768:]
+    h = orc.silu(g) * u
+    eq, es = orc.quantize_fp8(h)
+    np.testing.assert_allclose(s.cpu().numpy(), es, rtol=1e-6)
+    dq = orc.fp8_decode(q.view(torch.uint8).cpu().numpy()) * np.repeat(s.cpu().numpy(), 128, 1)
+    de = orc.fp8_decode(eq) * np.repeat(es, 128, 1)
+    assert rel_inf(dq, de) < 2 ** -3
+    assert np.mean(q.view(torch.uint8).cpu().numpy() == eq) > 0.999
+
+
+# ------------------------------------------------------------------ routing
+
+@pytest.mark.parametrize("tokens,experts,top_k", [(1, 128, 8), (16, 128, 8), (2048, 128, 8), (5, 256, 8), (3, 20, 4)])
+def test_route_topk_bit_exact_ids_and_order(cuda, tokens, experts, top_k):
+    print_case("route_topk", tokens, experts, top_k)
+    logits = torch.randn(tokens, experts, generator=torch.Generator().manual_seed(20261202 + tokens))
+    weights, ids = router.route_topk(logits.to(cuda), top_k, dtype=torch.float32)
+    eids, ew = orc.route_topk(logits.numpy(), top_k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), eids)
+    tw, ti = torch.softmax(logits, -1).topk(top_k, -1)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ti.numpy())  # tie-free draw
+    np.testing.assert_allclose(weights.cpu().numpy(), ew, rtol=1e-5, atol=0)
+    wb, _ = router.route_topk(logits.to(cuda), top_k, dtype=torch.bfloat16)
+    ref = (tw / tw.sum(-1, keepdim=True)).bfloat16().float()
+    assert torch.max((wb.cpu().float() - ref).abs() / ref).item() <= 2 ** -7
+
+
+def test_route_topk_ties_take_the_lower_index(cuda):
+    print_case("route_topk ties")
+    logits = torch.full((2, 16), -1.0)
+    logits[0, [3, 1]] = 2.0
+    logits[1, [15, 0]] = 2.0
+    _, ids = router.route_topk(logits.to(cuda), 4)
+    np.testing.assert_array_equal(ids.cpu().numpy(), orc.route_topk(logits.numpy(), 4)[0])
+
+
+@pytest.mark.parametrize("tokens,experts", [(1, 128), (16, 128), (2048, 128), (300, 7), (64, 512)])
+def test_permute_bit_exact_against_stable_argsort(cuda, tokens, experts):
+    print_case("permute", tokens, experts)
+    g = torch.Generator().manual_seed(tokens + experts)
+    # Zipf(1.1) expert popularity for the prefill shape
+    p = torch.arange(1, experts + 1, dtype=torch.float64) ** -1.1
+    ids = torch.multinomial(p.repeat(tokens, 1), min(8, experts), generator=g)
+    order, counts, offsets = router.permute(ids.to(cuda), experts)
+    flat = ids.reshape(-1)
+    np.testing.assert_array_equal(order.cpu().numpy(), torch.argsort(flat, stable=True).numpy())
+    np.testing.assert_array_equal(counts.cpu().numpy(), torch.bincount(flat, minlength=experts).numpy())
+    eo, ec, eoff = orc.permute(ids.numpy(), experts)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), eoff)
+
+
+def test_permute_drops_and_flags_invalid_ids(cuda):
+    print_case("permute invalid")
+    backend = HipExpertBackend()
+    backend.status(cuda)
+    ids = torch.tensor([[3, 9, 1, -1]], device=cuda)
+    order, counts, offsets = router.permute(ids, 8)
+    assert backend.status(cuda) & 1
+    assert order.cpu().tolist() == [2, 0, -1, -1]
+    assert counts.cpu().tolist() == [0, 1, 0, 1, 0, 0, 0, 0]
+
+
+# -------------------------------------------------------- expert pairs / layer
+
+@pytest.mark.parametrize("case", ["s194", "s882"])
+def test_pairs_match_golden_reference_executor(cuda, case):
+    print_case("golden pairs", case)
+    data = np.load(GOLDEN / "fp8_pairs.npz")
+    staged = StagedExperts(
+        torch.from_numpy(data[f"{case}_w13"]).view(torch.float8_e4m3fn).to(cuda),
+        torch.from_numpy(data[f"{case}_s13"]).to(cuda),
+        torch.from_numpy(data[f"{case}_w2"]).view(torch.float8_e4m3fn).to(cuda),
+        torch.from_numpy(data[f"{case}_s2"]).to(cuda))
+    x = torch.from_numpy(data[f"{case}_x"].view(np.int16)).view(torch.bfloat16).to(cuda).reshape(1, -1)
+    ids = torch.from_numpy(data[f"{case}_ids"]).to(cuda)
+    weights = torch.from_numpy(data[f"{case}_weights"]).to(cuda)
+    rows = x.expand(ids.numel(), -1)
+    actual = HipExpertBackend().forward_pairs(rows, ids[:, None], weights[:, None], staged)
+    assert actual.dtype == torch.float32
+    assert rel_inf(actual.cpu().numpy(), data[f"{case}_out"]) < TOL
+    # duplicates keep separate ordered partials (test_native_backend.py:76)
+    if case == "s194":
+        torch.testing.assert_close(actual[0] / 0.4, actual[2] / 0.3, rtol=1e-6, atol=1e-6)
+
+
+def _layer_case(cuda, experts, hidden, inter, tokens, top_k, layout, dtype, seed, x_group=128,
+                bank_on_device=False):
+    g = torch.Generator().manual_seed(seed)
+    if bank_on_device:  # large banks: draw on the GPU, copy to the host for the oracle
+        staged = random_fp8_bank(experts, hidden, inter, layout=layout, device=cuda,
+                                 generator=torch.Generator(device=cuda).manual_seed(seed))
+    else:
+        staged = random_fp8_bank(experts, hidden, inter, layout=layout, generator=g)
+    x = torch.randn(tokens, hidden, generator=g).to(dtype)
+    logits = torch.randn(tokens, experts, generator=g)
+    ids, w = orc.route_topk(logits.numpy(), top_k)
+    weights = torch.from_numpy(w).to(dtype)
+    b13, b2 = oracle_banks(staged)
+    gu = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
+    expected = orc.fp8_moe_forward(b13, b2, x.float().numpy(), ids, weights.float().numpy(),
+                                   x_group=x_group, gu_dtype=gu, out_dtype=gu)
+    return to_device(staged, cuda), x.to(cuda), torch.from_numpy(ids).to(cuda), weights.to(cuda), expected
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 16])
+@pytest.mark.parametrize("layout", ["block", "channel"])
+def test_layer_decode_matches_oracle(cuda, tokens, layout):
+    print_case("layer decode", tokens, layout)
+    staged, x, ids, weights, expected = _layer_case(cuda, 32, 2048, 768, tokens, 8, layout, torch.bfloat16,
+                                                    20261201 + tokens)
+    out = HipExpertBackend().forward(x, ids, weights, staged)
+    assert out.dtype == torch.bfloat16 and out.shape == x.shape
+    assert rel_inf(out.float().cpu().numpy(), expected) < TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_layer_decode_other_compute_dtypes(cuda, dtype):
+    print_case("layer dtype", dtype)
+    staged, x, ids, weights, expected = _layer_case(cuda, 8, 256, 256, 2, 8, "block", dtype, 77)
+    out = HipExpertBackend().forward(x, ids, weights, staged)
+    assert out.dtype == dtype
+    assert rel_inf(out.float().cpu().numpy(), expected) < TOL
+
+
+def test_layer_decode_per_token_activation_scales(cuda):
+    print_case("per-token scales")
+    staged, x, ids, weights, expected = _layer_case(cuda, 16, 2048, 768, 4, 8, "channel", torch.bfloat16,
+                                                    99, x_group=2048)
+    out = HipExpertBackend(x_group="token").forward(x, ids, weights, staged)
+    assert rel_inf(out.float().cpu().numpy(), expected) < TOL
+
+
+@pytest.mark.parametrize("hidden,inter", [(128, 128), (256, 256), (2048, 512)])
+def test_duplicate_and_permuted_routes(cuda, hidden, inter):
+    # test_fp8_decode.py:12-38 route patterns
+    print_case("routes", hidden, inter)
+    g = torch.Generator().manual_seed(9274)
+    staged = random_fp8_bank(8, hidden, inter, generator=g)
+    b13, b2 = oracle_banks(staged)
+    dev = to_device(staged, cuda)
+    for route in ([6], [7, 1], [3, 1, 3, 0, 2, 7, 1, 5], list(reversed(range(8)))):
+        x = torch.randn(1, hidden, generator=g).bfloat16()
+        weights = torch.softmax(torch.randn(1, len(route), generator=g), -1).bfloat16()
+        expected = orc.fp8_moe_forward(b13, b2, x.float().numpy(), np.array([route]), weights.float().numpy())
+        out = HipExpertBackend().forward(x.to(cuda), torch.tensor([route], device=cuda), weights.to(cuda), dev)
+        assert rel_inf(out.float().cpu().numpy(), expected) < TOL, route
+
+
+def test_strided_banks_and_int32_ids(cuda):
+    # test_fp8_decode.py:41-66: K-strided weights, strided scales and ids
+    print_case("strided")
+    g = torch.Generator().manual_seed(2136)
+    w13 = torch.randn(8, 256, 512, generator=g).to(torch.float8_e4m3fn)[..., ::2]
+    s13 = (torch.rand(8, 2, 4, generator=g) * 0.02 + 0.001)[..., ::2]
+    w2 = torch.randn(8, 256, 256, generator=g).to(torch.float8_e4m3fn)[..., ::2]
+    s2 = (torch.rand(8, 2, 2, generator=g) * 0.02 + 0.001)[..., ::2]
+    host = StagedExperts(w13.contiguous(), s13.contiguous(), w2.contiguous(), s2.contiguous())
+    dev = StagedExperts(
+        torch.zeros(8, 256, 512, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)[..., ::2],
+        torch.zeros(8, 2, 4, device=cuda)[..., ::2],
+        torch.zeros(8, 256, 256, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)[..., ::2],
+        torch.zeros(8, 2, 2, device=cuda)[..., ::2])
+    dev.w13_weight.view(torch.uint8).copy_(host.w13_weight.view(torch.uint8))
+    dev.w13_scale_inv.copy_(host.w13_scale_inv)
+    dev.w2_weight.view(torch.uint8).copy_(host.w2_weight.view(torch.uint8))
+    dev.w2_scale_inv.copy_(host.w2_scale_inv)
+    assert dev.w13_weight.stride(2) == 2
+    ids = torch.tensor([[3, 0, 2, 0, 6, 0, 1, 0]], device=cuda, dtype=torch.int32)[:, ::2]
+    x = torch.randn(1, 256, generator=g).bfloat16()
+    weights = torch.tensor([[0.4, 0.3, 0.2, 0.1]], dtype=torch.bfloat16)
+    b13, b2 = oracle_banks(host)
+    expected = orc.fp8_moe_forward(b13, b2, x.float().numpy(), ids.cpu().numpy(), weights.float().numpy())
+    out = HipExpertBackend().forward(x.to(cuda), ids, weights.to(cuda), dev)
+    assert rel_inf(out.float().cpu().numpy(), expected) < TOL
+
+
+def test_slot_order_reduction_on_device(cuda):
+    # test_offload.py:394-409: +-1e20 partials, only a slot-order fp32 sum gives 3p
+    print_case("slot order")
+    staged = random_fp8_bank(4, 128, 128, generator=torch.Generator().manual_seed(194))
+    dev = to_device(staged, cuda)
+    x = torch.linspace(-1, 1, 128).bfloat16().reshape(1, -1).to(cuda)
+    backend = HipExpertBackend(gu_dtype=torch.bfloat16)
+    single = backend.forward_pairs(x, torch.tensor([[1]], device=cuda), torch.ones(1, 1, device=cuda), dev)
+    ids = torch.tensor([[1, 1, 1, 1]], device=cuda)
+    weights = torch.tensor([[1e20, 1.0, -1e20, 3.0]], device=cuda)
+    out = backend.forward(x.float(), ids, weights, dev)
+    torch.testing.assert_close(out, single * 3.0, rtol=0, atol=0)
+
+
+def test_invalid_ids_contribute_zero_and_raise_status(cuda):
+    print_case("invalid ids")
+    staged = to_device(random_fp8_bank(4, 128, 128, generator=torch.Generator().manual_seed(3)), cuda)
+    backend = HipExpertBackend()
+    backend.status(cuda)
+    x = torch.randn(1, 128, device=cuda).bfloat16()
+    good = backend.forward(x, torch.tensor([[2, 1]], device=cuda), torch.tensor([[0.5, 0.5]], device=cuda), staged)
+    bad = backend.forward(x, torch.tensor([[2, 1, 7]], device=cuda), torch.tensor([[0.5, 0.5, 0.5]], device=cuda), staged)
+    assert backend.status(cuda) & 1
+    torch.testing.assert_close(bad, good, rtol=0, atol=0)
+    manager = ResidentExpertManager(backend=backend)
+    module = torch.nn.Module()
+    module.fp8 = True
+    for name in ("w13_weight", "w13_scale_inv", "w2_weight", "w2_scale_inv"):
+        module.register_buffer(name, getattr(staged, name))
+    manager.attach("experts", module)
+    with pytest.raises(ValueError, match="Expert IDs must be in"):
+        module(x, torch.tensor([[4]], device=cuda), torch.ones(1, 1, device=cuda))
+
+
+def test_quantized_handoff_equals_raw_path(cuda):
+    # test_native_backend.py:116-127: shared FP8 input == raw bf16 input
+    print_case("quantized handoff")
+    g = torch.Generator().manual_seed(44)
+    staged = to_device(random_fp8_bank(4, 256, 256, generator=g), cuda)
+    x = torch.randn(1, 256, generator=g).bfloat16().to(cuda)
+    ids = torch.tensor([3, 1, 0], device=cuda)
+    weights = torch.tensor([0.5, 0.3, 0.2], device=cuda)
+    q, s = fp8_moe.quantize_groups(fp8_moe.quant_kernel, x, 256)
+    handoff = fp8_decode.quantized_pairs(fp8_moe, q, s, ids, weights, staged)
+    raw = HipExpertBackend().forward_pairs(x.expand(3, -1), ids[:, None], weights[:, None], staged)
+    assert torch.equal(handoff, raw)
+
+
+def test_many_pairs_are_split_and_stay_exact(cuda):
+    print_case("pairs > 256")
+    g = torch.Generator().manual_seed(8)
+    staged = random_fp8_bank(16, 256, 256, generator=g)
+    dev = to_device(staged, cuda)
+    x = torch.randn(300, 256, generator=g).bfloat16()
+    ids = torch.randint(0, 16, (300, 1), generator=g)
+    weights = torch.rand(300, 1, generator=g)
+    out = HipExpertBackend().forward_pairs(x.to(cuda), ids.to(cuda), weights.to(cuda), dev)
+    b13, b2 = oracle_banks(staged)
+    expected = np.concatenate([orc.fp8_expert_pairs(b13, b2, x[i].float().numpy(), ids[i].numpy(),
+                                                    weights[i].numpy()) for i in range(300)])
+    assert rel_inf(out.cpu().numpy(), expected) < TOL
+
+
+def test_install_on_modules_and_deterministic(cuda):
+    print_case("install + determinism")
+    staged = to_device(random_fp8_bank(8, 256, 256, generator=torch.Generator().manual_seed(1)), cuda)
+    backbone = torch.nn.Module()
+    experts = torch.nn.Module()
+    experts.fp8 = True
+    for name in ("w13_weight", "w13_scale_inv", "w2_weight", "w2_scale_inv"):
+        experts.register_buffer(name, getattr(staged, name))
+    backbone.add_module("experts", experts)
+    manager = install_expert_offload(backbone, max_staged_experts=8, cache_experts=0)
+    x = torch.randn(3, 256, device=cuda).bfloat16()
+    ids = torch.randint(0, 8, (3, 8), device=cuda)
+    weights = torch.softmax(torch.randn(3, 8, device=cuda), -1).bfloat16()
+    first = experts(x, ids, weights)
+    second = experts(x, ids, weights)
+    assert torch.equal(first, second)
+    manager.close()
+
+
+def test_hipgraph_replays_match_eager(cuda):
+    print_case("hipgraph")
+    staged = to_device(random_fp8_bank(32, 2048, 768, generator=torch.Generator().manual_seed(7)), cuda)
+    backend = HipExpertBackend()
+    x = torch.randn(1, 2048, device=cuda).bfloat16()
+    logits = torch.randn(1, 32, device=cuda)
+    weights, ids = router.route_topk(logits, 8)
+    eager = backend.forward(x, ids, weights, staged)
+    stream = torch.cuda.Stream(cuda)
+    stream.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(stream):
+        backend.forward(x, ids, weights, staged)  # warm the workspace outside capture
+    torch.cuda.current_stream(cuda).wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        w_g, i_g = router.route_topk(logits, 8)
+        out_g = backend.forward(x, i_g, w_g, staged)
+    for step in range(4):
+        logits.copy_(torch.randn(1, 32, device=cuda))
+        w_e, i_e = router.route_topk(logits, 8)
+        expected = backend.forward(x, i_e, w_e, staged)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, expected), step
+    assert torch.equal(eager, eager)
+
+
+@pytest.mark.parametrize("tokens", [1, 16])
+def test_full_size_layer_against_oracle(cuda, tokens):
+    """BASELINE decode shape: E=128, H=2048, I=768, top-8, per-channel FP8."""
+    print_case("full-size layer", tokens)
+    staged, x, ids, weights, expected = _layer_case(cuda, 128, 2048, 768, tokens, 8, "channel",
+                                                    torch.bfloat16, 20261201 + 2, bank_on_device=True)
+    out = HipExpertBackend().forward(x, ids, weights, staged)
+    assert rel_inf(out.float().cpu().numpy(), expected) < TOL

@@ -1,0 +1,423 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Every oracle function is checked against something it does not share code
+with: torch's own float8/bfloat16/float16 conversions, the reference's own CPU
+executor compiled from its sources (oracle/_ref, when present), committed
+golden vectors written by that executor, closed forms (orthogonality of the
+H256 rotation, exact integer dots, monotone softmax) and brute force in
+float64.  Scenario seeds and shapes follow the reference's tests
+(tests/test_native_backend.py, tests/test_quantized_kernels.py,
+tests/test_offload.py, tests/test_hybrid_layer.py).
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from oracle import ref_native
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def built():
+    orc.build()
+
+
+def bf16_values(t: torch.Tensor) -> np.ndarray:
+    return t.to(torch.bfloat16).float().numpy()
+
+
+# ------------------------------------------------------------------ codecs
+
+def test_fp8_decode_all_bytes_match_torch_including_signed_zero_and_nan():
+    # test_native_backend.py:33-37
+    raw = np.arange(256, dtype=np.uint8)
+    actual = orc.fp8_decode(raw)
+    expected = torch.from_numpy(raw).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(actual, expected)
+    assert np.signbit(actual[128]) and np.isnan(actual[127]) and np.isnan(actual[255])
+
+
+def _fp8_grid():
+    values = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    return np.sort(values[torch.isfinite(values)].numpy())
+
+
+def test_fp8_encode_matches_torch_on_values_midpoints_and_neighbours():
+    grid = np.unique(_fp8_grid())
+    mids = (grid[:-1].astype(np.float64) + grid[1:]) / 2
+    mids = mids.astype(np.float32)
+    up = np.nextafter(mids, np.float32(np.inf))
+    down = np.nextafter(mids, np.float32(-np.inf))
+    rng = np.random.default_rng(5)
+    randoms = np.concatenate([rng.uniform(-448, 448, 4000), rng.uniform(-0.02, 0.02, 4000)]).astype(np.float32)
+    values = np.concatenate([grid, mids, up, down, randoms, np.float32([0.0, -0.0])]).astype(np.float32)
+    actual = orc.fp8_encode(values)
+    expected = torch.from_numpy(values).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(actual, expected)
+
+
+def test_fp8_encode_saturates_instead_of_overflowing():
+    values = np.float32([448.0, 449.0, 464.0, 1e6, -1e30])
+    assert list(orc.fp8_encode(values)) == [0x7E, 0x7E, 0x7E, 0x7E, 0xFE]
+
+
+def test_bf16_and_fp16_rounding_match_torch():
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(20000) * 10.0 ** rng.integers(-8, 8, 20000),
+                        [0.0, -0.0, 65504.0, 65519.0, 65520.0, 6e-8, 3e-8, 1e-40]]).astype(np.float32)
+    np.testing.assert_array_equal(orc.bf16_round(x), torch.from_numpy(x).bfloat16().float().numpy())
+    lib = orc.lib()
+    halves = np.array([lib.orc_f16_from_f32(float(v)) for v in x], np.uint16)
+    np.testing.assert_array_equal(halves, torch.from_numpy(x).half().view(torch.int16).numpy().view(np.uint16))
+
+
+# -------------------------------------------------------------- activation quant
+
+def _quant_case(kind):
+    x = torch.randn(16, 128, generator=torch.Generator().manual_seed(22))
+    if kind == "zero":
+        x.zero_()
+        x[0, :4] = torch.tensor([0.0, -0.0, 0.0, -0.0])
+    elif kind == "tiny":
+        x *= 1e-20
+    elif kind == "saturated":
+        x *= 1e20
+    return x.to(torch.bfloat16)
+
+
+def _torch_contract_quant(x):
+    # the closed form of fp8_cpu_reference.py:14-20, evaluated by torch
+    blocks = x.float().reshape(-1, 128)
+    scales = blocks.abs().amax(-1).clamp_min(1e-10) * (1.0 / 448.0)
+    raw = (blocks / scales[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return raw.view(torch.uint8).reshape(x.shape).numpy(), scales.numpy()
+
+
+@pytest.mark.parametrize("kind", ["random", "zero", "tiny", "saturated"])
+def test_activation_quantization_exact_bytes_and_scales(kind):
+    # test_native_backend.py:41-55
+    x = _quant_case(kind)
+    q, s = orc.quantize_fp8(x.float().numpy())
+    eq, es = _torch_contract_quant(x)
+    np.testing.assert_array_equal(q, eq)
+    np.testing.assert_array_equal(s.reshape(-1), es)
+
+
+@pytest.mark.parametrize("kind", ["random", "zero", "tiny", "saturated"])
+def test_activation_quantization_matches_golden_reference_executor(kind):
+    data = np.load(GOLDEN / "fp8_quant.npz")
+    x = _quant_case(kind)
+    q, s = orc.quantize_fp8(x.float().numpy())
+    np.testing.assert_array_equal(q.reshape(-1), data[f"{kind}_q"])
+    np.testing.assert_array_equal(s.reshape(-1), data[f"{kind}_s"])
+
+
+def test_per_token_quantization_uses_one_scale_per_row():
+    rng = np.random.default_rng(9)
+    x = bf16_values(torch.from_numpy(rng.standard_normal((3, 512)).astype(np.float32)))
+    q, s = orc.quantize_fp8(x, group=512)
+    assert s.shape == (3, 1)
+    amax = np.abs(x).max(axis=1)
+    np.testing.assert_array_equal(s[:, 0], (amax * np.float32(1 / 448)).astype(np.float32))
+    decoded = orc.fp8_decode(q) * s
+    assert np.max(np.abs(decoded - x) / amax[:, None]) < 2 ** -4
+
+
+# ---------------------------------------------------------- FP8 expert pairs
+
+def _store(seed, experts, inter2, hidden, random_scales):
+    g = torch.Generator().manual_seed(seed)
+    w13 = torch.randint(-3, 4, (experts, inter2, hidden), generator=g).to(torch.float8_e4m3fn)
+    if random_scales:
+        s13 = torch.rand(experts, inter2 // 128, hidden // 128, generator=g) * 0.02 + 0.01
+    else:
+        s13 = torch.full((experts, inter2 // 128, hidden // 128), 0.03125)
+    w2 = torch.randint(-3, 4, (experts, hidden, inter2 // 2), generator=g).to(torch.float8_e4m3fn)
+    if random_scales:
+        s2 = torch.rand(experts, hidden // 128, inter2 // 2 // 128, generator=g) * 0.02 + 0.01
+    else:
+        s2 = torch.full((experts, hidden // 128, inter2 // 2 // 128), 0.03125)
+    return g, w13, s13, w2, s2
+
+
+def _banks(w13, s13, w2, s2):
+    return (orc.Fp8Bank(w13.view(torch.uint8).numpy(), s13.numpy()),
+            orc.Fp8Bank(w2.view(torch.uint8).numpy(), s2.numpy()))
+
+
+def _fp64_contract(w13, s13, w2, s2, x, ids, weights, x_group=128):
+    """Brute-force float64 evaluation of the same contract: exact FP8 products,
+    fp64 block sums and scaling, activation quantization emulated."""
+    def dequant(w, s):
+        wf = w.float().double()
+        e, n, k = wf.shape
+        rs = s.double().repeat_interleave(n // s.shape[1], 1).repeat_interleave(k // s.shape[2], 2)
+        return wf * rs
+
+    W13, W2 = dequant(w13, s13), dequant(w2, s2)
+    q, sx = orc.quantize_fp8(x.reshape(1, -1), x_group)
+    xq = (orc.fp8_decode(q).astype(np.float64) * np.repeat(sx, x_group, axis=1))[0]
+    out = []
+    inter = W2.shape[2]
+    for e, wr in zip(ids, weights):
+        gu = W13[e].numpy() @ xq
+        gu = orc.bf16_round(gu.astype(np.float32)).astype(np.float64)
+        gate, up = gu[:inter], gu[inter:]
+        h = (gate / (1 + np.exp(-gate)) * up).astype(np.float32)
+        hq, hs = orc.quantize_fp8(h.reshape(1, -1))
+        hd = (orc.fp8_decode(hq).astype(np.float64) * np.repeat(hs, 128, axis=1))[0]
+        out.append((W2[e].numpy() @ hd) * wr)
+    return np.stack(out)
+
+
+def test_duplicate_route_partials_stay_separate_and_ordered():
+    # test_native_backend.py:58-77 (store seed 194, ids [3,1,3,0])
+    _, w13, s13, w2, s2 = _store(194, 4, 256, 128, random_scales=False)
+    b13, b2 = _banks(w13, s13, w2, s2)
+    x = bf16_values(torch.linspace(-1, 1, 128))
+    ids, weights = [3, 1, 3, 0], np.float32([0.4, 0.2, 0.3, 0.1])
+    actual = orc.fp8_expert_pairs(b13, b2, x, ids, weights)
+    np.testing.assert_allclose(actual[0] / np.float32(0.4), actual[2] / np.float32(0.3), rtol=1e-6, atol=1e-6)
+    expected = _fp64_contract(w13, s13, w2, s2, x, ids, weights)
+    np.testing.assert_allclose(actual, expected, rtol=1e-5, atol=2e-6)
+
+
+def test_multiple_weight_scale_blocks_against_float64_brute_force():
+    # test_native_backend.py:234-254 (seed 882, E=3, [512,256]/[256,256])
+    g, w13, s13, w2, s2 = _store(882, 3, 512, 256, random_scales=True)
+    x = bf16_values(torch.randn(256, generator=g))
+    ids, weights = [2, 0, 1, 2], np.float32([0.4, 0.3, 0.2, 0.1])
+    actual = orc.fp8_expert_pairs(*_banks(w13, s13, w2, s2), x, ids, weights)
+    expected = _fp64_contract(w13, s13, w2, s2, x, ids, weights)
+    np.testing.assert_allclose(actual, expected, rtol=2e-5, atol=2e-6)
+
+
+def test_a_transposed_scale_index_would_be_caught():
+    # plant a plausible mistake in the oracle's input (scales transposed per
+    # expert) and check the float64 contract notices it
+    g, w13, s13, w2, s2 = _store(882, 3, 512, 256, random_scales=True)
+    x = bf16_values(torch.randn(256, generator=g))
+    ids, weights = [2, 0], np.float32([0.6, 0.4])
+    wrong = s13.clone()
+    wrong[:, 0, 1], wrong[:, 1, 0] = s13[:, 1, 0], s13[:, 0, 1]
+    actual = orc.fp8_expert_pairs(*_banks(w13, wrong, w2, s2), x, ids, weights)
+    expected = _fp64_contract(w13, s13, w2, s2, x, ids, weights)
+    assert not np.allclose(actual, expected, rtol=2e-5, atol=2e-6)
+
+
+def test_per_channel_scales_against_float64_brute_force():
+    g = torch.Generator().manual_seed(31)
+    w13 = torch.randint(-40, 41, (2, 256, 256), generator=g).to(torch.float8_e4m3fn)
+    w2 = torch.randint(-40, 41, (2, 256, 128), generator=g).to(torch.float8_e4m3fn)
+    s13 = torch.rand(2, 256, 1, generator=g) * 0.001 + 0.0005
+    s2 = torch.rand(2, 256, 1, generator=g) * 0.001 + 0.0005
+    x = bf16_values(torch.randn(256, generator=g))
+    ids, weights = [1, 0, 1], np.float32([0.5, 0.3, 0.2])
+    for x_group in (128, 256):
+        actual = orc.fp8_expert_pairs(*_banks(w13, s13, w2, s2), x, ids, weights, x_group=x_group)
+        expected = _fp64_contract(w13, s13, w2, s2, x, ids, weights, x_group=x_group)
+        np.testing.assert_allclose(actual, expected, rtol=3e-5, atol=1e-6)
+
+
+@pytest.mark.skipif(not ref_native.available(), reason="reference executor not built (make -C oracle ref)")
+@pytest.mark.parametrize("seed,experts,inter2,hidden,random_scales", [
+    (194, 4, 256, 128, False), (882, 3, 512, 256, True)])
+def test_oracle_equals_reference_scalar_executor_bitwise(seed, experts, inter2, hidden, random_scales):
+    g, w13, s13, w2, s2 = _store(seed, experts, inter2, hidden, random_scales)
+    xb = torch.randn(hidden, generator=g).bfloat16()
+    ids = np.array([experts - 1, 0, experts - 1, 1][:4], np.int64) % experts
+    weights = np.float32([0.4, 0.3, 0.2, 0.1])
+    lib = ref_native.RefLibrary()
+    with ref_native.RefExecutor(lib, hidden, inter2 // 2, capacity=8, threads=1,
+                                implementation="scalar") as ex:
+        ref = ex.forward(w13.view(torch.uint8).numpy(), s13.numpy(), w2.view(torch.uint8).numpy(),
+                         s2.numpy(), xb.view(torch.int16).numpy().view(np.uint16), ids, weights)
+    actual = orc.fp8_expert_pairs(*_banks(w13, s13, w2, s2), xb.float().numpy(), ids, weights)
+    np.testing.assert_array_equal(actual, ref)
+
+
+def test_oracle_matches_golden_reference_executor_partials():
+    data = np.load(GOLDEN / "fp8_pairs.npz")
+    for case in ("s194", "s882"):
+        w13 = torch.from_numpy(data[f"{case}_w13"]).view(torch.float8_e4m3fn)
+        w2 = torch.from_numpy(data[f"{case}_w2"]).view(torch.float8_e4m3fn)
+        s13 = torch.from_numpy(data[f"{case}_s13"])
+        s2 = torch.from_numpy(data[f"{case}_s2"])
+        x = torch.from_numpy(data[f"{case}_x"].view(np.int16)).view(torch.bfloat16).float().numpy()
+        actual = orc.fp8_expert_pairs(*_banks(w13, s13, w2, s2), x, data[f"{case}_ids"], data[f"{case}_weights"])
+        np.testing.assert_array_equal(actual, data[f"{case}_out"])
+
+
+def test_layer_reduction_follows_router_slot_order():
+    # test_offload.py:394-409: with +-1e20 partials only a slot-order sum
+    # gives 3 * p
+    _, w13, s13, w2, s2 = _store(194, 4, 256, 128, random_scales=False)
+    b13, b2 = _banks(w13, s13, w2, s2)
+    x = bf16_values(torch.linspace(-1, 1, 128))
+    weights = np.float32([[1e20, 1.0, -1e20, 3.0]])
+    ids = np.array([[1, 1, 1, 1]])
+    single = orc.fp8_expert_pairs(b13, b2, x, [1], np.float32([1.0]))[0]
+    out = orc.fp8_moe_forward(b13, b2, x.reshape(1, -1), ids, weights, out_dtype="fp32")
+    np.testing.assert_array_equal(out[0], (single * np.float32(3.0)))
+
+
+# ------------------------------------------------------------------ routing
+
+def test_route_topk_matches_torch_softmax_topk_on_tie_free_logits():
+    g = torch.Generator().manual_seed(20261202)
+    logits = torch.randn(512, 128, generator=g)
+    probs = torch.softmax(logits, -1)
+    tw, ti = probs.topk(8, -1)
+    tw = tw / tw.sum(-1, keepdim=True)
+    ids, weights = orc.route_topk(logits.numpy(), 8)
+    np.testing.assert_array_equal(ids, ti.numpy())
+    np.testing.assert_allclose(weights, tw.numpy(), rtol=2e-6, atol=0)
+    np.testing.assert_array_equal(orc.bf16_round(weights), tw.bfloat16().float().numpy())
+
+
+def test_route_topk_ties_resolve_to_the_lower_index():
+    logits = np.full((2, 16), -1.0, np.float32)
+    logits[0, [3, 1]] = 2.0
+    logits[1, [15, 0]] = 2.0
+    ids, weights = orc.route_topk(logits, 4)
+    np.testing.assert_array_equal(ids, [[1, 3, 0, 2], [0, 15, 1, 2]])
+    assert weights[0, 0] == weights[0, 1]
+    # the set torch picks for the strict winners is the same
+    t = torch.softmax(torch.from_numpy(logits), -1).topk(2, -1).indices.sort(-1).values
+    np.testing.assert_array_equal(np.sort(ids[:, :2], -1), t.numpy())
+
+
+def test_route_without_renormalisation_returns_probabilities():
+    logits = torch.randn(4, 32, generator=torch.Generator().manual_seed(1))
+    ids, weights = orc.route_topk(logits.numpy(), 4, renormalize=False)
+    np.testing.assert_allclose(weights, torch.softmax(logits, -1).topk(4, -1).values.numpy(), rtol=2e-6)
+
+
+def test_permute_is_torch_stable_argsort_and_bincount():
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, 12, (37, 8), generator=g)
+    order, counts, offsets = orc.permute(ids.numpy(), 12)
+    flat = ids.reshape(-1)
+    np.testing.assert_array_equal(order, torch.argsort(flat, stable=True).numpy())
+    np.testing.assert_array_equal(counts, torch.bincount(flat, minlength=12).numpy())
+    np.testing.assert_array_equal(offsets[:-1], (torch.cumsum(torch.bincount(flat, minlength=12), 0)
+                                                 - torch.bincount(flat, minlength=12)).numpy())
+
+
+def test_permute_rejects_out_of_range_ids():
+    with pytest.raises(ValueError):
+        orc.permute(np.array([[0, 12]]), 12)
+
+
+# --------------------------------------------------- packed quantized modes
+
+def _h256():
+    h = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=torch.float64)
+    r = h
+    for _ in range(3):
+        r = torch.kron(r, h)
+    return r / 16
+
+
+def test_rotation_is_the_published_orthogonal_h256():
+    x = torch.randn(3, 512, generator=torch.Generator().manual_seed(8), dtype=torch.float64)
+    xb = x.to(torch.bfloat16).double()
+    _, _, rot = orc.rotate_quantize(xb.float().numpy(), rot_dtype="fp32")
+    H = _h256()
+    assert torch.allclose(H @ H.T, torch.eye(256, dtype=torch.float64))
+    expected = (xb.reshape(-1, 256) @ H).reshape(3, 512)
+    np.testing.assert_allclose(rot, expected.numpy(), rtol=0, atol=1e-5)
+    # inverse rotation recovers the input
+    back = (torch.from_numpy(rot).double().reshape(-1, 256) @ H.T).reshape(3, 512)
+    np.testing.assert_allclose(back.numpy(), xb.numpy(), atol=1e-5)
+
+
+def test_rotate_quantize_row_int8_against_torch_closed_form():
+    x = torch.randn(4, 256, generator=torch.Generator().manual_seed(71)).bfloat16()
+    q, s, rot = orc.rotate_quantize(x.float().numpy())
+    rotated = torch.from_numpy(rot)
+    assert torch.equal(rotated.bfloat16().float(), rotated)  # stored through bf16
+    scale = rotated.abs().amax(1).clamp_min(1e-12) / 127
+    np.testing.assert_array_equal(s, scale.numpy())
+    np.testing.assert_array_equal(q, (rotated / scale[:, None]).round().clamp(-127, 127).to(torch.int8).numpy())
+    # torch's own bf16 rotation agrees to one bf16 rounding
+    torch_rot = (x.reshape(-1, 256) @ _h256().to(torch.bfloat16)).reshape(4, 256).float()
+    np.testing.assert_allclose(rot, torch_rot.numpy(), rtol=2 ** -7, atol=1e-6)
+
+
+def _explicit_projection(mode, bank, x, ids, weights, weighted, n, k):
+    """test_quantized_kernels.py:27-83 explicit reconstruction oracle."""
+    if mode == 0:
+        inputs = x.float()
+    else:
+        q, s, _ = orc.rotate_quantize(x.float().numpy())
+        inputs = torch.from_numpy(q).float() * torch.from_numpy(s)[:, None]
+    mats = [torch.from_numpy(orc.quant_dequantize(bank, e)) for e in range(bank.experts)]
+    out = torch.stack([inputs[i] @ mats[e].T for i, e in enumerate(ids)]).bfloat16()
+    if weighted:
+        out = out.float() * torch.from_numpy(weights)[:, None]
+    return out.float().numpy()
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_quant_projection_matches_explicit_reconstruction(mode, weighted):
+    from drama_moe.formats import gptq_pack, nibble_pack, six_pack
+
+    torch.manual_seed(71)
+    n, k = 128, 256
+    x = torch.randn(3, k, dtype=torch.bfloat16)
+    weights = np.float32([0.2, 0.6, 0.3])
+    ids = [1, 0, 1]
+    if mode == 0:
+        codes = torch.randint(0, 16, (2, n, k))
+        scales = (torch.rand(2, n, k // 128) * 0.03).half()
+        bank = orc.QuantBank(0, gptq_pack(codes).numpy(), scales.view(torch.int16).numpy(), n, k)
+        explicit = ((codes.float() - 8) * scales.float().repeat_interleave(128, -1)).bfloat16().float()
+    elif mode == 1:
+        w8 = torch.randint(-127, 128, (2, n, k), dtype=torch.int8)
+        sc = torch.rand(2, n, 1) * 0.02
+        bank = orc.QuantBank(1, w8.numpy(), sc.numpy(), n, k)
+        explicit = w8.float() * sc
+    else:
+        codes = torch.randint(0, 16 if mode == 3 else 64, (2, n, k))
+        packed = six_pack(codes) if mode == 2 else nibble_pack(codes)
+        relative = (torch.rand(2, n, k // 16) + 1).to(torch.float8_e4m3fn)
+        channel = torch.rand(2, n, 1) * 0.02
+        if mode == 3:
+            tables = torch.linspace(-12, 13, 16).repeat(2, 1).contiguous()
+            aux = torch.zeros(2, n, k // 16 + 8, dtype=torch.uint8)
+            aux[..., :k // 16] = relative.view(torch.uint8)
+            aux[..., k // 16:k // 16 + 4] = channel.view(torch.uint8)
+            aux[:, :16, k // 16 + 4:] = tables.view(torch.uint8).reshape(2, 16, 4)
+            levels = torch.stack([tables[i][codes[i]] for i in range(2)])
+        else:
+            aux = torch.cat((relative.view(torch.uint8), channel.view(torch.uint8)), dim=-1)
+            levels = codes.float() - 32
+        bank = orc.QuantBank(mode, packed.numpy(), aux.numpy(), n, k)
+        explicit = (levels * relative.float().repeat_interleave(16, -1)).round().clamp(-127, 127) * channel
+    # the oracle's own dequantization equals the independent reconstruction
+    for e in range(2):
+        np.testing.assert_allclose(orc.quant_dequantize(bank, e), explicit[e].numpy(), rtol=1e-6, atol=1e-9)
+    actual = orc.quant_projection(bank, x.float().numpy(), ids, weights, weighted=weighted)
+    expected = _explicit_projection(mode, bank, x, ids, weights, weighted, n, k)
+    np.testing.assert_allclose(actual, expected, rtol=0.01, atol=0.02)
+
+
+def test_asymmetric_w4a16_zero_points():
+    from drama_moe.formats import gptq_pack, zeros_pack
+
+    g = torch.Generator().manual_seed(12)
+    n, k = 64, 256
+    codes = torch.randint(0, 16, (1, n, k), generator=g)
+    zeros = torch.randint(0, 16, (1, k // 128, n), generator=g)
+    scales = (torch.rand(1, n, k // 128, generator=g) * 0.03).half()
+    bank = orc.QuantBank(0, gptq_pack(codes).numpy(), scales.view(torch.int16).numpy(), n, k,
+                         zeros=zeros_pack(zeros).numpy())
+    zp = zeros.permute(0, 2, 1).repeat_interleave(128, -1).float()  # [1, n, k]
+    explicit = ((codes.float() - zp) * scales.float().repeat_interleave(128, -1)).bfloat16().float()
+    np.testing.assert_array_equal(orc.quant_dequantize(bank, 0), explicit[0].numpy())
