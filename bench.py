@@ -85,8 +85,7 @@ def run_gpu(steps: int, warmup: int):
     outs = torch.empty(LAYERS, 1, HIDDEN, device=device, dtype=torch.bfloat16)
 
     def step(i):
-        weights, ids = router.route_topk(logits[i], TOP_K)
-        outs[i].copy_(backend.forward(xs[i], ids, weights, banks[i]))
+        backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
 
     # warm up the workspace and descriptor caches outside capture
     with torch.cuda.stream(stream):
@@ -138,19 +137,33 @@ def run_gpu(steps: int, warmup: int):
     state = device_state(device)
     ids_dev = ids_all.contiguous()
     w_dev = torch.full((LAYERS, TOP_K), 1.0 / TOP_K, device=device)
-    gu_bytes = [u * (2 * INTER * HIDDEN + 2 * INTER * 4) + HIDDEN * 2 + TOP_K * INTER + TOP_K * (INTER // 128) * 4
-                for u in uniq]
+    # gate/up stage bytes: weights + per-channel scales of the distinct experts,
+    # the FP8 activation row + scales, the FP8 hidden + scales written
+    gu_bytes = [u * (2 * INTER * HIDDEN + 2 * INTER * 4) + HIDDEN + (HIDDEN // 128) * 4 + TOP_K * INTER
+                + TOP_K * (INTER // 128) * 4 for u in uniq]
     kstream = torch.cuda.Stream(device)
     hq = torch.empty(TOP_K, INTER, dtype=torch.uint8, device=device)
     hs = torch.empty(TOP_K, INTER // 128, device=device)
 
+    # one prepared workspace per layer (grouping + quantized x), then the
+    # gate/up stage alone: a single kernel launch per layer
+    workspaces = []
+    for i in range(LAYERS):
+        bank = fp8_bank_struct(banks[i])
+        nbytes = lib.dmoe_fp8_workspace_bytes(bank, TOP_K)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _lib.check(lib.dmoe_fp8_prepare(
+            bank, _lib.ptr(xs[i]), _lib.BF16, HIDDEN, 1, TOP_K, _lib.ptr(ids_dev[i]), _lib.I64, TOP_K, 128,
+            _lib.ptr(ws), nbytes, _lib.ptr(state.status), _lib.stream_handle(device)))
+        workspaces.append(ws)
+    torch.cuda.synchronize()
+
     def gateup_only(i):
         bank = fp8_bank_struct(banks[i])
-        ws = state.workspace_for(lib.dmoe_fp8_workspace_bytes(bank, TOP_K))
+        ws = workspaces[i]
         _lib.check(lib.dmoe_fp8_gate_up(
-            bank, _lib.ptr(xs[i]), _lib.BF16, HIDDEN, 1, TOP_K, _lib.ptr(ids_dev[i]), _lib.I64, TOP_K,
-            128, _lib.BF16, _lib.ptr(hq), _lib.ptr(hs), _lib.ptr(ws), ws.numel(), _lib.ptr(state.status),
-            _lib.stream_handle(device)))
+            bank, TOP_K, TOP_K, 128, _lib.BF16, _lib.ptr(hq), _lib.ptr(hs), _lib.ptr(ws), ws.numel(),
+            _lib.ptr(state.status), _lib.stream_handle(device)))
 
     kgraph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(kstream):

@@ -93,33 +93,42 @@ BankGeom check_bank(const DmoeFp8Bank* bank) {
 }
 
 struct Fp8Workspace {
+    int* counters;
+    dmoe::Grouping* grouping;
+    uint8_t* xq;
+    float* xs;
     float* h32;
     uint8_t* hq;
     float* hs;
-    int* counters;
 };
 
 // Workspace: the arrival counters come first at a fixed size, so one
 // zero-filled workspace serves calls of any pair count and bank geometry;
-// the per-pair regions follow.
+// the grouping and the per-call buffers follow.
 constexpr size_t kCounterBytes = (size_t)dmoe::kMaxDecodePairs * (dmoe::kMaxInter / 128) * 4;
 
-size_t fp8_workspace_layout(int pairs, int I, char* base, Fp8Workspace* ws) {
+size_t fp8_workspace_layout(int pairs, int H, int I, char* base, Fp8Workspace* ws) {
     size_t off = 0;
     auto take = [&](size_t n) {
-        size_t o = off;
+        const size_t o = off;
         off = align256(off + n);
         return base ? base + o : nullptr;
     };
     char* counters = take(kCounterBytes);
+    char* grouping = take(sizeof(dmoe::Grouping));
+    char* xq = take((size_t)pairs * H);
+    char* xs = take((size_t)pairs * (H / 128) * 4);
     char* h32 = take((size_t)pairs * I * 4);
     char* hq = take((size_t)pairs * I);
     char* hs = take((size_t)pairs * (I / 128) * 4);
     if (ws) {
+        ws->counters = reinterpret_cast<int*>(counters);
+        ws->grouping = reinterpret_cast<dmoe::Grouping*>(grouping);
+        ws->xq = reinterpret_cast<uint8_t*>(xq);
+        ws->xs = reinterpret_cast<float*>(xs);
         ws->h32 = reinterpret_cast<float*>(h32);
         ws->hq = reinterpret_cast<uint8_t*>(hq);
         ws->hs = reinterpret_cast<float*>(hs);
-        ws->counters = reinterpret_cast<int*>(counters);
     }
     return off;
 }
@@ -148,32 +157,61 @@ void check_activations(const BankGeom& g, const Activations& a, int pairs) {
         require(a.xs_row_stride >= g.H / a.x_group, "activation scale row stride too small");
     } else {
         require(a.x != nullptr && is_float_dtype(a.x_dtype), "activations must be fp32, bf16 or fp16");
-        require(a.x_row_stride >= g.H, "activation row stride smaller than the hidden size");
+        const int esize = a.x_dtype == DMOE_F32 ? 4 : 2;
+        require(a.x_row_stride >= g.H && (a.x_row_stride * esize) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(a.x) % 16 == 0,
+                "activation rows must be contiguous and 16-byte aligned");
     }
 }
 
-// Stage 1: gate/up projection, SiLU(gate) * up, FP8 128-group quantization of
-// the hidden activation into hq [pairs, I] / hs [pairs, I/128].
-void launch_gate_up(const BankGeom& g, const Activations& a, const void* ids, int ids_dtype, int pairs,
-                    int gu_dtype, uint8_t* hq, float* hs, const Fp8Workspace& ws, int* status,
-                    hipStream_t stream) {
+// Small decode calls quantize the hidden activation inside the down kernel.
+bool down_quantizes(const BankGeom& g, int pairs) {
+    return pairs <= dmoe::kDownQuantPairs && (int64_t)pairs * g.I <= dmoe::kDownQuantBytes;
+}
+
+dmoe::RouteSource ids_source(const void* ids, int ids_dtype) {
+    return dmoe::RouteSource{ids, ids_dtype, nullptr, 0, 0, 0, nullptr, nullptr, 0};
+}
+
+// Prep: grouping from ids or logits, and (raw activations) FP8 quantization of
+// the rows the pairs read into the workspace.  Returns where the FP8 rows live.
+void launch_prep(const BankGeom& g, Activations& a, const dmoe::RouteSource& route, int pairs,
+                 const Fp8Workspace& ws, int* status, hipStream_t stream) {
+    dmoe::PrepArgs pa{};
+    pa.route = route;
+    pa.pairs = pairs;
+    pa.experts = g.experts;
+    pa.grouping = ws.grouping;
+    pa.status = status;
+    if (a.xq == nullptr) {
+        const int rows = (pairs - 1) / a.row_div + 1;
+        pa.quant = dmoe::QuantArgs{a.x, a.x_dtype, a.x_row_stride, rows, g.H, a.x_group, 0, ws.xq, ws.xs, status};
+        a.xq = ws.xq;
+        a.xs = ws.xs;
+        a.xq_row_stride = g.H;
+        a.xs_row_stride = g.H / a.x_group;
+    }
+    dmoe::launch_moe_prep(pa, stream);
+}
+
+// Stage 1: gate/up projection and SiLU(gate) * up; with quantize_hidden the
+// FP8 128-group quantization of the hidden activation into hq / hs.
+void launch_gate_up(const BankGeom& g, const Activations& a, int pairs, int gu_dtype, uint8_t* hq, float* hs,
+                    const Fp8Workspace& ws, int* status, hipStream_t stream, bool quantize_hidden) {
     dmoe::GateUpArgs ga{};
     ga.w13 = g.w13;
     ga.experts = g.experts;
-    ga.x = a.x;
-    ga.x_dtype = a.x_dtype;
-    ga.x_row_stride = a.x_row_stride;
+    ga.grouping = ws.grouping;
     ga.xq = a.xq;
     ga.xs = a.xs;
     ga.xq_row_stride = a.xq_row_stride;
     ga.xs_row_stride = a.xs_row_stride;
     ga.x_group = a.x_group;
-    ga.ids = ids;
-    ga.ids_dtype = ids_dtype;
     ga.pairs = pairs;
     ga.row_div = a.row_div;
     ga.gu_dtype = gu_dtype;
     ga.h32 = ws.h32;
+    ga.quantize_hidden = quantize_hidden;
     ga.hq = hq;
     ga.hs = hs;
     ga.counters = ws.counters;
@@ -181,18 +219,19 @@ void launch_gate_up(const BankGeom& g, const Activations& a, const void* ids, in
     dmoe::launch_fp8_gateup_decode(ga, std::min(pairs, g.experts), stream);
 }
 
-// Stage 2: down projection of the FP8 hidden activation, route weight, and
-// either the slot-order layer combine (out) or ordered fp32 partials.
-void launch_down(const BankGeom& g, const uint8_t* hq, const float* hs, const void* ids, int ids_dtype,
+// Stage 2: down projection of the hidden activation, route weight, and either
+// the slot-order layer combine (out) or ordered fp32 partials.
+void launch_down(const BankGeom& g, const Fp8Workspace& ws, const uint8_t* hq, const float* hs,
                  const void* weights, int weights_dtype, int pairs, int top_k, void* out, int out_dtype,
-                 int64_t out_row_stride, float* out_pairs, int* status, hipStream_t stream) {
+                 int64_t out_row_stride, float* out_pairs, int* status, hipStream_t stream, const float* h32) {
     dmoe::DownArgs da{};
     da.w2 = g.w2;
     da.experts = g.experts;
+    da.grouping = ws.grouping;
+    da.h32 = h32;
+    da.quantize_hidden = h32 != nullptr;
     da.hq = hq;
     da.hs = hs;
-    da.ids = ids;
-    da.ids_dtype = ids_dtype;
     da.weights = weights;
     da.w_dtype = weights_dtype;
     da.pairs = pairs;
@@ -206,11 +245,11 @@ void launch_down(const BankGeom& g, const uint8_t* hq, const float* hs, const vo
 }
 
 Fp8Workspace take_workspace(const BankGeom& g, int pairs, void* workspace, size_t workspace_bytes) {
-    const size_t need = fp8_workspace_layout(pairs, g.I, nullptr, nullptr);
+    const size_t need = fp8_workspace_layout(pairs, g.H, g.I, nullptr, nullptr);
     require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
     require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
     Fp8Workspace ws{};
-    fp8_workspace_layout(pairs, g.I, static_cast<char*>(workspace), &ws);
+    fp8_workspace_layout(pairs, g.H, g.I, static_cast<char*>(workspace), &ws);
     return ws;
 }
 
@@ -224,23 +263,23 @@ void check_gu_dtype(int gu_dtype) {
     require(gu_dtype == DMOE_F32 || gu_dtype == DMOE_BF16 || gu_dtype == DMOE_F16, "bad gate/up dtype");
 }
 
-// Shared body of the three whole-path grouped FP8 entry points.
-void fp8_grouped(const BankGeom& g, const Activations& a, const void* ids, int ids_dtype,
-                 const void* weights, int weights_dtype, int pairs, int top_k, int gu_dtype,
-                 void* out, int out_dtype, int64_t out_row_stride, float* out_pairs,
-                 void* workspace, size_t workspace_bytes, int* status, hipStream_t stream) {
-    check_activations(g, a, pairs);
-    check_routes(ids, ids_dtype, weights, weights_dtype);
-    check_gu_dtype(gu_dtype);
-    if (out_pairs == nullptr) {
-        require(out != nullptr && is_float_dtype(out_dtype), "output must be fp32, bf16 or fp16");
-        require(out_row_stride >= g.H, "output row stride smaller than the hidden size");
-        require(top_k >= 1 && pairs % top_k == 0, "pairs must be tokens * top_k");
-    }
+void check_output(const BankGeom& g, void* out, int out_dtype, int64_t out_row_stride, int pairs, int top_k) {
+    require(out != nullptr && is_float_dtype(out_dtype), "output must be fp32, bf16 or fp16");
+    require(out_row_stride >= g.H, "output row stride smaller than the hidden size");
+    require(top_k >= 1 && pairs % top_k == 0, "pairs must be tokens * top_k");
+}
+
+// The three launches of a whole grouped FP8 call.
+void fp8_grouped(const BankGeom& g, Activations a, const dmoe::RouteSource& route, const void* weights,
+                 int weights_dtype, int pairs, int top_k, int gu_dtype, void* out, int out_dtype,
+                 int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes, int* status,
+                 hipStream_t stream) {
     const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
-    launch_gate_up(g, a, ids, ids_dtype, pairs, gu_dtype, ws.hq, ws.hs, ws, status, stream);
-    launch_down(g, ws.hq, ws.hs, ids, ids_dtype, weights, weights_dtype, pairs, top_k, out, out_dtype,
-                out_row_stride, out_pairs, status, stream);
+    const bool in_down = down_quantizes(g, pairs);
+    launch_prep(g, a, route, pairs, ws, status, stream);
+    launch_gate_up(g, a, pairs, gu_dtype, ws.hq, ws.hs, ws, status, stream, !in_down);
+    launch_down(g, ws, ws.hq, ws.hs, weights, weights_dtype, pairs, top_k, out, out_dtype, out_row_stride,
+                out_pairs, status, stream, in_down ? ws.h32 : nullptr);
 }
 
 }  // namespace
@@ -315,7 +354,7 @@ int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t
 
 size_t dmoe_fp8_workspace_bytes(const DmoeFp8Bank* bank, int pairs) {
     if (!bank || pairs < 1) return 0;
-    return fp8_workspace_layout(pairs, bank->w13.n / 2, nullptr, nullptr);
+    return fp8_workspace_layout(pairs, bank->w13.k, bank->w13.n / 2, nullptr, nullptr);
 }
 
 int dmoe_fp8_moe_forward(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride,
@@ -326,8 +365,13 @@ int dmoe_fp8_moe_forward(const DmoeFp8Bank* bank, const void* x, int x_dtype, in
     return checked([&] {
         const BankGeom g = check_bank(bank);
         require(tokens >= 1 && top_k >= 1 && top_k <= g.experts, "bad token count or top_k");
+        const int pairs = tokens * top_k;
         const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, x_group};
-        fp8_grouped(g, a, ids, ids_dtype, weights, weights_dtype, tokens * top_k, top_k, gu_dtype, out,
+        check_activations(g, a, pairs);
+        check_routes(ids, ids_dtype, weights, weights_dtype);
+        check_gu_dtype(gu_dtype);
+        check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
+        fp8_grouped(g, a, ids_source(ids, ids_dtype), weights, weights_dtype, pairs, top_k, gu_dtype, out,
                     out_dtype, out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
@@ -340,8 +384,11 @@ int dmoe_fp8_moe_pairs(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
         const BankGeom g = check_bank(bank);
         require(out != nullptr, "output partials are required");
         const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, rows, row_div, x_group};
-        fp8_grouped(g, a, ids, ids_dtype, weights, weights_dtype, pairs, 1, gu_dtype, nullptr, DMOE_F32, 0,
-                    out, workspace, workspace_bytes, status, as_stream(stream));
+        check_activations(g, a, pairs);
+        check_routes(ids, ids_dtype, weights, weights_dtype);
+        check_gu_dtype(gu_dtype);
+        fp8_grouped(g, a, ids_source(ids, ids_dtype), weights, weights_dtype, pairs, 1, gu_dtype, nullptr,
+                    DMOE_F32, 0, out, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
 
@@ -355,47 +402,81 @@ int dmoe_fp8_quantized_pairs(const DmoeFp8Bank* bank, const uint8_t* xq, const f
         require(xq != nullptr, "quantized activations are required");
         require(out != nullptr, "output partials are required");
         const Activations a{nullptr, DMOE_F32, 0, xq, xs, xq_row_stride, xs_row_stride, rows, row_div, x_group};
-        fp8_grouped(g, a, ids, ids_dtype, weights, weights_dtype, pairs, 1, gu_dtype, nullptr, DMOE_F32, 0,
-                    out, workspace, workspace_bytes, status, as_stream(stream));
+        check_activations(g, a, pairs);
+        check_routes(ids, ids_dtype, weights, weights_dtype);
+        check_gu_dtype(gu_dtype);
+        fp8_grouped(g, a, ids_source(ids, ids_dtype), weights, weights_dtype, pairs, 1, gu_dtype, nullptr,
+                    DMOE_F32, 0, out, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
 
-int dmoe_fp8_gate_up(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride, int rows,
-                     int row_div, const void* ids, int ids_dtype, int pairs, int x_group, int gu_dtype,
+int dmoe_fp8_prepare(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride, int rows,
+                     int row_div, const void* ids, int ids_dtype, int pairs, int x_group, void* workspace,
+                     size_t workspace_bytes, int* status, void* stream) {
+    return checked([&] {
+        const BankGeom g = check_bank(bank);
+        Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, rows, row_div, x_group};
+        check_activations(g, a, pairs);
+        require(ids != nullptr && is_id_dtype(ids_dtype), "route ids must be int32 or int64");
+        const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
+        launch_prep(g, a, ids_source(ids, ids_dtype), pairs, ws, status, as_stream(stream));
+    });
+}
+
+int dmoe_fp8_gate_up(const DmoeFp8Bank* bank, int row_div, int pairs, int x_group, int gu_dtype,
                      uint8_t* hidden_q, float* hidden_scales, void* workspace, size_t workspace_bytes,
                      int* status, void* stream) {
     return checked([&] {
         const BankGeom g = check_bank(bank);
-        const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, rows, row_div, x_group};
-        check_activations(g, a, pairs);
-        require(ids != nullptr && is_id_dtype(ids_dtype), "route ids must be int32 or int64");
+        require(pairs >= 1 && pairs <= dmoe::kMaxDecodePairs, "pair count outside [1, 256]");
+        require(row_div >= 1, "row_div must be positive");
+        require(x_group == 128 || x_group == g.H, "activation group must be 128 or the hidden size");
         check_gu_dtype(gu_dtype);
         require(hidden_q && hidden_scales, "hidden activation outputs are required");
         require(reinterpret_cast<uintptr_t>(hidden_q) % 16 == 0, "hidden FP8 rows must be 16-byte aligned");
         const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
-        launch_gate_up(g, a, ids, ids_dtype, pairs, gu_dtype, hidden_q, hidden_scales, ws, status,
-                       as_stream(stream));
+        const Activations a{nullptr, DMOE_F32, 0, ws.xq, ws.xs, g.H, g.H / x_group,
+                            (pairs - 1) / row_div + 1, row_div, x_group};
+        launch_gate_up(g, a, pairs, gu_dtype, hidden_q, hidden_scales, ws, status, as_stream(stream), true);
     });
 }
 
 int dmoe_fp8_down(const DmoeFp8Bank* bank, const uint8_t* hidden_q, const float* hidden_scales,
-                  const void* ids, int ids_dtype, const void* weights, int weights_dtype, int pairs,
-                  int top_k, void* out, int out_dtype, int64_t out_row_stride, float* out_pairs,
+                  const void* weights, int weights_dtype, int pairs, int top_k, void* out, int out_dtype,
+                  int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes,
                   int* status, void* stream) {
     return checked([&] {
         const BankGeom g = check_bank(bank);
         require(pairs >= 1 && pairs <= dmoe::kMaxDecodePairs, "pair count outside [1, 256]");
-        check_routes(ids, ids_dtype, weights, weights_dtype);
+        require(weights != nullptr && is_float_dtype(weights_dtype), "route weights must be fp32, bf16 or fp16");
         require(hidden_q && hidden_scales, "hidden activation inputs are required");
         require(reinterpret_cast<uintptr_t>(hidden_q) % 16 == 0, "hidden FP8 rows must be 16-byte aligned");
-        if (out_pairs == nullptr) {
-            require(out != nullptr && is_float_dtype(out_dtype), "output must be fp32, bf16 or fp16");
-            require(out_row_stride >= g.H, "output row stride smaller than the hidden size");
-            require(top_k >= 1 && pairs % top_k == 0, "pairs must be tokens * top_k");
-        }
-        launch_down(g, hidden_q, hidden_scales, ids, ids_dtype, weights, weights_dtype, pairs,
-                    out_pairs ? 1 : top_k, out, out_dtype, out_row_stride, out_pairs, status,
-                    as_stream(stream));
+        if (out_pairs == nullptr) check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
+        const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
+        launch_down(g, ws, hidden_q, hidden_scales, weights, weights_dtype, pairs, out_pairs ? 1 : top_k, out,
+                    out_dtype, out_row_stride, out_pairs, status, as_stream(stream), nullptr);
+    });
+}
+
+int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride,
+                       int tokens, const float* logits, int64_t logits_row_stride, int top_k,
+                       int renormalize, int64_t* ids_out, void* weights_out, int weights_dtype,
+                       int x_group, int gu_dtype, void* out, int out_dtype, int64_t out_row_stride,
+                       void* workspace, size_t workspace_bytes, int* status, void* stream) {
+    return checked([&] {
+        const BankGeom g = check_bank(bank);
+        require(tokens >= 1 && top_k >= 1 && top_k <= g.experts && top_k <= 64, "bad token count or top_k");
+        require(logits != nullptr && logits_row_stride >= g.experts, "router logits [tokens, experts] required");
+        require(ids_out && weights_out && is_float_dtype(weights_dtype), "routing outputs are required");
+        const int pairs = tokens * top_k;
+        const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, x_group};
+        check_activations(g, a, pairs);
+        check_gu_dtype(gu_dtype);
+        check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
+        const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
+                                      ids_out, weights_out, weights_dtype};
+        fp8_grouped(g, a, route, weights_out, weights_dtype, pairs, top_k, gu_dtype, out, out_dtype,
+                    out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
 

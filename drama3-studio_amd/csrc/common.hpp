@@ -104,6 +104,50 @@ __device__ __forceinline__ v4i mfma_i8(const v4i& a, const v4i& b, const v4i& c)
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
+// DPP lane permutations (no LDS round trip).  quad_perm / row mirrors stay
+// inside a 16-lane row, so every lane has a source.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16 lanes
+
+// Max over each 16-lane row; every lane of the row receives it.
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp_f32<kDppXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppMirror>(v));
+    return v;
+}
+__device__ __forceinline__ float row_sum(float v) {
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<kDppHalfMirror>(v);
+    v += dpp_f32<kDppMirror>(v);
+    return v;
+}
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+// Wave-wide max / sum: row reduction by DPP, then the four rows by readlane.
+// The result is wave-uniform; the summation order is fixed.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = row_max(v);
+    return fmaxf(fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)), fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = row_sum(v);
+    return (readlane_f32(v, 0) + readlane_f32(v, 16)) + (readlane_f32(v, 32) + readlane_f32(v, 48));
+}
+
 // Butterfly max / sum over all 64 lanes of a wave.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -120,23 +164,38 @@ __device__ __forceinline__ void raise_status(int* status, int bits) {
     if (status) __hip_atomic_fetch_or(status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Release this workgroup's global writes, count its arrival, and report to
+// Cross-workgroup hand-off without cache-wide fences.
+//
+// On this chip an agent-scope release/acquire fence writes back / invalidates
+// a whole L2 (measured at ~20 us per fence), so hand-offs between workgroups
+// publish their data with agent-scope atomic stores and read it with
+// agent-scope atomic loads -- the L2-coherent ("sc1") accesses the compiler
+// itself uses for such atomics -- and count arrivals with a relaxed atomic.
+// The store side waits for its coherent stores to complete (the barrier below
+// drains vmcnt) before the arrival is counted, and the reader issues its
+// coherent loads only after it has observed the final count.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Count this workgroup's arrival (after its coherent stores) and report to
 // every thread whether it was the last of `expected` arrivals.  The last
-// arriver also performs the matching acquire and re-arms the counter (so the
-// counter needs no clearing between launches or graph replays).
+// arriver re-arms the counter, so it needs no clearing between launches or
+// graph replays.
 __device__ __forceinline__ bool arrive_last(int* counter, int expected, int* lds_flag) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's coherent stores are complete
     __syncthreads();
     if (threadIdx.x == 0) {
-        int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        bool last = old == expected - 1;
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old == expected - 1;
         if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *lds_flag = last;
     }
     __syncthreads();
-    bool last = *lds_flag != 0;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return last;
+    return *lds_flag != 0;
 }
 
 }  // namespace dmoe

@@ -10,20 +10,25 @@
 //   h -> FP8 128-groups, down rows as above, * route weight -> fp32 partial
 //   layer output = fp32 sum of partials in router slot order -> compute dtype
 //
-// Two kernels:
-//   gateup: grid (active expert, 16-column tile of I).  The 4 waves split the
-//           128-column K blocks; each lane streams 32 contiguous weight bytes of
-//           one gate row and one up row per block into an FP8 MFMA whose A rows
-//           are the expert's routed pairs.  The last of the 8 tiles of a
-//           128-column group (counted with an agent-scope atomic) quantizes the
-//           hidden activation of that group to FP8.
-//   down:   grid (8-row tile of H).  Waves take the active experts in turn, and
-//           the workgroup sums the weighted partials of every token in router
-//           slot order before one store: no atomics on the output, no partial
-//           round trip through HBM, deterministic.
-// Both kernels derive the expert grouping from the route ids themselves
-// (LDS flags + wave ballots), so a decode step needs no host sync and no
-// extra routing launch.
+// A decode call is three launches: the prep kernel (route_quant.hip) routes or
+// validates ids, records the expert grouping and quantizes x once; then
+//   gateup: grid (active expert, 16-column tile of I), 8 waves that split the
+//           128-column K blocks.  Each lane streams 32 contiguous weight bytes
+//           of one gate row and one up row per block into an FP8 MFMA whose A
+//           rows are the expert's routed pairs (four per pass).  h is stored
+//           fp32; for larger calls the last of the 8 tiles of a 128-column
+//           group (agent-scope arrival counter, coherent hand-off) quantizes
+//           that group.
+//   down:   grid (8-row tile of H), 4 waves.  One MFMA serves two experts
+//           (B columns 0..7 / 8..15, A rows 0..7 / 8..15), every lane streams
+//           weight bytes, batches of experts are double-buffered, and the
+//           workgroup sums the weighted partials of every token in router slot
+//           order before one store: no atomics on the output, deterministic.
+//           Small calls quantize h here, overlapped with the weight stream.
+// Kernels issue all of their input loads at entry and the small ones before
+// the weight stream: loads retire in issue order.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -31,173 +36,152 @@ namespace dmoe {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
-
-// Shared routing scratch: expert flags, the ascending active list, the ids.
-struct RouteLds {
-    int flag[kMaxExperts];
-    int active[kMaxExperts];
-    int num_active;
-    int count;
-    int16_t id[kMaxDecodePairs];
-};
-
-// Load the route ids, validate them, and build the ascending list of active
-// experts.  Invalid ids become -1 (no work, zero contribution) and raise
-// kBadExpertId.
-__device__ void build_route(RouteLds& r, const void* ids, int ids_dtype, int pairs, int experts,
-                            int* status) {
-    for (int e = threadIdx.x; e < experts; e += kThreads) r.flag[e] = 0;
-    __syncthreads();
-    for (int p = threadIdx.x; p < pairs; p += kThreads) {
-        int64_t id = load_id(ids, p, ids_dtype);
-        bool ok = id >= 0 && id < experts;
-        if (!ok) raise_status(status, kBadExpertId);
-        r.id[p] = ok ? (int16_t)id : (int16_t)-1;
-        if (ok) r.flag[id] = 1;
-    }
-    __syncthreads();
-    if (threadIdx.x < kWave) {
-        int lane = threadIdx.x, base = 0;
-        for (int c = 0; c < experts; c += kWave) {
-            int e = c + lane;
-            bool on = e < experts && r.flag[e];
-            uint64_t mask = __ballot(on);
-            if (on) r.active[base + __popcll(mask & ((1ull << lane) - 1))] = e;
-            base += __popcll(mask);
-        }
-        if (lane == 0) r.num_active = base;
-    }
-    __syncthreads();
-}
-
-// Pairs routed to expert e, in ascending pair order, into `out`; returns the
-// count.  Executed by one whole wave.
-__device__ int wave_pairs_of(const RouteLds& r, int pairs, int e, int* out) {
-    int lane = threadIdx.x % kWave, count = 0;
-    for (int c = 0; c < pairs; c += kWave) {
-        int p = c + lane;
-        bool on = p < pairs && r.id[p] == e;
-        uint64_t mask = __ballot(on);
-        if (on) out[count + __popcll(mask & ((1ull << lane) - 1))] = p;
-        count += __popcll(mask);
-    }
-    return count;
-}
+constexpr int kUpWaves = 8, kUpThreads = kUpWaves * kWave;
+constexpr int kDnWaves = 4, kDnThreads = kDnWaves * kWave;
+constexpr int kRowsPerPass = 4;  // activation rows per MFMA pass of the gate/up kernel
 
 __device__ __forceinline__ float proj_scale(const Fp8Proj& p, int e, int n, int kb) {
     return p.s[(int64_t)e * p.s_se + (int64_t)(n / p.n_div) * p.s_sn + (int64_t)(kb / p.kb_div) * p.s_sk];
 }
 
 __device__ __forceinline__ v8i load32(const uint8_t* p) {
-    v4i lo = *(const v4i*)p, hi = *(const v4i*)(p + 16);
+    const v4i lo = *(const v4i*)p, hi = *(const v4i*)(p + 16);
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Weight stream: read once per call, marked non-temporal so the streamed bank
+// does not evict the small per-call data (grouping, activations) and code from L2.
+__device__ __forceinline__ v8i load32_stream(const uint8_t* p) {
+    const v4i lo = __builtin_nontemporal_load((const v4i*)p), hi = __builtin_nontemporal_load((const v4i*)(p + 16));
     return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
 __device__ __forceinline__ bool finite(float v) { return fabsf(v) <= 3.402823466e38f; }
+
+struct F8 {
+    float v[8];
+};
+
+__device__ __forceinline__ F8 zero8() {
+    F8 r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r.v[j] = 0.0f;
+    return r;
+}
+
+__device__ __forceinline__ uint64_t encode8(const F8& x, float scale) {
+    uint64_t q = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q |= (uint64_t)fp8_encode(x.v[j] / scale) << (8 * j);
+    return q;
+}
+
+__device__ __forceinline__ float absmax8(const F8& x, int* status) {
+    float m = 0.0f;
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        m = fmaxf(m, fabsf(x.v[j]));
+        ok = ok && finite(x.v[j]);
+    }
+    if (!ok) raise_status(status, kNonFinite);
+    return m;
+}
+
+// Pairs of active expert `ai` in ascending order into `out` (one whole wave);
+// returns the count.  The pair set is the grouping's bitmask.
+__device__ int wave_pairs_of(const Grouping* g, int ai, int pairs, int* out) {
+    const int lane = threadIdx.x % kWave;
+    int count = 0;
+    for (int c = 0; c < pairs; c += kWave) {
+        const int p = c + lane;
+        const bool on = p < pairs && ((g->mask[ai][p / 32] >> (p % 32)) & 1u);
+        const uint64_t bits = __ballot(on);
+        if (on) out[count + __popcll(bits & ((1ull << lane) - 1))] = p;
+        count += __popcll(bits);
+    }
+    return count;
+}
 
 }  // namespace
 
 // ---------------------------------------------------------------- gate / up
 
 struct GateUpLds {
-    RouteLds route;
-    int rows[kMaxDecodePairs];                 // pairs of this workgroup's expert
-    alignas(16) uint8_t qa[kWaves][16][128];   // per-wave quantized A block
-    float sa[kWaves][16];                      // its activation scales
-    float red[kWaves][kWave][8];               // cross-wave reduction of gate/up
+    int rows[kUpWaves][kMaxDecodePairs];        // each wave's copy of the expert's pairs
+    float red[kUpWaves][kWave][8];              // cross-wave gate/up reduction
     int last;
 };
 
-// KBW = 128-column K blocks per wave (H <= 4 * 128 * KBW).
+// KBW = 128-column K blocks per wave (H <= 8 * 128 * KBW).
 template <int KBW>
-__global__ __launch_bounds__(kThreads) void fp8_gateup_decode_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(kUpThreads, (KBW <= 2 ? 4 : 2)) void fp8_gateup_decode_kernel(GateUpArgs a) {
     __shared__ GateUpLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    build_route(s.route, a.ids, a.ids_dtype, a.pairs, a.experts, a.status);
-    if ((int)blockIdx.x >= s.route.num_active) return;
-    const int e = s.route.active[blockIdx.x];
+    const Grouping* gr = a.grouping;
+    if ((int)blockIdx.x >= gr->num_active) return;
+    const int e = gr->expert[blockIdx.x];
     const int I = a.w13.N / 2, H = a.w13.K, KB = H / 128;
     const int n0 = blockIdx.y * 16;
     const int col = lane % 16, grp = lane / 16;
+    int* rows = s.rows[wave];
+    const int M = wave_pairs_of(gr, blockIdx.x, a.pairs, rows);  // per wave: no barrier
+    const v4f zero = {0, 0, 0, 0};
+    const v8i zero8i = {0, 0, 0, 0, 0, 0, 0, 0};
 
-    // Issue this wave's weight loads first: gate row n0+col and up row I+n0+col.
+    // A fragments of a pass: lane (col, grp) holds row `col` (< mc), K slice
+    // grp; per-row activation scales for the C rows 4 * grp + r (grp 0 only).
+    auto load_a = [&](int m0, int mc, v8i* af, float (*sx)[4]) {
+        const bool live = col < mc;
+        const int64_t row = live ? rows[m0 + col] / a.row_div : 0;
+#pragma unroll
+        for (int i = 0; i < KBW; ++i) {
+            const int kb = wave + i * kUpWaves;
+            if (kb < KB) {
+                af[i] = live ? load32(a.xq + row * a.xq_row_stride + kb * 128 + grp * 32) : zero8i;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool lr = grp == 0 && r < mc;
+                    const int64_t rr = lr ? rows[m0 + r] / a.row_div : 0;
+                    sx[i][r] = lr ? a.xs[rr * a.xs_row_stride + (a.x_group == 128 ? kb : 0)] : 0.0f;
+                }
+            }
+        }
+    };
+
+    // activation fragments of the first pass, then the weight stream
+    v8i af[KBW];
+    float sx[KBW][4];
+    load_a(0, min(kRowsPerPass, M), af, sx);
     const uint8_t* wg = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)(n0 + col) * a.w13.w_sn + grp * 32;
     const uint8_t* wu = wg + (int64_t)I * a.w13.w_sn;
     v8i bg[KBW], bu[KBW];
+    float swg[KBW], swu[KBW];
 #pragma unroll
     for (int i = 0; i < KBW; ++i) {
-        const int kb = wave + i * kWaves;
+        const int kb = wave + i * kUpWaves;
         if (kb < KB) {
-            bg[i] = load32(wg + kb * 128);
-            bu[i] = load32(wu + kb * 128);
+            bg[i] = load32_stream(wg + kb * 128);
+            bu[i] = load32_stream(wu + kb * 128);
+            swg[i] = proj_scale(a.w13, e, n0 + col, kb);
+            swu[i] = proj_scale(a.w13, e, I + n0 + col, kb);
         }
     }
 
-    if (wave == 0) {
-        int m = wave_pairs_of(s.route, a.pairs, e, s.rows);
-        if (lane == 0) s.route.count = m;
-    }
-    __syncthreads();
-    const int M = s.route.count;
-
-    const float inv448 = 1.0f / 448.0f;
-    for (int m0 = 0; m0 < M; m0 += 16) {
-        const int mc = min(16, M - m0);
-        v4f acc_g = {0, 0, 0, 0}, acc_u = {0, 0, 0, 0};
+    for (int m0 = 0; m0 < M; m0 += kRowsPerPass) {
+        const int mc = min(kRowsPerPass, M - m0);
+        if (m0 > 0) load_a(m0, mc, af, sx);
+        v4f acc_g = zero, acc_u = zero;
 #pragma unroll
         for (int i = 0; i < KBW; ++i) {
-            const int kb = wave + i * kWaves;
+            const int kb = wave + i * kUpWaves;
             if (kb < KB) {
-            // Activation block kb of rows m0..m0+mc into LDS (quantized here,
-            // or copied when the caller passes FP8 bytes and scales).
-#pragma unroll 1
-            for (int m = 0; m < 16; ++m) {
-                uint32_t q2 = 0;
-                float scale = 0.0f;
-                if (m < mc) {
-                    const int64_t row = s.rows[m0 + m] / a.row_div;
-                    if (a.xq) {
-                        q2 = *(const uint16_t*)(a.xq + row * a.xq_row_stride + kb * 128 + 2 * lane);
-                        scale = a.xs[row * a.xs_row_stride + (a.x_group == 128 ? kb : 0)];
-                    } else {
-                        const int64_t base = row * a.x_row_stride;
-                        const float v0 = load_as_f32(a.x, base + kb * 128 + 2 * lane, a.x_dtype);
-                        const float v1 = load_as_f32(a.x, base + kb * 128 + 2 * lane + 1, a.x_dtype);
-                        float amax;
-                        if (a.x_group == 128) {
-                            amax = fmaxf(fabsf(v0), fabsf(v1));
-                        } else {
-                            amax = 0.0f;
-                            for (int k = lane; k < H; k += kWave)
-                                amax = fmaxf(amax, fabsf(load_as_f32(a.x, base + k, a.x_dtype)));
-                        }
-                        if (!finite(v0) || !finite(v1)) raise_status(a.status, kNonFinite);
-                        amax = fmaxf(wave_max(amax), 1e-10f);
-                        scale = amax * inv448;
-                        q2 = fp8_encode(v0 / scale) | (fp8_encode(v1 / scale) << 8);
-                    }
-                }
-                *(uint16_t*)&s.qa[wave][m][2 * lane] = (uint16_t)q2;
-                if (lane == 0) s.sa[wave][m] = scale;
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes done
-            __builtin_amdgcn_wave_barrier();
-            const v8i afrag = *(const v8i*)&s.qa[wave][col][grp * 32];
-            const v4f zero = {0, 0, 0, 0};
-            const v4f dg = mfma_fp8(afrag, bg[i], zero);
-            const v4f du = mfma_fp8(afrag, bu[i], zero);
-            const float swg = proj_scale(a.w13, e, n0 + col, kb);
-            const float swu = proj_scale(a.w13, e, I + n0 + col, kb);
+                const v4f dg = mfma_fp8(af[i], bg[i], zero), du = mfma_fp8(af[i], bu[i], zero);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float sx = s.sa[wave][grp * 4 + r];
-                acc_g[r] = fmaf(dg[r] * sx, swg, acc_g[r]);
-                acc_u[r] = fmaf(du[r] * sx, swu, acc_u[r]);
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);
-            __builtin_amdgcn_wave_barrier();
+                for (int r = 0; r < 4; ++r) {
+                    acc_g[r] = fmaf(dg[r] * sx[i][r], swg[i], acc_g[r]);
+                    acc_u[r] = fmaf(du[r] * sx[i][r], swu[i], acc_u[r]);
+                }
             }
         }
 #pragma unroll
@@ -206,123 +190,199 @@ __global__ __launch_bounds__(kThreads) void fp8_gateup_decode_kernel(GateUpArgs 
             s.red[wave][lane][4 + r] = acc_u[r];
         }
         __syncthreads();
-        if (wave == 0) {
+        if (wave == 0 && grp == 0) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float g = s.red[0][lane][r], u = s.red[0][lane][4 + r];
-                for (int w = 1; w < kWaves; ++w) {
-                    g += s.red[w][lane][r];
-                    u += s.red[w][lane][4 + r];
-                }
-                const int m = grp * 4 + r;
-                if (m < mc) {
+                if (r < mc) {
+                    float g = s.red[0][lane][r], u = s.red[0][lane][4 + r];
+                    for (int w = 1; w < kUpWaves; ++w) {
+                        g += s.red[w][lane][r];
+                        u += s.red[w][lane][4 + r];
+                    }
                     g = round_through(g, a.gu_dtype);
                     u = round_through(u, a.gu_dtype);
+                    float* dst = a.h32 + (int64_t)rows[m0 + r] * I + n0 + col;
                     const float h = g / (1.0f + __expf(-g)) * u;
-                    a.h32[(int64_t)s.rows[m0 + m] * I + n0 + col] = h;
+                    if (a.quantize_hidden) store_coherent(dst, h);
+                    else *dst = h;
                 }
             }
         }
         __syncthreads();
     }
+    if (!a.quantize_hidden) return;  // the down kernel quantizes h
 
-    // The last of the 8 column tiles of this 128-group quantizes it.
+    // The last of the 8 column tiles of this 128-group quantizes it: one
+    // 16-lane row per pair, 8 values per lane, read coherently.
     const int group = n0 / 128;
     int* counter = a.counters + (int64_t)blockIdx.x * (I / 128) + group;
     if (!arrive_last(counter, 128 / 16, &s.last)) return;
-    for (int m = wave; m < M; m += kWaves) {
-        const int64_t p = s.rows[m];
-        const float* hrow = a.h32 + p * I + group * 128;
-        const float v0 = hrow[2 * lane], v1 = hrow[2 * lane + 1];
-        if (!finite(v0) || !finite(v1)) raise_status(a.status, kNonFinite);
-        const float amax = fmaxf(wave_max(fmaxf(fabsf(v0), fabsf(v1))), 1e-10f);
-        const float scale = amax * inv448;
-        const uint32_t q2 = fp8_encode(v0 / scale) | (fp8_encode(v1 / scale) << 8);
-        *(uint16_t*)(a.hq + p * I + group * 128 + 2 * lane) = (uint16_t)q2;
-        if (lane == 0) a.hs[p * (I / 128) + group] = scale;
+    for (int m = threadIdx.x / 16; m < M; m += kUpThreads / 16) {
+        const int64_t p = s.rows[0][m];
+        const float* hrow = a.h32 + p * I + group * 128 + col * 8;
+        F8 h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h.v[j] = load_coherent(hrow + j);
+        const float scale = fmaxf(row_max(absmax8(h, a.status)), 1e-10f) * (1.0f / 448.0f);
+        *(uint64_t*)(a.hq + p * I + group * 128 + col * 8) = encode8(h, scale);
+        if (col == 0) a.hs[p * (I / 128) + group] = scale;
     }
 }
 
 // ---------------------------------------------------------------------- down
 
 struct DownLds {
-    RouteLds route;
-    int rows[kWaves][kMaxDecodePairs];
+    float wt[kMaxDecodePairs];                  // route weights of all pairs, fp32
+    int rows[kDnWaves][2][kMaxDecodePairs];     // pairs of the wave's two experts
     float part[kMaxDecodePairs][8];
+    alignas(16) uint8_t hq[kDownQuantBytes];    // hidden FP8 quantized here (small decode)
+    float hs[kDownQuantBytes / 128];
 };
 
-// KBM = upper bound of 128-column K blocks (I <= 128 * KBM).
-template <int KBM>
-__global__ __launch_bounds__(kThreads) void fp8_down_decode_kernel(DownArgs a) {
+template <int KB2>
+struct DownBatch {
+    v8i b[KB2];
+    float sw[KB2];
+    int ai0, ai1;  // active indices of the two experts (ai1 = -1: none)
+};
+
+// Batch bi = active experts 2 bi and 2 bi + 1 (if any).
+template <int KB2>
+__device__ __forceinline__ void load_down_batch(const DownArgs& a, int num_active, int bi, int n0, int col, int grp,
+                                                int KB, DownBatch<KB2>& bt) {
+    const v8i zero8i = {0, 0, 0, 0, 0, 0, 0, 0};
+    bt.ai0 = 2 * bi;
+    bt.ai1 = 2 * bi + 1 < num_active ? 2 * bi + 1 : -1;
+    const int ai = col < 8 ? bt.ai0 : bt.ai1;
+    const int e = ai >= 0 ? a.grouping->expert[ai] : -1;
+    const int n = n0 + (col & 7);
+    const uint8_t* wrow = a.w2.w + (int64_t)(e < 0 ? 0 : e) * a.w2.w_se + (int64_t)n * a.w2.w_sn + grp * 32;
+#pragma unroll
+    for (int kb = 0; kb < KB2; ++kb) {
+        bt.b[kb] = (e >= 0 && kb < KB) ? load32_stream(wrow + kb * 128) : zero8i;
+        bt.sw[kb] = (e >= 0 && kb < KB) ? proj_scale(a.w2, e, n, kb) : 0.0f;
+    }
+}
+
+// KB2 = upper bound of the 128-column K blocks of the down projection
+// (I <= 128 * KB2); the runtime count KB guards every block.
+template <int KB2>
+__global__ __launch_bounds__(kDnThreads) void fp8_down_decode_kernel(DownArgs a) {
     __shared__ DownLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int col = lane % 16, grp = lane / 16;
     const int I = a.w2.K, H = a.w2.N, KB = I / 128;
     const int n0 = blockIdx.x * 8;
-    for (int i = threadIdx.x; i < a.pairs * 8; i += kThreads) s.part[i / 8][i % 8] = 0.0f;
-    build_route(s.route, a.ids, a.ids_dtype, a.pairs, a.experts, a.status);
-    const bool live_col = col < 8;
-    const int n = n0 + (live_col ? col : 0);
+    const v4f zero = {0, 0, 0, 0};
+    const v8i zero8i = {0, 0, 0, 0, 0, 0, 0, 0};
 
-    for (int ai = wave; ai < s.route.num_active; ai += kWaves) {
-        const int e = s.route.active[ai];
-        const uint8_t* wrow = a.w2.w + (int64_t)e * a.w2.w_se + (int64_t)n * a.w2.w_sn + grp * 32;
-        v8i b[KBM];
-        float sw[KBM];
+    // Entry loads: the fp32 hidden rows to quantize (small calls), the route
+    // weights, the grouping; then the first weight batch.
+    constexpr int kQuantPasses = kDownQuantBytes / 128 / (kDnThreads / 16);
+    F8 hv[kQuantPasses];
+    const int units = a.quantize_hidden ? a.pairs * KB : 0;
+    const int unit0 = threadIdx.x / 16;
+    if (a.quantize_hidden) {
 #pragma unroll
-        for (int kb = 0; kb < KBM; ++kb) {
-            if (kb < KB) {
-                b[kb] = live_col ? load32(wrow + kb * 128) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-                sw[kb] = proj_scale(a.w2, e, n, kb);
+        for (int q = 0; q < kQuantPasses; ++q) {
+            const int u = unit0 + q * (kDnThreads / 16);
+            if (u < units) {
+                const float* src = a.h32 + (int64_t)(u / KB) * I + (u % KB) * 128 + col * 8;
+                const v4f h0 = *(const v4f*)src, h1 = *(const v4f*)(src + 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hv[q].v[j] = h0[j];
+                    hv[q].v[4 + j] = h1[j];
+                }
+            } else {
+                hv[q] = zero8();
             }
         }
-        const int M = wave_pairs_of(s.route, a.pairs, e, s.rows[wave]);
-        for (int m0 = 0; m0 < M; m0 += 16) {
-            const int mc = min(16, M - m0);
-            const bool live_row = col < mc;
-            const int64_t prow = live_row ? s.rows[wave][m0 + col] : 0;
-            int64_t rrow[4];
+    }
+    for (int p = threadIdx.x; p < a.pairs; p += kDnThreads) s.wt[p] = load_as_f32(a.weights, p, a.w_dtype);
+    for (int i = threadIdx.x; i < a.pairs * 8; i += kDnThreads) s.part[i / 8][i % 8] = 0.0f;
+    const int num_active = a.grouping->num_active;
+    const int batches = (num_active + 1) / 2;
+    DownBatch<KB2> cur;
+    if (wave < batches) load_down_batch<KB2>(a, num_active, wave, n0, col, grp, KB, cur);
+    if (a.quantize_hidden) {
+#pragma unroll
+        for (int q = 0; q < kQuantPasses; ++q) {
+            const int u = unit0 + q * (kDnThreads / 16);
+            if (u < units) {
+                const float scale = fmaxf(row_max(absmax8(hv[q], a.status)), 1e-10f) * (1.0f / 448.0f);
+                *(uint64_t*)&s.hq[(u / KB) * I + (u % KB) * 128 + col * 8] = encode8(hv[q], scale);
+                if (col == 0) s.hs[u] = scale;
+            }
+        }
+    }
+    __syncthreads();
+    const uint8_t* hq = a.quantize_hidden ? s.hq : a.hq;
+    const float* hs = a.quantize_hidden ? s.hs : a.hs;
+
+    for (int bi = wave; bi < batches; bi += kDnWaves) {
+        const int M0 = wave_pairs_of(a.grouping, cur.ai0, a.pairs, s.rows[wave][0]);
+        const int M1 = cur.ai1 >= 0 ? wave_pairs_of(a.grouping, cur.ai1, a.pairs, s.rows[wave][1]) : 0;
+        const int passes = max((M0 + 7) / 8, (M1 + 7) / 8);
+        // pair of A row `row` (0..7: expert ai0, 8..15: expert ai1) in a pass
+        auto a_row = [&](int pass, int row) -> int {
+            const int m = pass * 8 + (row & 7);
+            if (row < 8) return m < M0 ? s.rows[wave][0][m] : -1;
+            return m < M1 ? s.rows[wave][1][m] : -1;
+        };
+        v8i af[KB2];
+        const int arow0 = a_row(0, col);
+#pragma unroll
+        for (int kb = 0; kb < KB2; ++kb)
+            af[kb] = (arow0 >= 0 && kb < KB) ? load32(hq + (int64_t)arow0 * I + kb * 128 + grp * 32) : zero8i;
+        // the next batch's weights go out after this batch's activation loads
+        DownBatch<KB2> nxt;
+        const bool more = bi + kDnWaves < batches;
+        if (more) load_down_batch<KB2>(a, num_active, bi + kDnWaves, n0, col, grp, KB, nxt);
+        for (int pass = 0; pass < passes; ++pass) {
+            if (pass > 0) {
+                const int ar = a_row(pass, col);
+#pragma unroll
+                for (int kb = 0; kb < KB2; ++kb)
+                    af[kb] = (ar >= 0 && kb < KB) ? load32(hq + (int64_t)ar * I + kb * 128 + grp * 32) : zero8i;
+            }
+            int crow[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = grp * 4 + r;
-                rrow[r] = m < mc ? s.rows[wave][m0 + m] : -1;
+                const int row = grp * 4 + r;
+                // keep the diagonal blocks: B column half must match A row half
+                crow[r] = ((row < 8) == (col < 8)) ? a_row(pass, row) : -1;
             }
-            v4f acc = {0, 0, 0, 0};
+            v4f acc = zero;
 #pragma unroll
-            for (int kb = 0; kb < KBM; ++kb) {
+            for (int kb = 0; kb < KB2; ++kb) {
                 if (kb < KB) {
-                const v8i afrag = live_row ? load32(a.hq + prow * I + kb * 128 + grp * 32)
-                                           : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-                const v4f zero = {0, 0, 0, 0};
-                const v4f d = mfma_fp8(afrag, b[kb], zero);
+                    const v4f d = mfma_fp8(af[kb], cur.b[kb], zero);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float sx = rrow[r] >= 0 ? a.hs[rrow[r] * KB + kb] : 0.0f;
-                    acc[r] = fmaf(d[r] * sx, sw[kb], acc[r]);
-                }
+                    for (int r = 0; r < 4; ++r) {
+                        const float sxv = crow[r] >= 0 ? hs[(int64_t)crow[r] * KB + kb] : 0.0f;
+                        acc[r] = fmaf(d[r] * sxv, cur.sw[kb], acc[r]);
+                    }
                 }
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (rrow[r] >= 0 && live_col) {
-                    const int p = (int)rrow[r];
-                    s.part[p][col] = acc[r] * load_as_f32(a.weights, p, a.w_dtype);
-                }
-            }
+            for (int r = 0; r < 4; ++r)
+                if (crow[r] >= 0) s.part[crow[r]][col & 7] = acc[r] * s.wt[crow[r]];
         }
+        if (more) cur = nxt;
     }
     __syncthreads();
 
     if (a.out_pairs) {
         // forward_pairs: ordered fp32 partials, one row per pair.
-        for (int i = threadIdx.x; i < a.pairs * 8; i += kThreads) {
+        for (int i = threadIdx.x; i < a.pairs * 8; i += kDnThreads) {
             const int p = i / 8, c = i % 8;
             a.out_pairs[(int64_t)p * H + n0 + c] = s.part[p][c];
         }
     } else {
         // Layer output: fp32 sum of each token's partials in router slot order.
         const int tokens = a.pairs / a.top_k;
-        for (int i = threadIdx.x; i < tokens * 8; i += kThreads) {
+        for (int i = threadIdx.x; i < tokens * 8; i += kDnThreads) {
             const int t = i / 8, c = i % 8;
             float acc = s.part[t * a.top_k][c];
             for (int j = 1; j < a.top_k; ++j) acc += s.part[t * a.top_k + j][c];
@@ -332,19 +392,19 @@ __global__ __launch_bounds__(kThreads) void fp8_down_decode_kernel(DownArgs a) {
 }
 
 void launch_fp8_gateup_decode(const GateUpArgs& a, int max_active, hipStream_t stream) {
-    const dim3 grid(max_active, a.w13.N / 2 / 16), block(kThreads);
-    const int kbw = (a.w13.K / 128 + kWaves - 1) / kWaves;
+    const dim3 grid(max_active, a.w13.N / 2 / 16), block(kUpThreads);
+    const int kbw = (a.w13.K / 128 + kUpWaves - 1) / kUpWaves;
     if (kbw <= 1) hipLaunchKernelGGL(fp8_gateup_decode_kernel<1>, grid, block, 0, stream, a);
     else if (kbw <= 2) hipLaunchKernelGGL(fp8_gateup_decode_kernel<2>, grid, block, 0, stream, a);
     else if (kbw <= 4) hipLaunchKernelGGL(fp8_gateup_decode_kernel<4>, grid, block, 0, stream, a);
-    else if (kbw <= 8) hipLaunchKernelGGL(fp8_gateup_decode_kernel<8>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(fp8_gateup_decode_kernel<16>, grid, block, 0, stream, a);
+    else hipLaunchKernelGGL(fp8_gateup_decode_kernel<8>, grid, block, 0, stream, a);
 }
 
 void launch_fp8_down_decode(const DownArgs& a, hipStream_t stream) {
-    const dim3 grid(a.w2.N / 8), block(kThreads);
+    const dim3 grid(a.w2.N / 8), block(kDnThreads);
     const int kb = a.w2.K / 128;
-    if (kb <= 4) hipLaunchKernelGGL(fp8_down_decode_kernel<4>, grid, block, 0, stream, a);
+    if (kb <= 2) hipLaunchKernelGGL(fp8_down_decode_kernel<2>, grid, block, 0, stream, a);
+    else if (kb <= 4) hipLaunchKernelGGL(fp8_down_decode_kernel<4>, grid, block, 0, stream, a);
     else if (kb <= 6) hipLaunchKernelGGL(fp8_down_decode_kernel<6>, grid, block, 0, stream, a);
     else if (kb <= 8) hipLaunchKernelGGL(fp8_down_decode_kernel<8>, grid, block, 0, stream, a);
     else if (kb <= 16) hipLaunchKernelGGL(fp8_down_decode_kernel<16>, grid, block, 0, stream, a);

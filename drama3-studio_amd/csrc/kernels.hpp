@@ -11,6 +11,12 @@ constexpr int kMaxExperts = 512;      // routed experts per bank
 constexpr int kMaxDecodePairs = 256;  // tokens * top_k handled by the decode kernels
 constexpr int kMaxHidden = 8192;
 constexpr int kMaxInter = 4096;
+// Hidden-activation bytes (pairs * I) the down kernel quantizes itself in LDS
+// for small decode calls; larger calls quantize in the gate/up kernel.
+constexpr int kDownQuantBytes = 8192;  // 64 (pair, 128-group) units: 4 passes of 16
+constexpr int kDownQuantPairs = 16;
+// Activation bytes the gate/up kernel stages in LDS at entry (all rows a call reads).
+constexpr int kStageBytes = 16384;
 
 // One FP8 projection bank [E, N, K] (K contiguous) with fp32 scales addressed
 // as s[e*s_se + (n / n_div)*s_sn + (kb / kb_div)*s_sk] for 128-column block kb.
@@ -23,23 +29,44 @@ struct Fp8Proj {
     int32_t N, K;
 };
 
+// Where a decode kernel takes its routes from: caller ids, or router logits
+// it routes itself (then ids_out / weights_out receive the routing).
+struct RouteSource {
+    const void* ids;
+    int ids_dtype;
+    const float* logits;
+    int64_t logits_row_stride;
+    int top_k;
+    int renormalize;
+    int64_t* ids_out;
+    void* weights_out;
+    int w_dtype;
+};
+
+// Expert grouping of the route pairs of one decode call, written once by the
+// prep kernel and read by both decode kernels: the ascending active experts
+// and, per active expert, a bitmask of its pairs (pair p <-> bit p).
+struct Grouping {
+    int num_active;
+    int pad[3];
+    int expert[kMaxExperts];
+    uint32_t mask[kMaxExperts][kMaxDecodePairs / 32];
+};
+
 struct GateUpArgs {
     Fp8Proj w13;
     int experts;
-    // activations: either raw rows (x) or pre-quantized rows (xq, xs)
-    const void* x;
-    int x_dtype;
-    int64_t x_row_stride;
+    const Grouping* grouping;
+    // FP8 activation rows (prep output or caller's) and their scales
     const uint8_t* xq;
     const float* xs;
     int64_t xq_row_stride, xs_row_stride;
     int x_group;        // 128 or K (one scale per row)
-    const void* ids;
-    int ids_dtype;
     int pairs;
     int row_div;        // pair p reads activation row p / row_div
     int gu_dtype;       // storage type gate/up are rounded through
     float* h32;         // [pairs, I] silu(gate) * up
+    int quantize_hidden;  // 1: quantize h here (arrival counter); 0: the down kernel does
     uint8_t* hq;        // [pairs, I] FP8 hidden
     float* hs;          // [pairs, I/128]
     int* counters;      // [min(pairs, experts), I/128], zero at first use
@@ -49,10 +76,11 @@ struct GateUpArgs {
 struct DownArgs {
     Fp8Proj w2;
     int experts;
-    const uint8_t* hq;
+    const Grouping* grouping;
+    const float* h32;       // [pairs, I] when quantize_hidden: quantized in the kernel ...
+    int quantize_hidden;
+    const uint8_t* hq;      // ... else the FP8 hidden [pairs, I] and scales
     const float* hs;
-    const void* ids;
-    int ids_dtype;
     const void* weights;
     int w_dtype;
     int pairs;
@@ -65,6 +93,8 @@ struct DownArgs {
 };
 
 constexpr int kMaxPermutePairs = 16384;  // pairs one permutation workgroup sorts
+constexpr int kRouteElems = 1024;   // logits one workgroup ranks at a time (tokens * experts)
+constexpr int kRouteTokens = 8;     // tokens one workgroup routes at a time
 
 struct QuantArgs {
     const void* x;          // [rows, cols] (or [rows, 2*cols] gate|up when silu_mul)
@@ -97,6 +127,16 @@ struct PermuteArgs {
     int* status;
 };
 
+struct PrepArgs {
+    RouteSource route;      // caller ids, or router logits (routing also written out)
+    int pairs, experts;
+    QuantArgs quant;        // activation rows to quantize (quant.x == nullptr: none)
+    Grouping* grouping;
+    int* status;
+};
+
+void launch_moe_prep(const PrepArgs& a, hipStream_t stream);
+int quantize_blocks(const QuantArgs& a);
 void launch_fp8_gateup_decode(const GateUpArgs& a, int max_active, hipStream_t stream);
 void launch_fp8_down_decode(const DownArgs& a, hipStream_t stream);
 void launch_fp8_quantize(const QuantArgs& a, hipStream_t stream);

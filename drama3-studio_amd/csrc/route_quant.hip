@@ -1,9 +1,182 @@
-// Router top-k, stable expert permutation, and the standalone FP8 activation
-// quantizers of the MoE expert path.
+// Router, route grouping and FP8 activation quantization of the MoE expert
+// path, plus the stable permutation of route pairs.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace dmoe {
+
+namespace {
+
+__device__ __forceinline__ bool finite(float v) { return fabsf(v) <= 3.402823466e38f; }
+
+struct F8 {
+    float v[8];
+};
+
+__device__ __forceinline__ F8 load8(const void* x, int64_t i, int dtype) {
+    F8 r;
+    if (dtype == kF32) {
+        const v4f a = *(const v4f*)((const float*)x + i), b = *(const v4f*)((const float*)x + i + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r.v[j] = a[j];
+            r.v[4 + j] = b[j];
+        }
+    } else {
+        const v4i w = *(const v4i*)((const uint16_t*)x + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t u = (uint32_t)w[j];
+            if (dtype == kBF16) {
+                r.v[2 * j] = __uint_as_float(u << 16);
+                r.v[2 * j + 1] = __uint_as_float(u & 0xFFFF0000u);
+            } else {
+                r.v[2 * j] = f16_to_f32((uint16_t)(u & 0xFFFFu));
+                r.v[2 * j + 1] = f16_to_f32((uint16_t)(u >> 16));
+            }
+        }
+    }
+    return r;
+}
+
+// E4M3 bytes of v / scale (true division), packed little-endian.
+__device__ __forceinline__ uint64_t encode8(const F8& x, float scale) {
+    uint64_t q = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q |= (uint64_t)fp8_encode(x.v[j] / scale) << (8 * j);
+    return q;
+}
+
+__device__ __forceinline__ float absmax8(const F8& x, int* status) {
+    float m = 0.0f;
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        m = fmaxf(m, fabsf(x.v[j]));
+        ok = ok && finite(x.v[j]);
+    }
+    if (!ok) raise_status(status, kNonFinite);
+    return m;
+}
+
+// One DPP step of a (value desc, index asc) argmax within 16-lane rows.
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
+    const float ov = dpp_f32<CTRL>(bv);
+    const int oi = dpp_i32<CTRL>(bi);
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+// Router for a chunk of tokens by a whole workgroup, without serial rounds:
+// rank(t, e) = #{e' : l[e'] > l[e] or (l[e'] == l[e] and e' < e)}; the
+// experts of rank < k are the winners, rank = router slot.  Softmax max and
+// sum are workgroup reductions; weights = exp(l - max) / sum of the winners,
+// renormalised by their slot-order sum.  Reference: backbone_graph.py:317-323.
+// Results: ids_lds[t * k + slot] (local token t), and -- when `publish` -- the
+// global ids / weights of token t0 + t.
+struct RouteScratch {
+    float lv[kRouteElems];   // logits of the chunk
+    float ex[kRouteElems];   // exp(l - max)
+    float red[16][kRouteTokens];
+    float pk[kRouteTokens][64];
+    int ik[kRouteTokens][64];
+};
+
+template <int THREADS>
+__device__ void block_route(RouteScratch& rs, const RouteSource& src, int t0, int tcount, int experts,
+                            int16_t* ids_lds, bool publish) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    constexpr int kWavesB = THREADS / kWave;
+    const int elems = tcount * experts;
+    for (int i = threadIdx.x; i < elems; i += THREADS) {
+        const int t = i / experts, e = i % experts;
+        rs.lv[i] = src.logits[(int64_t)(t0 + t) * src.logits_row_stride + e];
+    }
+    __syncthreads();
+    // per-token max: one wave per token
+    for (int t = wave; t < tcount; t += kWavesB) {
+        float m = -INFINITY;
+#pragma unroll 4
+        for (int e = lane; e < experts; e += kWave) m = fmaxf(m, rs.lv[t * experts + e]);
+        m = wave_max_dpp(m);
+        if (lane == 0) rs.red[0][t] = m;
+    }
+    __syncthreads();
+    // ranks: TPE threads share one element's comparisons (quad of lanes)
+    const int tpe = elems * 4 <= THREADS ? 4 : elems * 2 <= THREADS ? 2 : 1;
+    const int sub = threadIdx.x % tpe;
+    for (int base = 0; base < elems; base += THREADS / tpe) {
+        const int i = base + threadIdx.x / tpe;
+        const bool live = i < elems;
+        const int t = live ? i / experts : 0, e = live ? i % experts : 0;
+        const float v = live ? rs.lv[i] : 0.0f;
+        int rank = 0;
+        if (live) {
+            // this thread's contiguous share of the row, 16 values per step
+            // (four 16-byte LDS reads in flight)
+            const float* row = rs.lv + t * experts;
+            const int per = (experts + tpe - 1) / tpe;
+            const int o0 = sub * per, o1 = min(experts, o0 + per);
+            int o = o0;
+            if (((t * experts + o0) & 3) == 0) {
+                for (; o + 16 <= o1; o += 16) {
+                    const v4f q0 = *(const v4f*)(row + o), q1 = *(const v4f*)(row + o + 4);
+                    const v4f q2 = *(const v4f*)(row + o + 8), q3 = *(const v4f*)(row + o + 12);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        rank += (q0[j] > v) || (q0[j] == v && o + j < e);
+                        rank += (q1[j] > v) || (q1[j] == v && o + 4 + j < e);
+                        rank += (q2[j] > v) || (q2[j] == v && o + 8 + j < e);
+                        rank += (q3[j] > v) || (q3[j] == v && o + 12 + j < e);
+                    }
+                }
+            }
+            for (; o < o1; ++o) {
+                const float w = row[o];
+                rank += (w > v) || (w == v && o < e);
+            }
+        }
+        if (tpe >= 2) rank += __builtin_bit_cast(int, dpp_f32<kDppXor1>(__builtin_bit_cast(float, rank)));
+        if (tpe >= 4) rank += __builtin_bit_cast(int, dpp_f32<kDppXor2>(__builtin_bit_cast(float, rank)));
+        if (live && sub == 0) {
+            const float x = expf(v - rs.red[0][t]);
+            rs.ex[i] = x;
+            if (rank < src.top_k) {
+                rs.ik[t][rank] = e;
+                rs.pk[t][rank] = x;  // divided by the sum below
+            }
+        }
+    }
+    __syncthreads();
+    // per-token sum of exp: one wave per token
+    for (int t = wave; t < tcount; t += kWavesB) {
+        float sum = 0.0f;
+#pragma unroll 4
+        for (int e = lane; e < experts; e += kWave) sum += rs.ex[t * experts + e];
+        sum = wave_sum_dpp(sum);
+        // winners: p = exp / sum, then the slot-order renormalisation
+        const float p = lane < src.top_k ? rs.pk[t][lane] / sum : 0.0f;
+        float wtot = 0.0f;
+        for (int j = 0; j < src.top_k; ++j) wtot += readlane_f32(p, j);
+        if (lane < src.top_k) {
+            const int id = rs.ik[t][lane];
+            ids_lds[t * src.top_k + lane] = (int16_t)id;
+            if (publish) {
+                src.ids_out[(int64_t)(t0 + t) * src.top_k + lane] = id;
+                store_from_f32(src.weights_out, (int64_t)(t0 + t) * src.top_k + lane, src.w_dtype,
+                               src.renormalize ? p / wtot : p);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+
+}  // namespace
 
 // ------------------------------------------------------------ FP8 quantizers
 
@@ -12,61 +185,57 @@ namespace dmoe {
 // fp8_decode.py:117, offload.py:308-310), restated at fp8_cpu_reference.py:14-20
 // and native/src/fp8_reference.cpp:52-93:
 //   scale = max(amax, 1e-10) * fl(1/448);  q = e4m3_rne(clamp(x / scale, +-448)).
-// One wave per 128-group (2 values per lane); for one scale per row the whole
-// 256-thread block reduces the row.
-__global__ __launch_bounds__(256) void fp8_quantize_kernel(QuantArgs a) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const float inv448 = 1.0f / 448.0f;
-    if (a.group == 128) {
-        const int groups = a.cols / 128;
-        const int64_t g = (int64_t)blockIdx.x * 4 + wave;
-        if (g >= (int64_t)a.rows * groups) return;
-        const int64_t row = g / groups, c0 = (g % groups) * 128;
-        float v0, v1;
-        if (a.silu_mul) {
-            const int64_t base = row * a.x_row_stride;
-            float g0 = load_as_f32(a.x, base + c0 + 2 * lane, a.x_dtype);
-            float g1 = load_as_f32(a.x, base + c0 + 2 * lane + 1, a.x_dtype);
-            float u0 = load_as_f32(a.x, base + a.cols + c0 + 2 * lane, a.x_dtype);
-            float u1 = load_as_f32(a.x, base + a.cols + c0 + 2 * lane + 1, a.x_dtype);
-            v0 = g0 / (1.0f + __expf(-g0)) * u0;
-            v1 = g1 / (1.0f + __expf(-g1)) * u1;
-        } else {
-            v0 = load_as_f32(a.x, row * a.x_row_stride + c0 + 2 * lane, a.x_dtype);
-            v1 = load_as_f32(a.x, row * a.x_row_stride + c0 + 2 * lane + 1, a.x_dtype);
-        }
-        if (!(fabsf(v0) <= 3.402823466e38f) || !(fabsf(v1) <= 3.402823466e38f))
-            raise_status(a.status, kNonFinite);
-        const float amax = fmaxf(wave_max(fmaxf(fabsf(v0), fabsf(v1))), 1e-10f);
-        const float scale = amax * inv448;
-        const uint32_t q2 = fp8_encode(v0 / scale) | (fp8_encode(v1 / scale) << 8);
-        *(uint16_t*)(a.q + row * a.cols + c0 + 2 * lane) = (uint16_t)q2;
-        if (lane == 0) a.scales[row * groups + c0 / 128] = scale;
-        return;
+// One 16-lane row per 128-group (8 values per lane, DPP max); for one scale
+// per row the 256-thread block reduces the row.  With `silu_mul` the row holds
+// gate|up and silu(gate) * up is quantized.
+__device__ void quantize_unit128(const QuantArgs& a, int64_t unit) {
+    const int col = threadIdx.x % 16;
+    const int groups = a.cols / 128;
+    const bool live = unit < (int64_t)a.rows * groups;
+    const int64_t row = live ? unit / groups : 0, c0 = live ? (unit % groups) * 128 : 0;
+    const int64_t base = row * a.x_row_stride;
+    F8 v;
+    if (a.silu_mul) {
+        F8 g = load8(a.x, base + c0 + col * 8, a.x_dtype), u = load8(a.x, base + a.cols + c0 + col * 8, a.x_dtype);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v.v[j] = g.v[j] / (1.0f + __expf(-g.v[j])) * u.v[j];
+    } else {
+        v = load8(a.x, base + c0 + col * 8, a.x_dtype);
     }
-    // one scale per row
+    const float scale = fmaxf(row_max(absmax8(v, live ? a.status : nullptr)), 1e-10f) * (1.0f / 448.0f);
+    if (live) {
+        *(uint64_t*)(a.q + row * a.cols + c0 + col * 8) = encode8(v, scale);
+        if (col == 0) a.scales[row * groups + c0 / 128] = scale;
+    }
+}
+
+__device__ void quantize_row(const QuantArgs& a, int64_t row) {
     __shared__ float red[4];
-    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int64_t base = row * a.x_row_stride;
     float amax = 0.0f;
-    for (int c = threadIdx.x; c < a.cols; c += 256) {
-        float v = load_as_f32(a.x, base + c, a.x_dtype);
-        if (!(fabsf(v) <= 3.402823466e38f)) raise_status(a.status, kNonFinite);
-        amax = fmaxf(amax, fabsf(v));
-    }
-    amax = wave_max(amax);
+    for (int c = threadIdx.x * 8; c < a.cols; c += 256 * 8) amax = fmaxf(amax, absmax8(load8(a.x, base + c, a.x_dtype), a.status));
+    amax = wave_max_dpp(amax);
     if (lane == 0) red[wave] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-10f);
-    const float scale = amax * inv448;
-    for (int c = threadIdx.x; c < a.cols; c += 256)
-        a.q[row * a.cols + c] = (uint8_t)fp8_encode(load_as_f32(a.x, base + c, a.x_dtype) / scale);
+    const float scale = amax * (1.0f / 448.0f);
+    for (int c = threadIdx.x * 8; c < a.cols; c += 256 * 8)
+        *(uint64_t*)(a.q + row * a.cols + c) = encode8(load8(a.x, base + c, a.x_dtype), scale);
     if (threadIdx.x == 0) a.scales[row] = scale;
 }
 
+__global__ __launch_bounds__(256) void fp8_quantize_kernel(QuantArgs a) {
+    if (a.group == 128) quantize_unit128(a, (int64_t)blockIdx.x * 16 + threadIdx.x / 16);
+    else quantize_row(a, blockIdx.x);
+}
+
+int quantize_blocks(const QuantArgs& a) {
+    return a.group == 128 ? (int)(((int64_t)a.rows * (a.cols / 128) + 15) / 16) : a.rows;
+}
+
 void launch_fp8_quantize(const QuantArgs& a, hipStream_t stream) {
-    const int64_t blocks = a.group == 128 ? ((int64_t)a.rows * (a.cols / 128) + 3) / 4 : a.rows;
-    hipLaunchKernelGGL(fp8_quantize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(fp8_quantize_kernel, dim3((unsigned)quantize_blocks(a)), dim3(256), 0, stream, a);
 }
 
 // Hardware E4M3 decode of a byte array (validation helper; the reference's
@@ -82,68 +251,100 @@ void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stre
 
 // ------------------------------------------------------------------ router
 
-// softmax(logits.float()) -> top-k -> optional renormalisation, one wave per
-// token.  Reference: src/drama_low_vram/backbone_graph.py:317-323.  Experts
-// are selected in (logit descending, index ascending) order -- softmax is
-// monotone, and exact ties resolve to the lower index.  Weights are the
-// selected softmax probabilities, divided by their slot-order sum when
-// renormalising, stored in the caller's dtype.
+// Stand-alone router: one workgroup per chunk of tokens.
 __global__ __launch_bounds__(256) void route_topk_kernel(RouteArgs a) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int64_t t = (int64_t)blockIdx.x * 4 + wave;
-    if (t >= a.tokens) return;
-    constexpr int kPer = kMaxExperts / kWave;
-    const float* l = a.logits + t * a.row_stride;
-    float v[kPer];
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int e = lane + i * kWave;
-        v[i] = e < a.experts ? l[e] : -INFINITY;
-        m = fmaxf(m, v[i]);
-    }
-    m = wave_max(m);
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int e = lane + i * kWave;
-        sum += e < a.experts ? expf(v[i] - m) : 0.0f;
-    }
-    sum = wave_sum(sum);
-    uint32_t taken = 0;
-    float wsel = 0.0f, wtot = 0.0f;
-    for (int j = 0; j < a.top_k; ++j) {
-        // lane-local best, then (value desc, index asc) butterfly
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int e = lane + i * kWave;
-            if (e < a.experts && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && e < bi))) {
-                bv = v[i];
-                bi = e;
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, kWave);
-            const int oi = __shfl_xor(bi, o, kWave);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if (bi % kWave == lane) taken |= 1u << (bi / kWave);
-        const float p = expf(bv - m) / sum;
-        if (lane == j) wsel = p;
-        wtot += p;  // same sequence on every lane: slot-order sum
-        if (lane == 0) a.ids[t * a.top_k + j] = bi;
-    }
-    if (lane < a.top_k) {
-        const float w = a.renormalize ? wsel / wtot : wsel;
-        store_from_f32(a.weights, t * a.top_k + lane, a.w_dtype, w);
-    }
+    __shared__ RouteScratch rs;
+    __shared__ int16_t ids[kRouteTokens * 64];
+    const RouteSource src{nullptr, kI64, a.logits, a.row_stride, a.top_k, a.renormalize, a.ids, a.weights,
+                          a.w_dtype};
+    const int chunk = max(1, min(kRouteTokens, kRouteElems / a.experts));
+    const int t0 = blockIdx.x * chunk;
+    block_route<256>(rs, src, t0, min(chunk, a.tokens - t0), a.experts, ids, true);
 }
 
 void launch_route_topk(const RouteArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((a.tokens + 3) / 4)), dim3(256), 0, stream, a);
+    const int chunk = std::max(1, std::min(kRouteTokens, kRouteElems / a.experts));
+    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((a.tokens + chunk - 1) / chunk)), dim3(256), 0, stream, a);
+}
+
+// ------------------------------------------------------------- decode prep
+
+// Decode preparation, once per call: workgroup 0 routes (or loads and
+// validates the caller's ids) and records the expert grouping -- the
+// ascending active experts and a pair bitmask per active expert -- that both
+// decode kernels read; the other workgroups quantize the activation rows to
+// FP8 (128-groups or one scale per row).  Invalid ids are left out of every
+// mask (zero contribution) and raise kBadExpertId.
+__global__ __launch_bounds__(256) void moe_prep_kernel(PrepArgs a) {
+    if (blockIdx.x > 0) {
+        if (a.quant.group == 128) quantize_unit128(a.quant, (int64_t)(blockIdx.x - 1) * 16 + threadIdx.x / 16);
+        else quantize_row(a.quant, blockIdx.x - 1);
+        return;
+    }
+    __shared__ RouteScratch rs;
+    __shared__ int16_t sid[kMaxDecodePairs];
+    __shared__ int flag[kMaxExperts];
+    __shared__ int aidx[kMaxExperts];
+    __shared__ uint32_t mask[kMaxExperts][kMaxDecodePairs / 32];
+    __shared__ int num_active;
+    const int P = a.pairs, E = a.experts, words = (P + 31) / 32;
+    const RouteSource& src = a.route;
+    for (int e = threadIdx.x; e < E; e += 256) flag[e] = 0;
+    for (int i = threadIdx.x; i < E * (kMaxDecodePairs / 32); i += 256) (&mask[0][0])[i] = 0;
+    if (src.logits) {
+        const int tokens = P / src.top_k;
+        const int chunk = max(1, min(kRouteTokens, kRouteElems / E));
+        for (int t0 = 0; t0 < tokens; t0 += chunk)
+            block_route<256>(rs, src, t0, min(chunk, tokens - t0), E, sid + t0 * src.top_k, true);
+        // NaN logits leave slots unranked: keep every id used below in range
+        for (int p = threadIdx.x; p < P; p += 256) {
+            if (sid[p] < 0 || sid[p] >= E) {
+                raise_status(a.status, kNonFinite);
+                sid[p] = -1;
+            }
+        }
+    } else {
+        for (int p = threadIdx.x; p < P; p += 256) {
+            const int64_t id = load_id(src.ids, p, src.ids_dtype);
+            const bool ok = id >= 0 && id < E;
+            if (!ok) raise_status(a.status, kBadExpertId);
+            sid[p] = ok ? (int16_t)id : (int16_t)-1;
+        }
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += 256)
+        if (sid[p] >= 0) flag[sid[p]] = 1;
+    __syncthreads();
+    if (threadIdx.x < kWave) {  // ascending active list by ballots
+        const int lane = threadIdx.x;
+        int base = 0;
+        for (int c = 0; c < E; c += kWave) {
+            const int e = c + lane;
+            const bool on = e < E && flag[e];
+            const uint64_t bits = __ballot(on);
+            if (on) {
+                const int ai = base + __popcll(bits & ((1ull << lane) - 1));
+                aidx[e] = ai;
+                a.grouping->expert[ai] = e;
+            }
+            base += __popcll(bits);
+        }
+        if (lane == 0) {
+            num_active = base;
+            a.grouping->num_active = base;
+        }
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += 256)
+        if (sid[p] >= 0) atomicOr(&mask[aidx[sid[p]]][p / 32], 1u << (p % 32));
+    __syncthreads();
+    for (int i = threadIdx.x; i < num_active * words; i += 256)
+        a.grouping->mask[i / words][i % words] = mask[i / words][i % words];
+}
+
+void launch_moe_prep(const PrepArgs& a, hipStream_t stream) {
+    const int qblocks = a.quant.x ? quantize_blocks(a.quant) : 0;
+    hipLaunchKernelGGL(moe_prep_kernel, dim3(1 + qblocks), dim3(256), 0, stream, a);
 }
 
 // -------------------------------------------------------------- permutation

@@ -60,9 +60,13 @@ _SIGNATURES = {
                               _P, _I, _L, _P, ctypes.c_size_t, _P, _P], _I),
     "dmoe_fp8_moe_pairs": ([ctypes.POINTER(Fp8Bank), _P, _I, _L, _I, _I, _P, _I, _P, _I, _I, _I,
                             _I, _P, _P, ctypes.c_size_t, _P, _P], _I),
-    "dmoe_fp8_gate_up": ([ctypes.POINTER(Fp8Bank), _P, _I, _L, _I, _I, _P, _I, _I, _I, _I, _P, _P, _P,
+    "dmoe_fp8_prepare": ([ctypes.POINTER(Fp8Bank), _P, _I, _L, _I, _I, _P, _I, _I, _I, _P,
                           ctypes.c_size_t, _P, _P], _I),
-    "dmoe_fp8_down": ([ctypes.POINTER(Fp8Bank), _P, _P, _P, _I, _P, _I, _I, _I, _P, _I, _L, _P, _P, _P], _I),
+    "dmoe_fp8_gate_up": ([ctypes.POINTER(Fp8Bank), _I, _I, _I, _I, _P, _P, _P, ctypes.c_size_t, _P, _P], _I),
+    "dmoe_fp8_down": ([ctypes.POINTER(Fp8Bank), _P, _P, _P, _I, _I, _I, _P, _I, _L, _P, _P,
+                       ctypes.c_size_t, _P, _P], _I),
+    "dmoe_fp8_moe_layer": ([ctypes.POINTER(Fp8Bank), _P, _I, _L, _I, _P, _L, _I, _I, _P, _P, _I, _I, _I,
+                            _P, _I, _L, _P, ctypes.c_size_t, _P, _P], _I),
     "dmoe_fp8_quantized_pairs": ([ctypes.POINTER(Fp8Bank), _P, _P, _L, _L, _I, _I, _I, _P, _I, _P,
                                   _I, _I, _I, _P, _P, ctypes.c_size_t, _P, _P], _I),
 }

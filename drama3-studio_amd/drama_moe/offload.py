@@ -99,12 +99,13 @@ class HipExpertBackend:
         return value
 
     # -- protocol ----------------------------------------------------------
-    def forward(self, x: Tensor, ids: Tensor, weights: Tensor, staged: StagedExperts) -> Tensor:
+    def forward(self, x: Tensor, ids: Tensor, weights: Tensor, staged: StagedExperts, *,
+                out: Tensor | None = None) -> Tensor:
         self._check(x)
         if x.ndim != 2 or ids.ndim != 2 or ids.shape[0] != x.shape[0] or weights.shape != ids.shape:
             raise ValueError("Expected x [T, H], ids and weights [T, top_k]")
         tokens, top_k = ids.shape
-        out = torch.empty_like(x)
+        out = self._out(x, out)
         if tokens == 0:
             return out
         bank = fp8_bank_struct(staged)
@@ -125,6 +126,39 @@ class HipExpertBackend:
                 _lib.ptr(ws), ws.numel(), _lib.ptr(state.status), stream))
         return out
 
+    def forward_routed(self, x: Tensor, logits: Tensor, top_k: int, staged: StagedExperts, *,
+                       renormalize: bool = True, weights_dtype: torch.dtype | None = None,
+                       out: Tensor | None = None):
+        """Router + routed experts in one call (decode: two kernels, no host
+        sync).  Returns (out [T, H], weights [T, top_k], ids [T, top_k])."""
+        self._check(x)
+        if x.ndim != 2 or logits.ndim != 2 or logits.shape[0] != x.shape[0]:
+            raise ValueError("Expected x [T, H] and router logits [T, E]")
+        if logits.dtype != torch.float32 or logits.stride(-1) != 1:
+            logits = logits.float().contiguous()
+        tokens = x.shape[0]
+        if tokens * top_k > DECODE_PAIRS:
+            from .router import route_topk
+
+            weights, ids = route_topk(logits, top_k, renormalize=renormalize,
+                                      dtype=weights_dtype or x.dtype)
+            return self.forward(x, ids, weights, staged, out=out), weights, ids
+        out = self._out(x, out)
+        bank = fp8_bank_struct(staged)
+        self._validate(x, staged)
+        ids = torch.empty((tokens, top_k), dtype=torch.int64, device=x.device)
+        weights = torch.empty((tokens, top_k), dtype=weights_dtype or x.dtype, device=x.device)
+        state = device_state(_device_of(x))
+        lib = _lib.library()
+        ws = state.workspace_for(lib.dmoe_fp8_workspace_bytes(bank, tokens * top_k))
+        _lib.check(lib.dmoe_fp8_moe_layer(
+            bank, _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), tokens, _lib.ptr(logits),
+            logits.stride(0), top_k, int(renormalize), _lib.ptr(ids), _lib.ptr(weights),
+            _lib.dtype_code(weights.dtype), self._group(x), self._gu(x), _lib.ptr(out),
+            _lib.dtype_code(out.dtype), out.stride(0), _lib.ptr(ws), ws.numel(),
+            _lib.ptr(state.status), _lib.stream_handle(x.device)))
+        return out, weights, ids
+
     def forward_pairs(self, x: Tensor, ids: Tensor, weights: Tensor, staged: StagedExperts) -> Tensor:
         """Weighted [pairs, hidden] fp32 contributions, before summing."""
         self._check(x)
@@ -137,6 +171,14 @@ class HipExpertBackend:
         return self.forward_pairs(x, ids, weights, staged)
 
     # -- internals ---------------------------------------------------------
+    @staticmethod
+    def _out(x: Tensor, out: Tensor | None) -> Tensor:
+        if out is None:
+            return torch.empty_like(x)
+        if out.shape != x.shape or out.dtype != x.dtype or out.device != x.device or out.stride(-1) != 1:
+            raise ValueError("out must match x in shape, dtype and device, with contiguous rows")
+        return out
+
     def _group(self, x: Tensor) -> int:
         return 128 if self.x_group == 128 else x.shape[-1]
 

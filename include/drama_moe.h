@@ -149,31 +149,59 @@ DMOE_API int dmoe_fp8_quantized_pairs(const DmoeFp8Bank* bank, const uint8_t* xq
                                       int gu_dtype, float* out, void* workspace,
                                       size_t workspace_bytes, int* status, void* stream);
 
-/* Decode stage 1 (gate/up): for the route pairs (pair p reads activation row
- * p / row_div), gate/up = block-scaled FP8 projection of the FP8-quantized
- * activation, rounded through gu_dtype, h = silu(gate) * up, then FP8
- * 128-group quantization into hidden_q [pairs, I] E4M3 and hidden_scales
- * [pairs, I/128] fp32.  Replaces the first decode_gemm launch plus
- * quantize_groups(silu_mul_quant_kernel) of fp8_decode.quantized_pairs
- * (fp8_decode.py:130-146) and runtime.cpp:184-225 of the CPU executor. */
-DMOE_API int dmoe_fp8_gate_up(const DmoeFp8Bank* bank, const void* x, int x_dtype,
+/* The decode path as three single-launch stages sharing one workspace (from
+ * dmoe_fp8_workspace_bytes for the same bank and pair count); calls after
+ * dmoe_fp8_prepare pass the same pairs, row_div and x_group.
+ *
+ * Stage 0 (prepare): validates the route ids of the pairs (pair p reads
+ * activation row p / row_div), records their expert grouping -- the ascending
+ * active experts and each one's pairs, the decode analogue of moe_align -- and
+ * quantizes the activation rows to FP8 in x_group-column groups, all into the
+ * workspace.  Replaces quantize_groups(x) of fp8_decode.quantized_pairs
+ * (fp8_decode.py:117, 136) and the route readback / expert grouping of
+ * offload.py:1202-1210. */
+DMOE_API int dmoe_fp8_prepare(const DmoeFp8Bank* bank, const void* x, int x_dtype,
                               int64_t x_row_stride, int rows, int row_div, const void* ids,
-                              int ids_dtype, int pairs, int x_group, int gu_dtype,
-                              uint8_t* hidden_q, float* hidden_scales, void* workspace,
+                              int ids_dtype, int pairs, int x_group, void* workspace,
                               size_t workspace_bytes, int* status, void* stream);
 
-/* Decode stage 2 (down + combine): partial_p = route_weight_p * (block-scaled
- * FP8 down projection of hidden p).  With out_pairs == NULL the partials of
- * each token (pairs = tokens * top_k, token-major) are summed in router slot
- * order in fp32 and stored to out [tokens, H] in out_dtype; otherwise the
- * ordered fp32 partials go to out_pairs [pairs, H].  Replaces the second
- * decode_gemm launch (ROUTE_WEIGHT) and down.sum(0) of fp8_decode.py:54-55,
- * 119, and the combine of offload.py:1242-1244. */
+/* Stage 1 (gate/up): gate/up = block-scaled FP8 projection of the prepared
+ * activation for every pair, rounded through gu_dtype, h = silu(gate) * up,
+ * then FP8 128-group quantization into hidden_q [pairs, I] E4M3 and
+ * hidden_scales [pairs, I/128] fp32.  Replaces the first decode_gemm launch
+ * plus quantize_groups(silu_mul_quant_kernel) of fp8_decode.quantized_pairs
+ * (fp8_decode.py:130-146) and runtime.cpp:184-225 of the CPU executor. */
+DMOE_API int dmoe_fp8_gate_up(const DmoeFp8Bank* bank, int row_div, int pairs, int x_group,
+                              int gu_dtype, uint8_t* hidden_q, float* hidden_scales,
+                              void* workspace, size_t workspace_bytes, int* status, void* stream);
+
+/* Stage 2 (down + combine): partial_p = route_weight_p * (block-scaled FP8
+ * down projection of hidden p) for the prepared pairs.  With out_pairs == NULL
+ * the partials of each token (pairs = tokens * top_k, token-major) are summed
+ * in router slot order in fp32 and stored to out [tokens, H] in out_dtype;
+ * otherwise the ordered fp32 partials go to out_pairs [pairs, H].  Replaces
+ * the second decode_gemm launch (ROUTE_WEIGHT) and down.sum(0) of
+ * fp8_decode.py:54-55, 119, and the combine of offload.py:1242-1244. */
 DMOE_API int dmoe_fp8_down(const DmoeFp8Bank* bank, const uint8_t* hidden_q,
-                           const float* hidden_scales, const void* ids, int ids_dtype,
-                           const void* weights, int weights_dtype, int pairs, int top_k, void* out,
-                           int out_dtype, int64_t out_row_stride, float* out_pairs, int* status,
+                           const float* hidden_scales, const void* weights, int weights_dtype,
+                           int pairs, int top_k, void* out, int out_dtype, int64_t out_row_stride,
+                           float* out_pairs, void* workspace, size_t workspace_bytes, int* status,
                            void* stream);
+
+/* Whole MoE routed-expert layer for decode: router softmax/top-k of logits
+ * [tokens, experts] fp32 (as dmoe_route_topk; the routing is also written to
+ * ids_out [tokens, top_k] int64 and weights_out in weights_dtype), then the
+ * routed experts and slot-order combine as dmoe_fp8_moe_forward, in two
+ * kernel launches and no host sync, for hipGraph-captured decode steps.
+ * Replaces the router of backbone_graph.py:317-323 followed by the expert
+ * call of backbone_graph.py:550-554 / ExpertOffloadManager.forward
+ * (offload.py:1016). */
+DMOE_API int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype,
+                                int64_t x_row_stride, int tokens, const float* logits,
+                                int64_t logits_row_stride, int top_k, int renormalize,
+                                int64_t* ids_out, void* weights_out, int weights_dtype, int x_group,
+                                int gu_dtype, void* out, int out_dtype, int64_t out_row_stride,
+                                void* workspace, size_t workspace_bytes, int* status, void* stream);
 
 #ifdef __cplusplus
 }

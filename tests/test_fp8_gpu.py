@@ -392,3 +392,105 @@ def test_full_size_layer_against_oracle(cuda, tokens):
                                                     torch.bfloat16, 20261201 + 2, bank_on_device=True)
     out = HipExpertBackend().forward(x, ids, weights, staged)
     assert rel_inf(out.float().cpu().numpy(), expected) < TOL
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 16])
+@pytest.mark.parametrize("layout", ["block", "channel"])
+def test_fused_router_layer_matches_oracle(cuda, tokens, layout):
+    """Whole-layer entry: router logits -> top-8 -> experts -> slot-order combine."""
+    print_case("fused layer", tokens, layout)
+    g = torch.Generator().manual_seed(4242 + tokens)
+    staged = random_fp8_bank(32, 2048, 768, layout=layout, generator=g)
+    x = torch.randn(tokens, 2048, generator=g).bfloat16()
+    logits = torch.randn(tokens, 32, generator=g)
+    out, weights, ids = HipExpertBackend().forward_routed(x.to(cuda), logits.to(cuda), 8, to_device(staged, cuda))
+    eids, ew = orc.route_topk(logits.numpy(), 8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), eids)
+    ref_w = torch.from_numpy(ew).bfloat16()
+    assert torch.max((weights.cpu().float() - ref_w.float()).abs() / ref_w.float()).item() <= 2 ** -7
+    b13, b2 = oracle_banks(staged)
+    expected = orc.fp8_moe_forward(b13, b2, x.float().numpy(), eids, weights.float().cpu().numpy())
+    assert rel_inf(out.float().cpu().numpy(), expected) < TOL
+
+
+def test_fused_router_layer_in_hipgraph(cuda):
+    print_case("fused layer hipgraph")
+    staged = to_device(random_fp8_bank(32, 2048, 768, generator=torch.Generator().manual_seed(17)), cuda)
+    backend = HipExpertBackend()
+    x = torch.randn(1, 2048, device=cuda).bfloat16()
+    logits = torch.randn(1, 32, device=cuda)
+    out = torch.empty_like(x)
+    stream = torch.cuda.Stream(cuda)
+    stream.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(stream):
+        backend.forward_routed(x, logits, 8, staged, out=out)
+    torch.cuda.current_stream(cuda).wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        _, w_g, i_g = backend.forward_routed(x, logits, 8, staged, out=out)
+    for step in range(4):
+        logits.copy_(torch.randn(1, 32, device=cuda))
+        x.copy_(torch.randn(1, 2048, device=cuda).bfloat16())
+        expected, w_e, i_e = backend.forward_routed(x, logits, 8, staged)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(i_g, i_e) and torch.equal(w_g, w_e), step
+        assert torch.equal(out, expected), step
+
+
+@pytest.mark.parametrize("tokens", [1, 16, 32])
+def test_three_stage_entry_points_match_oracle_and_fused_path(cuda, tokens):
+    """prepare -> gate_up -> down (one launch each) against the oracle, and
+    bit-identical to the fused call (same arithmetic, hidden quantized in the
+    gate/up stage instead of the down kernel for small calls)."""
+    print_case("three stages", tokens)
+    staged, x, ids, weights, expected = _layer_case(cuda, 32, 2048, 768, tokens, 8, "block", torch.bfloat16,
+                                                    6060 + tokens)
+    staged_out = fp8_decode.staged_forward(x, ids, weights, staged)
+    assert rel_inf(staged_out.float().cpu().numpy(), expected) < TOL
+    fused = HipExpertBackend().forward(x, ids, weights, staged)
+    assert torch.equal(staged_out, fused)
+    partials = fp8_decode.staged_forward(x, ids, weights, staged, pairs_out=True)
+    b13, b2 = oracle_banks(staged)
+    xh, ih, wh = x.float().cpu().numpy(), ids.cpu().numpy(), weights.float().cpu().numpy()
+    ref_pairs = np.concatenate([orc.fp8_expert_pairs(b13, b2, xh[t], ih[t], wh[t]) for t in range(tokens)])
+    assert rel_inf(partials.cpu().numpy(), ref_pairs) < TOL
+
+
+def test_stage_hidden_activation_is_valid_fp8_quantization(cuda):
+    """The FP8 hidden of stage 1 dequantizes to silu(gate) * up of a float64
+    restatement of the block-scaled gate/up projection, within one E4M3 code
+    step of each value (a flip of one code at a rounding boundary allowed)."""
+    print_case("stage hidden")
+    staged, x, ids, weights, _ = _layer_case(cuda, 8, 256, 256, 2, 4, "block", torch.float32, 515)
+    pairs, inter, hidden = 8, 256, 256
+    hq = torch.empty(pairs, inter, dtype=torch.uint8, device=cuda)
+    hs = torch.empty(pairs, inter // 128, device=cuda)
+    fp8_decode.staged_forward(x, ids, weights, staged, hidden=(hq, hs))
+    xq, xs = orc.quantize_fp8(x.cpu().numpy(), 128)
+    xd = (orc.fp8_decode(xq).reshape(2, -1, 128) * xs[:, :, None]).reshape(2, hidden).astype(np.float64)
+    w = orc.fp8_decode(staged.w13_weight.view(torch.uint8).cpu().numpy()).astype(np.float64)
+    s = np.repeat(np.repeat(staged.w13_scale_inv.cpu().numpy(), 128, axis=1), 128, axis=2)
+    flat = ids.cpu().numpy().reshape(-1)
+    gu = np.stack([(w[e] * s[e]) @ xd[p // 4] for p, e in enumerate(flat)])
+    h = gu[:, :inter] / (1 + np.exp(-gu[:, :inter])) * gu[:, inter:]
+    scale = np.repeat(hs.cpu().numpy(), 128, axis=1).astype(np.float64)
+    deq = orc.fp8_decode(hq.cpu().numpy()) * scale
+    q = np.abs(h) / scale
+    spacing = np.exp2(np.maximum(np.floor(np.log2(np.maximum(q, 1e-30))), -6) - 3) * scale
+    assert np.all(np.abs(deq - h) <= spacing * 1.001)
+    amax = np.abs(h).reshape(pairs, -1, 128).max(axis=2)
+    np.testing.assert_allclose(hs.cpu().numpy(), amax / 448, rtol=2e-4)  # fp32 vs float64 sums
+
+
+def test_stage_down_requires_prepared_workspace_geometry(cuda):
+    print_case("stage down errors")
+    staged = to_device(random_fp8_bank(4, 256, 256, generator=torch.Generator().manual_seed(3)), cuda)
+    x = torch.randn(1, 256, device=cuda)
+    ids = torch.zeros(1, 2, dtype=torch.int64, device=cuda)
+    w = torch.ones(1, 2, device=cuda)
+    with pytest.raises(ValueError, match="256 route pairs"):
+        fp8_decode.staged_forward(x.expand(200, 256).contiguous(), ids.expand(200, 2).contiguous(),
+                                  w.expand(200, 2).contiguous(), staged)
