@@ -145,8 +145,7 @@ struct Activations {
 
 void check_activations(const BankGeom& g, const Activations& a, int pairs) {
     require(pairs >= 1, "at least one route pair is required");
-    require(pairs <= dmoe::kMaxDecodePairs,
-            "more than 256 route pairs per call: split the rows (the decode kernels take <= 256 pairs)");
+    require(pairs <= dmoe::kMaxPermutePairs, "more than 16384 route pairs per call: split the rows");
     require(a.row_div >= 1 && (int64_t)(pairs - 1) / a.row_div < a.rows, "pairs read past the activation rows");
     require(a.x_group == 128 || a.x_group == g.H, "activation group must be 128 or the hidden size");
     if (a.xq) {
@@ -269,8 +268,8 @@ void check_output(const BankGeom& g, void* out, int out_dtype, int64_t out_row_s
     require(top_k >= 1 && pairs % top_k == 0, "pairs must be tokens * top_k");
 }
 
-// The three launches of a whole grouped FP8 call.
-void fp8_grouped(const BankGeom& g, Activations a, const dmoe::RouteSource& route, const void* weights,
+// The three launches of a whole decode FP8 call (<= 256 pairs).
+void fp8_decode_call(const BankGeom& g, Activations a, const dmoe::RouteSource& route, const void* weights,
                  int weights_dtype, int pairs, int top_k, int gu_dtype, void* out, int out_dtype,
                  int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes, int* status,
                  hipStream_t stream) {
@@ -280,6 +279,147 @@ void fp8_grouped(const BankGeom& g, Activations a, const dmoe::RouteSource& rout
     launch_gate_up(g, a, pairs, gu_dtype, ws.hq, ws.hs, ws, status, stream, !in_down);
     launch_down(g, ws, ws.hq, ws.hs, weights, weights_dtype, pairs, top_k, out, out_dtype, out_row_stride,
                 out_pairs, status, stream, in_down ? ws.h32 : nullptr);
+}
+
+// Workspace of the grouped (prefill) path: the moe_align map, FP8 activations
+// (one row per pair at most), the FP8 hidden in sorted order and the fp32
+// partials of every pair.  It starts with the same reserved counter region as
+// the decode layout and never writes it, so one workspace serves both paths
+// and the decode arrival counters stay zero.
+struct PrefillWorkspace {
+    int32_t* order;
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* tile_expert;
+    int32_t* tile_m0;
+    uint8_t* xq;
+    float* xs;
+    uint8_t* hq;
+    float* hs;
+    float* partial;
+};
+
+size_t prefill_workspace_layout(int pairs, int experts, int H, int I, char* base, PrefillWorkspace* ws) {
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        const size_t o = off;
+        off = align256(off + n);
+        return base ? base + o : nullptr;
+    };
+    const int tiles = dmoe::max_block_tiles(pairs, experts, dmoe::kGroupM);
+    take(kCounterBytes);  // decode arrival counters: reserved, untouched here
+    char* order = take((size_t)pairs * 4);
+    char* counts = take((size_t)experts * 4);
+    char* offsets = take((size_t)(experts + 1) * 4);
+    char* tile_expert = take((size_t)tiles * 4);
+    char* tile_m0 = take((size_t)tiles * 4);
+    char* xq = take((size_t)pairs * H);
+    char* xs = take((size_t)pairs * (H / 128) * 4);
+    char* hq = take((size_t)pairs * I);
+    char* hs = take((size_t)pairs * (I / 128) * 4);
+    char* partial = take((size_t)pairs * H * 4);
+    if (ws) {
+        ws->order = reinterpret_cast<int32_t*>(order);
+        ws->counts = reinterpret_cast<int32_t*>(counts);
+        ws->offsets = reinterpret_cast<int32_t*>(offsets);
+        ws->tile_expert = reinterpret_cast<int32_t*>(tile_expert);
+        ws->tile_m0 = reinterpret_cast<int32_t*>(tile_m0);
+        ws->xq = reinterpret_cast<uint8_t*>(xq);
+        ws->xs = reinterpret_cast<float*>(xs);
+        ws->hq = reinterpret_cast<uint8_t*>(hq);
+        ws->hs = reinterpret_cast<float*>(hs);
+        ws->partial = reinterpret_cast<float*>(partial);
+    }
+    return off;
+}
+
+size_t workspace_bytes_for(const BankGeom& g, int pairs) {
+    if (pairs <= dmoe::kMaxDecodePairs) return fp8_workspace_layout(pairs, g.H, g.I, nullptr, nullptr);
+    return prefill_workspace_layout(pairs, g.experts, g.H, g.I, nullptr, nullptr);
+}
+
+// Grouped (prefill) call: permutation + moe_align tile map, activation
+// quantization, grouped gate/up GEMM (+ SiLU, FP8 hidden), grouped down GEMM
+// (* route weight, fp32 partials), slot-order combine.  Five launches.
+void fp8_prefill_call(const BankGeom& g, Activations a, const void* ids, int ids_dtype, const void* weights,
+                      int weights_dtype, int pairs, int top_k, int gu_dtype, void* out, int out_dtype,
+                      int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes,
+                      int* status, hipStream_t stream) {
+    const size_t need = prefill_workspace_layout(pairs, g.experts, g.H, g.I, nullptr, nullptr);
+    require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+    require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+    PrefillWorkspace ws{};
+    prefill_workspace_layout(pairs, g.experts, g.H, g.I, static_cast<char*>(workspace), &ws);
+    const int tiles = dmoe::max_block_tiles(pairs, g.experts, dmoe::kGroupM);
+
+    dmoe::PermuteArgs pa{ids, ids_dtype, pairs, g.experts, ws.order, ws.counts, ws.offsets, status,
+                         dmoe::kGroupM, tiles, ws.tile_expert, ws.tile_m0};
+    dmoe::launch_permute(pa, stream);
+    if (a.xq == nullptr) {
+        const int rows = (pairs - 1) / a.row_div + 1;
+        const dmoe::QuantArgs qa{a.x, a.x_dtype, a.x_row_stride, rows, g.H, a.x_group, 0, ws.xq, ws.xs, status};
+        dmoe::launch_fp8_quantize(qa, stream);
+        a.xq = ws.xq;
+        a.xs = ws.xs;
+        a.xq_row_stride = g.H;
+        a.xs_row_stride = g.H / a.x_group;
+    }
+    dmoe::GroupedGateUpArgs ga{};
+    ga.w13 = g.w13;
+    ga.order = ws.order;
+    ga.offsets = ws.offsets;
+    ga.tile_expert = ws.tile_expert;
+    ga.tile_m0 = ws.tile_m0;
+    ga.max_tiles = tiles;
+    ga.xq = a.xq;
+    ga.xs = a.xs;
+    ga.xq_row_stride = a.xq_row_stride;
+    ga.xs_row_stride = a.xs_row_stride;
+    ga.x_group = a.x_group;
+    ga.row_div = a.row_div;
+    ga.gu_dtype = gu_dtype;
+    ga.hq = ws.hq;
+    ga.hs = ws.hs;
+    ga.status = status;
+    dmoe::launch_fp8_grouped_gateup(ga, stream);
+
+    dmoe::GroupedDownArgs da{};
+    da.w2 = g.w2;
+    da.order = ws.order;
+    da.offsets = ws.offsets;
+    da.tile_expert = ws.tile_expert;
+    da.tile_m0 = ws.tile_m0;
+    da.max_tiles = tiles;
+    da.hq = ws.hq;
+    da.hs = ws.hs;
+    da.weights = weights;
+    da.w_dtype = weights_dtype;
+    da.partial = out_pairs ? out_pairs : ws.partial;
+    da.partial_row_stride = g.H;
+    da.status = status;
+    dmoe::launch_fp8_grouped_down(da, stream);
+    if (out_pairs) {  // forward_pairs: rows of invalid pairs are zero, as in the decode kernels
+        const dmoe::CombineArgs za{out_pairs, g.H, ids, ids_dtype, g.experts, pairs, 1, g.H, nullptr, DMOE_F32, 0};
+        dmoe::launch_zero_invalid_rows(za, stream);
+        return;
+    }
+    const dmoe::CombineArgs ca{ws.partial, g.H, ids, ids_dtype, g.experts, pairs / top_k, top_k, g.H,
+                               out, out_dtype, out_row_stride};
+    dmoe::launch_combine(ca, stream);
+}
+
+// Whole-call dispatch by pair count: decode kernels up to 256 pairs, grouped
+// GEMMs above.
+void fp8_call(const BankGeom& g, Activations a, const dmoe::RouteSource& route, const void* ids, int ids_dtype,
+              const void* weights, int weights_dtype, int pairs, int top_k, int gu_dtype, void* out, int out_dtype,
+              int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes, int* status,
+              hipStream_t stream) {
+    if (pairs <= dmoe::kMaxDecodePairs)
+        fp8_decode_call(g, a, route, weights, weights_dtype, pairs, top_k, gu_dtype, out, out_dtype, out_row_stride,
+                        out_pairs, workspace, workspace_bytes, status, stream);
+    else
+        fp8_prefill_call(g, a, ids, ids_dtype, weights, weights_dtype, pairs, top_k, gu_dtype, out, out_dtype,
+                         out_row_stride, out_pairs, workspace, workspace_bytes, status, stream);
 }
 
 }  // namespace
@@ -347,14 +487,16 @@ int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t
         require(is_id_dtype(ids_dtype), "route ids must be int32 or int64");
         require(experts >= 1 && experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
         require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 16384]");
-        dmoe::PermuteArgs a{ids, ids_dtype, pairs, experts, order, counts, offsets, status};
+        dmoe::PermuteArgs a{ids, ids_dtype, pairs, experts, order, counts, offsets, status, 0, 0, nullptr, nullptr};
         dmoe::launch_permute(a, as_stream(stream));
     });
 }
 
 size_t dmoe_fp8_workspace_bytes(const DmoeFp8Bank* bank, int pairs) {
-    if (!bank || pairs < 1) return 0;
-    return fp8_workspace_layout(pairs, bank->w13.k, bank->w13.n / 2, nullptr, nullptr);
+    if (!bank || pairs < 1 || pairs > dmoe::kMaxPermutePairs) return 0;
+    if (pairs <= dmoe::kMaxDecodePairs) return fp8_workspace_layout(pairs, bank->w13.k, bank->w13.n / 2, nullptr, nullptr);
+    const int experts = std::max(1, std::min(bank->experts, dmoe::kMaxExperts));
+    return prefill_workspace_layout(pairs, experts, bank->w13.k, bank->w13.n / 2, nullptr, nullptr);
 }
 
 int dmoe_fp8_moe_forward(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride,
@@ -371,8 +513,8 @@ int dmoe_fp8_moe_forward(const DmoeFp8Bank* bank, const void* x, int x_dtype, in
         check_routes(ids, ids_dtype, weights, weights_dtype);
         check_gu_dtype(gu_dtype);
         check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
-        fp8_grouped(g, a, ids_source(ids, ids_dtype), weights, weights_dtype, pairs, top_k, gu_dtype, out,
-                    out_dtype, out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
+        fp8_call(g, a, ids_source(ids, ids_dtype), ids, ids_dtype, weights, weights_dtype, pairs, top_k, gu_dtype,
+                 out, out_dtype, out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
 
@@ -387,8 +529,8 @@ int dmoe_fp8_moe_pairs(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
         check_activations(g, a, pairs);
         check_routes(ids, ids_dtype, weights, weights_dtype);
         check_gu_dtype(gu_dtype);
-        fp8_grouped(g, a, ids_source(ids, ids_dtype), weights, weights_dtype, pairs, 1, gu_dtype, nullptr,
-                    DMOE_F32, 0, out, workspace, workspace_bytes, status, as_stream(stream));
+        fp8_call(g, a, ids_source(ids, ids_dtype), ids, ids_dtype, weights, weights_dtype, pairs, 1, gu_dtype,
+                 nullptr, DMOE_F32, 0, out, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
 
@@ -405,8 +547,8 @@ int dmoe_fp8_quantized_pairs(const DmoeFp8Bank* bank, const uint8_t* xq, const f
         check_activations(g, a, pairs);
         check_routes(ids, ids_dtype, weights, weights_dtype);
         check_gu_dtype(gu_dtype);
-        fp8_grouped(g, a, ids_source(ids, ids_dtype), weights, weights_dtype, pairs, 1, gu_dtype, nullptr,
-                    DMOE_F32, 0, out, workspace, workspace_bytes, status, as_stream(stream));
+        fp8_call(g, a, ids_source(ids, ids_dtype), ids, ids_dtype, weights, weights_dtype, pairs, 1, gu_dtype,
+                 nullptr, DMOE_F32, 0, out, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
 
@@ -416,6 +558,7 @@ int dmoe_fp8_prepare(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_
     return checked([&] {
         const BankGeom g = check_bank(bank);
         Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, rows, row_div, x_group};
+        require(pairs >= 1 && pairs <= dmoe::kMaxDecodePairs, "pair count outside [1, 256]");
         check_activations(g, a, pairs);
         require(ids != nullptr && is_id_dtype(ids_dtype), "route ids must be int32 or int64");
         const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
@@ -475,8 +618,13 @@ int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
         check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
         const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
                                       ids_out, weights_out, weights_dtype};
-        fp8_grouped(g, a, route, weights_out, weights_dtype, pairs, top_k, gu_dtype, out, out_dtype,
-                    out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
+        if (pairs > dmoe::kMaxDecodePairs) {  // the prefill path routes in its own launch first
+            const dmoe::RouteArgs ra{logits, logits_row_stride, tokens, g.experts, top_k, renormalize != 0,
+                                     ids_out, weights_out, weights_dtype};
+            dmoe::launch_route_topk(ra, as_stream(stream));
+        }
+        fp8_call(g, a, route, ids_out, DMOE_I64, weights_out, weights_dtype, pairs, top_k, gu_dtype, out, out_dtype,
+                 out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
 

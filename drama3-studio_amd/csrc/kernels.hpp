@@ -125,6 +125,68 @@ struct PermuteArgs {
     int32_t* counts;        // [experts]
     int32_t* offsets;       // [experts + 1]
     int* status;
+    // Optional moe_align tile map (tile_expert == nullptr: none): the sorted
+    // pairs of each expert cut into block_m-row tiles, expert-major; tile i
+    // covers sorted positions [tile_m0[i], min(tile_m0[i] + block_m,
+    // offsets[e + 1])) of expert e = tile_expert[i]; -1 past the last tile.
+    int block_m;
+    int max_tiles;
+    int32_t* tile_expert;
+    int32_t* tile_m0;
+};
+
+// Tile-map capacity for `pairs` route pairs over `experts` experts.
+inline int max_block_tiles(int pairs, int experts, int block_m) { return (pairs + block_m - 1) / block_m + experts; }
+
+// Grouped (prefill) FP8 GEMMs over the moe_align tile map: 64 sorted pairs
+// per tile.  Gate/up writes the FP8 hidden of every sorted position; down
+// writes route-weighted fp32 partials by original pair index.
+constexpr int kGroupM = 64;
+
+struct GroupedGateUpArgs {
+    Fp8Proj w13;
+    const int32_t* order;
+    const int32_t* offsets;
+    const int32_t* tile_expert;
+    const int32_t* tile_m0;
+    int max_tiles;
+    const uint8_t* xq;      // [rows, H] FP8 activations, row = pair / row_div
+    const float* xs;
+    int64_t xq_row_stride, xs_row_stride;
+    int x_group;            // 128 or H
+    int row_div;
+    int gu_dtype;
+    uint8_t* hq;            // [pairs (sorted position), I]
+    float* hs;              // [pairs, I / 128]
+    int* status;
+};
+
+struct GroupedDownArgs {
+    Fp8Proj w2;
+    const int32_t* order;
+    const int32_t* offsets;
+    const int32_t* tile_expert;
+    const int32_t* tile_m0;
+    int max_tiles;
+    const uint8_t* hq;      // [pairs (sorted position), I]
+    const float* hs;
+    const void* weights;    // route weight of each original pair
+    int w_dtype;
+    float* partial;         // [pairs (original index), H] fp32
+    int64_t partial_row_stride;
+    int* status;
+};
+
+struct CombineArgs {
+    const float* partial;   // [tokens * top_k, H]
+    int64_t partial_row_stride;
+    const void* ids;        // validity of every pair
+    int ids_dtype;
+    int experts;
+    int tokens, top_k, H;
+    void* out;
+    int out_dtype;
+    int64_t out_row_stride;
 };
 
 struct PrepArgs {
@@ -143,5 +205,9 @@ void launch_fp8_quantize(const QuantArgs& a, hipStream_t stream);
 void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stream);
 void launch_route_topk(const RouteArgs& a, hipStream_t stream);
 void launch_permute(const PermuteArgs& a, hipStream_t stream);
+void launch_fp8_grouped_gateup(const GroupedGateUpArgs& a, hipStream_t stream);
+void launch_fp8_grouped_down(const GroupedDownArgs& a, hipStream_t stream);
+void launch_combine(const CombineArgs& a, hipStream_t stream);
+void launch_zero_invalid_rows(const CombineArgs& a, hipStream_t stream);
 
 }  // namespace dmoe

@@ -73,18 +73,27 @@ __device__ __forceinline__ void argmax_step(float& bv, int& bi) {
 }
 // Router for a chunk of tokens by a whole workgroup, without serial rounds:
 // rank(t, e) = #{e' : l[e'] > l[e] or (l[e'] == l[e] and e' < e)}; the
-// experts of rank < k are the winners, rank = router slot.  Softmax max and
+// experts of rank < k are the winners, rank = router slot.  Each logit gets a
+// unique 64-bit key (order-preserving logit bits, then the inverted expert
+// index), so the rank is a branch-free count of larger keys.  Softmax max and
 // sum are workgroup reductions; weights = exp(l - max) / sum of the winners,
 // renormalised by their slot-order sum.  Reference: backbone_graph.py:317-323.
 // Results: ids_lds[t * k + slot] (local token t), and -- when `publish` -- the
 // global ids / weights of token t0 + t.
 struct RouteScratch {
-    float lv[kRouteElems];   // logits of the chunk
-    float ex[kRouteElems];   // exp(l - max)
+    uint64_t key[kRouteElems];  // (ordered logit << 32) | ~expert
+    float lv[kRouteElems];      // logits of the chunk
+    float ex[kRouteElems];      // exp(l - max)
     float red[16][kRouteTokens];
     float pk[kRouteTokens][64];
     int ik[kRouteTokens][64];
 };
+
+// Order-preserving map of a float to uint32 (-0 and +0 compare equal).
+__device__ __forceinline__ uint32_t ordered_bits(float v) {
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
 
 template <int THREADS>
 __device__ void block_route(RouteScratch& rs, const RouteSource& src, int t0, int tcount, int experts,
@@ -94,7 +103,9 @@ __device__ void block_route(RouteScratch& rs, const RouteSource& src, int t0, in
     const int elems = tcount * experts;
     for (int i = threadIdx.x; i < elems; i += THREADS) {
         const int t = i / experts, e = i % experts;
-        rs.lv[i] = src.logits[(int64_t)(t0 + t) * src.logits_row_stride + e];
+        const float l = src.logits[(int64_t)(t0 + t) * src.logits_row_stride + e];
+        rs.lv[i] = l;
+        rs.key[i] = ((uint64_t)ordered_bits(l) << 32) | (uint32_t)~e;
     }
     __syncthreads();
     // per-token max: one wave per token
@@ -106,44 +117,40 @@ __device__ void block_route(RouteScratch& rs, const RouteSource& src, int t0, in
         if (lane == 0) rs.red[0][t] = m;
     }
     __syncthreads();
-    // ranks: TPE threads share one element's comparisons (quad of lanes)
+    // ranks: TPE threads share one element's comparisons (neighbour lanes)
     const int tpe = elems * 4 <= THREADS ? 4 : elems * 2 <= THREADS ? 2 : 1;
     const int sub = threadIdx.x % tpe;
     for (int base = 0; base < elems; base += THREADS / tpe) {
         const int i = base + threadIdx.x / tpe;
         const bool live = i < elems;
         const int t = live ? i / experts : 0, e = live ? i % experts : 0;
-        const float v = live ? rs.lv[i] : 0.0f;
+        const uint64_t mine = live ? rs.key[i] : ~0ull;
         int rank = 0;
         if (live) {
-            // this thread's contiguous share of the row, 16 values per step
-            // (four 16-byte LDS reads in flight)
-            const float* row = rs.lv + t * experts;
+            // this thread's contiguous share of the row, 8 keys per step
+            const uint64_t* row = rs.key + t * experts;
             const int per = (experts + tpe - 1) / tpe;
             const int o0 = sub * per, o1 = min(experts, o0 + per);
             int o = o0;
-            if (((t * experts + o0) & 3) == 0) {
-                for (; o + 16 <= o1; o += 16) {
-                    const v4f q0 = *(const v4f*)(row + o), q1 = *(const v4f*)(row + o + 4);
-                    const v4f q2 = *(const v4f*)(row + o + 8), q3 = *(const v4f*)(row + o + 12);
+            if (((t * experts + o0) & 1) == 0) {
+                for (; o + 8 <= o1; o += 8) {
+                    const v4i q0 = *(const v4i*)(row + o), q1 = *(const v4i*)(row + o + 2);
+                    const v4i q2 = *(const v4i*)(row + o + 4), q3 = *(const v4i*)(row + o + 6);
+                    const v4i q[4] = {q0, q1, q2, q3};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        rank += (q0[j] > v) || (q0[j] == v && o + j < e);
-                        rank += (q1[j] > v) || (q1[j] == v && o + 4 + j < e);
-                        rank += (q2[j] > v) || (q2[j] == v && o + 8 + j < e);
-                        rank += (q3[j] > v) || (q3[j] == v && o + 12 + j < e);
+                        const uint64_t k0 = ((uint64_t)(uint32_t)q[j][1] << 32) | (uint32_t)q[j][0];
+                        const uint64_t k1 = ((uint64_t)(uint32_t)q[j][3] << 32) | (uint32_t)q[j][2];
+                        rank += (int)(k0 > mine) + (int)(k1 > mine);
                     }
                 }
             }
-            for (; o < o1; ++o) {
-                const float w = row[o];
-                rank += (w > v) || (w == v && o < e);
-            }
+            for (; o < o1; ++o) rank += (int)(row[o] > mine);
         }
         if (tpe >= 2) rank += __builtin_bit_cast(int, dpp_f32<kDppXor1>(__builtin_bit_cast(float, rank)));
         if (tpe >= 4) rank += __builtin_bit_cast(int, dpp_f32<kDppXor2>(__builtin_bit_cast(float, rank)));
         if (live && sub == 0) {
-            const float x = expf(v - rs.red[0][t]);
+            const float x = expf(rs.lv[i] - rs.red[0][t]);
             rs.ex[i] = x;
             if (rank < src.top_k) {
                 rs.ik[t][rank] = e;
@@ -405,6 +412,31 @@ __global__ __launch_bounds__(1024) void permute_kernel(PermuteArgs a) {
         a.counts[t] = stop - start;
         if (t == a.experts - 1) a.offsets[a.experts] = total;
     }
+    if (a.tile_expert == nullptr) return;
+    // moe_align tile map: exclusive scan of per-expert tile counts
+    __syncthreads();  // every thread has read wsum
+    const int estart = t < a.experts ? scan[t * parts] : 0;
+    const int ecount = t < a.experts ? (t + 1 < a.experts ? scan[(t + 1) * parts] : total) - estart : 0;
+    const int ntiles = (ecount + a.block_m - 1) / a.block_m;
+    int tincl = ntiles;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int n = __shfl_up(tincl, o, kWave);
+        if (lane >= o) tincl += n;
+    }
+    if (lane == kWave - 1) wsum[wave] = tincl;
+    __syncthreads();
+    int tbase = 0, ttotal = 0;
+    for (int w = 0; w < 16; ++w) {
+        if (w < wave) tbase += wsum[w];
+        ttotal += wsum[w];
+    }
+    const int tstart = tbase + tincl - ntiles;
+    for (int j = 0; j < ntiles; ++j) {
+        a.tile_expert[tstart + j] = t;
+        a.tile_m0[tstart + j] = estart + j * a.block_m;
+    }
+    for (int i = ttotal + t; i < a.max_tiles; i += 1024) a.tile_expert[i] = -1;
 }
 
 void launch_permute(const PermuteArgs& a, hipStream_t stream) {

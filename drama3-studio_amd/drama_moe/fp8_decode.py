@@ -12,7 +12,7 @@ import torch
 
 from . import _lib
 from .formats import StagedExperts, fp8_bank_struct
-from .offload import DECODE_PAIRS, HipExpertBackend, device_state
+from .offload import DECODE_PAIRS, MAX_PAIRS, HipExpertBackend, device_state
 
 
 def forward(kernel, x, ids, weights, staged: StagedExperts):
@@ -26,8 +26,8 @@ def quantized_pairs(kernel, q, scales, ids, weights, staged: StagedExperts, *, d
     ids = ids.reshape(-1).contiguous()
     weights = weights.reshape(-1).contiguous()
     count, hidden = ids.numel(), q.shape[1]
-    if count > DECODE_PAIRS:
-        raise ValueError(f"quantized_pairs takes at most {DECODE_PAIRS} pairs per call")
+    if count > MAX_PAIRS:
+        raise ValueError(f"quantized_pairs takes at most {MAX_PAIRS} pairs per call")
     if q.shape[0] not in (1, count):
         raise ValueError("quantized rows must be one shared row or one per pair")
     out = torch.empty((count, hidden), dtype=torch.float32, device=q.device)

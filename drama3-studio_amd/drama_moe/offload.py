@@ -25,7 +25,8 @@ from torch import Tensor, nn
 from . import _lib
 from .formats import EXPERT_BUFFER_NAMES, FP8_DTYPE, StagedExperts, fp8_bank_struct
 
-DECODE_PAIRS = 256  # route pairs one fused decode launch pair handles
+DECODE_PAIRS = 256  # route pairs up to which a call runs the decode kernels
+MAX_PAIRS = 16384   # route pairs of one call (above DECODE_PAIRS: grouped GEMMs)
 
 
 class _DeviceState:
@@ -112,7 +113,7 @@ class HipExpertBackend:
         self._validate(x, staged)
         ids, weights = ids.contiguous(), weights.contiguous()
         state = device_state(_device_of(x))
-        chunk = max(1, DECODE_PAIRS // top_k)
+        chunk = max(1, MAX_PAIRS // top_k)
         lib = _lib.library()
         ws = state.workspace_for(lib.dmoe_fp8_workspace_bytes(bank, min(tokens, chunk) * top_k))
         stream = _lib.stream_handle(x.device)
@@ -129,15 +130,16 @@ class HipExpertBackend:
     def forward_routed(self, x: Tensor, logits: Tensor, top_k: int, staged: StagedExperts, *,
                        renormalize: bool = True, weights_dtype: torch.dtype | None = None,
                        out: Tensor | None = None):
-        """Router + routed experts in one call (decode: two kernels, no host
-        sync).  Returns (out [T, H], weights [T, top_k], ids [T, top_k])."""
+        """Router + routed experts in one call, no host sync (decode: three
+        kernels; prefill: router, permutation, quantization, two grouped GEMMs
+        and the combine).  Returns (out [T, H], weights [T, top_k], ids [T, top_k])."""
         self._check(x)
         if x.ndim != 2 or logits.ndim != 2 or logits.shape[0] != x.shape[0]:
             raise ValueError("Expected x [T, H] and router logits [T, E]")
         if logits.dtype != torch.float32 or logits.stride(-1) != 1:
             logits = logits.float().contiguous()
         tokens = x.shape[0]
-        if tokens * top_k > DECODE_PAIRS:
+        if tokens * top_k > MAX_PAIRS:
             from .router import route_topk
 
             weights, ids = route_topk(logits, top_k, renormalize=renormalize,
@@ -206,11 +208,11 @@ class HipExpertBackend:
         ids, weights = ids.contiguous(), weights.contiguous()
         state = device_state(_device_of(x))
         lib = _lib.library()
-        ws = state.workspace_for(lib.dmoe_fp8_workspace_bytes(bank, min(pairs, DECODE_PAIRS)))
+        ws = state.workspace_for(lib.dmoe_fp8_workspace_bytes(bank, min(pairs, MAX_PAIRS)))
         stream = _lib.stream_handle(x.device)
         shared = x.shape[0] > 1 and x.stride(0) == 0  # an expanded single row
-        for start in range(0, pairs, DECODE_PAIRS):
-            stop = min(pairs, start + DECODE_PAIRS)
+        for start in range(0, pairs, MAX_PAIRS):
+            stop = min(pairs, start + MAX_PAIRS)
             if shared:
                 rows, div = x[:1], stop - start
             else:

@@ -109,12 +109,19 @@ DMOE_API int dmoe_route_topk(const float* logits, int64_t row_stride, int tokens
 DMOE_API int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t* order,
                           int32_t* counts, int32_t* offsets, int* status, void* stream);
 
-/* Workspace bytes for dmoe_fp8_moe_forward / _pairs / _quantized_pairs. */
+/* Workspace bytes of an FP8 call over `pairs` route pairs (0 outside
+ * [1, 16384]).  A workspace is zero-filled once when allocated (256-byte
+ * aligned) and reused by later calls of any size it covers: its leading
+ * region holds arrival counters that the decode kernels return to zero.
+ * Calls sharing one workspace must not overlap. */
 DMOE_API size_t dmoe_fp8_workspace_bytes(const DmoeFp8Bank* bank, int pairs);
 
 /* Whole routed-expert call: x [tokens, H] (bf16/fp16/fp32, row stride in
  * elements), ids/weights [tokens, top_k] contiguous, out [tokens, H] in
  * out_dtype = fp32 sum of the weighted expert partials in router slot order.
+ * Up to 256 pairs (tokens * top_k) run the decode kernels; up to 16384 the
+ * grouped path: moe_align permutation, grouped gate/up and down FP8 GEMMs on
+ * MFMA and the slot-order combine.
  * x_group = 128 (reference contract) or H (one activation scale per token);
  * gu_dtype = type the gate/up projection is stored in before SiLU (the
  * reference uses the compute dtype).  Replaces ExpertBackend.forward

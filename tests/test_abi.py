@@ -72,11 +72,13 @@ def test_forward_rejects_bad_bank_geometry(bank, message):
     assert message in _lib.library().dmoe_last_error().decode()
 
 
-def test_forward_rejects_small_workspace_and_oversized_decode():
+def test_forward_rejects_small_workspace_and_oversized_calls():
     assert _forward(_bank(), ws_bytes=16) == -1
     assert "workspace too small" in _lib.library().dmoe_last_error().decode()
-    assert _forward(_bank(), tokens=200, top_k=2) == -1
-    assert "256 route pairs" in _lib.library().dmoe_last_error().decode()
+    assert _forward(_bank(), tokens=200, top_k=2, ws_bytes=16) == -1  # grouped path: its own workspace
+    assert "workspace too small" in _lib.library().dmoe_last_error().decode()
+    assert _forward(_bank(), tokens=10000, top_k=2) == -1
+    assert "16384 route pairs" in _lib.library().dmoe_last_error().decode()
 
 
 def test_workspace_query_grows_with_pairs():
@@ -84,7 +86,11 @@ def test_workspace_query_grows_with_pairs():
     bank = _bank()
     small = lib.dmoe_fp8_workspace_bytes(ctypes.byref(bank), 8)
     large = lib.dmoe_fp8_workspace_bytes(ctypes.byref(bank), 64)
-    assert 0 < small < large
+    grouped = lib.dmoe_fp8_workspace_bytes(ctypes.byref(bank), 4096)
+    assert 0 < small < large < grouped
+    # the grouped workspace holds at least the fp32 partials of every pair
+    assert grouped >= 4096 * bank.w13.k * 4
+    assert lib.dmoe_fp8_workspace_bytes(ctypes.byref(bank), 16385) == 0
 
 
 def test_route_and_permute_validate_geometry():
