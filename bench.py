@@ -194,6 +194,64 @@ def run_gpu(steps: int, warmup: int):
     }
 
 
+PREFILL_TOKENS = 2048
+PREFILL_SEED = 20261203  # 20261201 + config index 2
+FP8_PEAK_TFLOPS = 5000.0
+
+
+def zipf_logits(tokens: int, experts: int, seed: int, exponent: float = 1.1):
+    """log p_e + Gumbel(0, 1), p_e ~ rank_e^-exponent over a seeded rank
+    permutation: the top-k of these logits samples experts without replacement."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    ranks = torch.randperm(experts, generator=g).double() + 1
+    logp = -exponent * torch.log(ranks)
+    logp -= torch.logsumexp(logp, 0)
+    u = torch.rand(tokens, experts, generator=g, dtype=torch.float64).clamp_(1e-12, 1 - 1e-12)
+    return (logp - torch.log(-torch.log(u))).float()
+
+
+def run_prefill(reps: int = 10):
+    """2048-token MoE layer: router + grouped FP8 experts, per-token activation
+    scales (and the reference's per-128 groups), one 606 MB bank."""
+    import torch
+
+    from drama_moe.offload import HipExpertBackend
+
+    device = torch.device("cuda", 0)
+    bank = make_layer_bank(LAYERS, device)
+    g = torch.Generator(device=device).manual_seed(PREFILL_SEED)
+    x = torch.randn(PREFILL_TOKENS, HIDDEN, device=device, generator=g).bfloat16()
+    logits = zipf_logits(PREFILL_TOKENS, EXPERTS, PREFILL_SEED).to(device)
+    out = torch.empty_like(x)
+    flops = 2.0 * PREFILL_TOKENS * TOP_K * 3 * INTER * HIDDEN
+    nbytes = EXPERTS * (3 * INTER * HIDDEN + (2 * INTER + HIDDEN) * 4) + 2 * PREFILL_TOKENS * HIDDEN * 2 \
+        + PREFILL_TOKENS * EXPERTS * 4
+    result = {}
+    for name, group in (("per_token", "token"), ("per_128", 128)):
+        backend = HipExpertBackend(x_group=group)
+        for _ in range(3):
+            backend.forward_routed(x, logits, TOP_K, bank, out=out)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            backend.forward_routed(x, logits, TOP_K, bank, out=out)
+        stop.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(stop) * 1e3 / reps
+        tflops = flops / (us * 1e-6) / 1e12
+        gbs = nbytes / (us * 1e-6) / 1e9
+        result[name] = {"us": round(us, 2), "tflops": round(tflops, 1),
+                        "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "roofline_frac": round(max(tflops / FP8_PEAK_TFLOPS, gbs / HBM_PEAK_GBS), 4)}
+    result.update({"tokens": PREFILL_TOKENS, "top_k": TOP_K, "experts": EXPERTS, "routing": "zipf1.1",
+                   "alg_gflop": round(flops / 1e9, 2), "alg_mb": round(nbytes / 1e6, 1)})
+    return result
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The reference CPU expert executor (oracle/_ref), one token per call with
     8 route slots over 8 worker threads, block-128 FP8 banks of the same layer
@@ -253,6 +311,7 @@ def main():
     parser.add_argument("--steps", type=int, default=4096)
     parser.add_argument("--warmup", type=int, default=256)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-prefill", action="store_true")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path is built and "
@@ -264,6 +323,8 @@ def main():
     steps = max(1, args.steps)
     gpu = run_gpu(steps, args.warmup)
     log("gpu", json.dumps(gpu))
+    prefill = None if args.no_prefill else run_prefill()
+    log("prefill", json.dumps(prefill))
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log("cpu", json.dumps(cpu))
@@ -292,6 +353,7 @@ def main():
                      "kernel": "fp8_gateup_decode_kernel", "kernel_us": round(gpu["kernel_us"], 3),
                      "alg_bytes_per_launch": round(gpu["kernel_bytes"])},
         "cpu_baseline": cpu,
+        "prefill_fp8": prefill,
     }
     print(json.dumps(line), flush=True)
 

@@ -145,7 +145,7 @@ struct Activations {
 
 void check_activations(const BankGeom& g, const Activations& a, int pairs) {
     require(pairs >= 1, "at least one route pair is required");
-    require(pairs <= dmoe::kMaxPermutePairs, "more than 16384 route pairs per call: split the rows");
+    require(pairs <= dmoe::kMaxPermutePairs, "more than 1048576 route pairs per call: split the rows");
     require(a.row_div >= 1 && (int64_t)(pairs - 1) / a.row_div < a.rows, "pairs read past the activation rows");
     require(a.x_group == 128 || a.x_group == g.H, "activation group must be 128 or the hidden size");
     if (a.xq) {
@@ -287,6 +287,7 @@ void fp8_decode_call(const BankGeom& g, Activations a, const dmoe::RouteSource& 
 // the decode layout and never writes it, so one workspace serves both paths
 // and the decode arrival counters stay zero.
 struct PrefillWorkspace {
+    int32_t* permute_scratch;
     int32_t* order;
     int32_t* counts;
     int32_t* offsets;
@@ -308,6 +309,7 @@ size_t prefill_workspace_layout(int pairs, int experts, int H, int I, char* base
     };
     const int tiles = dmoe::max_block_tiles(pairs, experts, dmoe::kGroupM);
     take(kCounterBytes);  // decode arrival counters: reserved, untouched here
+    char* scratch = take(dmoe::permute_scratch_bytes(pairs, experts));
     char* order = take((size_t)pairs * 4);
     char* counts = take((size_t)experts * 4);
     char* offsets = take((size_t)(experts + 1) * 4);
@@ -319,6 +321,7 @@ size_t prefill_workspace_layout(int pairs, int experts, int H, int I, char* base
     char* hs = take((size_t)pairs * (I / 128) * 4);
     char* partial = take((size_t)pairs * H * 4);
     if (ws) {
+        ws->permute_scratch = reinterpret_cast<int32_t*>(scratch);
         ws->order = reinterpret_cast<int32_t*>(order);
         ws->counts = reinterpret_cast<int32_t*>(counts);
         ws->offsets = reinterpret_cast<int32_t*>(offsets);
@@ -353,7 +356,8 @@ void fp8_prefill_call(const BankGeom& g, Activations a, const void* ids, int ids
     const int tiles = dmoe::max_block_tiles(pairs, g.experts, dmoe::kGroupM);
 
     dmoe::PermuteArgs pa{ids, ids_dtype, pairs, g.experts, ws.order, ws.counts, ws.offsets, status,
-                         dmoe::kGroupM, tiles, ws.tile_expert, ws.tile_m0};
+                         ws.permute_scratch, ws.permute_scratch + pairs, dmoe::kGroupM, tiles, ws.tile_expert,
+                         ws.tile_m0};
     dmoe::launch_permute(pa, stream);
     if (a.xq == nullptr) {
         const int rows = (pairs - 1) / a.row_div + 1;
@@ -480,14 +484,25 @@ int dmoe_route_topk(const float* logits, int64_t row_stride, int tokens, int exp
     });
 }
 
+size_t dmoe_permute_workspace_bytes(int pairs, int experts) {
+    if (pairs < 1 || pairs > dmoe::kMaxPermutePairs || experts < 1 || experts > dmoe::kMaxExperts) return 0;
+    return dmoe::permute_scratch_bytes(pairs, experts);
+}
+
 int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t* order,
-                 int32_t* counts, int32_t* offsets, int* status, void* stream) {
+                 int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes, int* status,
+                 void* stream) {
     return checked([&] {
         require(ids && order && counts && offsets, "permutation buffers are required");
         require(is_id_dtype(ids_dtype), "route ids must be int32 or int64");
         require(experts >= 1 && experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
-        require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 16384]");
-        dmoe::PermuteArgs a{ids, ids_dtype, pairs, experts, order, counts, offsets, status, 0, 0, nullptr, nullptr};
+        require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 1048576]");
+        require(workspace != nullptr && workspace_bytes >= dmoe::permute_scratch_bytes(pairs, experts) &&
+                    reinterpret_cast<uintptr_t>(workspace) % 4 == 0,
+                "workspace too small");
+        int32_t* scratch = static_cast<int32_t*>(workspace);
+        dmoe::PermuteArgs a{ids, ids_dtype, pairs, experts, order, counts, offsets, status,
+                            scratch, scratch + pairs, 0, 0, nullptr, nullptr};
         dmoe::launch_permute(a, as_stream(stream));
     });
 }

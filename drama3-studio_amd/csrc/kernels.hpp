@@ -92,7 +92,8 @@ struct DownArgs {
     int* status;
 };
 
-constexpr int kMaxPermutePairs = 16384;  // pairs one permutation workgroup sorts
+constexpr int kMaxPermutePairs = 1 << 20;  // route pairs of one permutation / grouped call
+constexpr int kPermuteBlock = 256;         // pairs per block of the permutation kernels
 constexpr int kRouteElems = 1024;   // logits one workgroup ranks at a time (tokens * experts)
 constexpr int kRouteTokens = 8;     // tokens one workgroup routes at a time
 
@@ -125,6 +126,9 @@ struct PermuteArgs {
     int32_t* counts;        // [experts]
     int32_t* offsets;       // [experts + 1]
     int* status;
+    // scratch: rank [pairs] then hist [ceil(pairs / kPermuteBlock), experts]
+    int32_t* rank;
+    int32_t* hist;
     // Optional moe_align tile map (tile_expert == nullptr: none): the sorted
     // pairs of each expert cut into block_m-row tiles, expert-major; tile i
     // covers sorted positions [tile_m0[i], min(tile_m0[i] + block_m,
@@ -205,6 +209,7 @@ void launch_fp8_quantize(const QuantArgs& a, hipStream_t stream);
 void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stream);
 void launch_route_topk(const RouteArgs& a, hipStream_t stream);
 void launch_permute(const PermuteArgs& a, hipStream_t stream);
+size_t permute_scratch_bytes(int64_t pairs, int experts);
 void launch_fp8_grouped_gateup(const GroupedGateUpArgs& a, hipStream_t stream);
 void launch_fp8_grouped_down(const GroupedDownArgs& a, hipStream_t stream);
 void launch_combine(const CombineArgs& a, hipStream_t stream);

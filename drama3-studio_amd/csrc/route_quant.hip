@@ -359,70 +359,94 @@ void launch_moe_prep(const PrepArgs& a, hipStream_t stream) {
 // Stable expert-major permutation of the flattened route pairs: order[i] is
 // the i-th pair in (expert, pair index) order, with per-expert counts and
 // offsets.  Reference: offload.py:1206-1210 (argsort(stable=True), bincount,
-// starts = cumsum - counts).  One 1024-thread workgroup: thread (e, part)
-// counts expert e inside its contiguous chunk of pairs, a block-wide exclusive
-// scan over (e, part) gives every chunk its output base, and a second pass
-// writes the pair indices -- stable by construction.
-__global__ __launch_bounds__(1024) void permute_kernel(PermuteArgs a) {
-    __shared__ int16_t sid[kMaxPermutePairs];
-    __shared__ int scan[1024];
-    __shared__ int wsum[16];
-    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
-    for (int i = t; i < a.pairs; i += 1024) {
+// starts = cumsum - counts).  A stable counting sort in three launches:
+//   rank:    per block of 256 pairs, each pair's rank among the earlier pairs
+//            of its block with the same expert, and the block's histogram;
+//   scan:    one workgroup scans the histograms in (expert, block) order into
+//            each block's output base per expert, the offsets / counts and the
+//            moe_align tile map;
+//   scatter: order[base(block, expert) + rank] = pair.
+// No atomics on global memory and no state carried between calls.
+__global__ __launch_bounds__(kPermuteBlock) void permute_rank_kernel(PermuteArgs a) {
+    __shared__ int16_t sid[kPermuteBlock];
+    __shared__ int hist[kMaxExperts];
+    const int t = threadIdx.x;
+    const int64_t i = (int64_t)blockIdx.x * kPermuteBlock + t;
+    int e = -1;
+    if (i < a.pairs) {
         const int64_t id = load_id(a.ids, i, a.ids_dtype);
-        const bool ok = id >= 0 && id < a.experts;
-        if (!ok) raise_status(a.status, kBadExpertId);
-        sid[i] = ok ? (int16_t)id : (int16_t)-1;
+        if (id >= 0 && id < a.experts) e = (int)id;
+        else raise_status(a.status, kBadExpertId);
+    }
+    sid[t] = (int16_t)e;
+    for (int x = t; x < a.experts; x += kPermuteBlock) hist[x] = 0;
+    __syncthreads();
+    if (e >= 0) {
+        int r = 0;
+        for (int j = 0; j < t; ++j) r += (int)(sid[j] == e);
+        a.rank[i] = (e << 16) | r;
+        atomicAdd(&hist[e], 1);
+    } else if (i < a.pairs) {
+        a.rank[i] = -1;
     }
     __syncthreads();
-    const int parts = max(1, 1024 / a.experts);
-    const int owners = a.experts * parts;
-    const int e = t / parts, part = t % parts;
-    const int chunk = (a.pairs + parts - 1) / parts;
-    const int begin = min(a.pairs, part * chunk), end = min(a.pairs, begin + chunk);
-    int count = 0;
-    if (t < owners)
-        for (int i = begin; i < end; ++i) count += sid[i] == e;
-    // block-wide exclusive scan of count over t
-    int incl = count;
+    for (int x = t; x < a.experts; x += kPermuteBlock) a.hist[(int64_t)blockIdx.x * a.experts + x] = hist[x];
+}
+
+// Exclusive scan of the [blocks, experts] histogram table in (expert, block)
+// order, in place: hist[b][e] becomes the first output position of block b's
+// pairs of expert e.
+__global__ __launch_bounds__(1024) void permute_scan_kernel(PermuteArgs a) {
+    __shared__ int wsum[16];
+    __shared__ int offs[kMaxExperts + 1];
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    const int blocks = (a.pairs + kPermuteBlock - 1) / kPermuteBlock;
+    const int64_t n = (int64_t)blocks * a.experts;
+    const int64_t per = (n + 1023) / 1024;
+    const int64_t lo = min(n, t * per), hi = min(n, lo + per);
+    auto at = [&](int64_t idx) -> int32_t* {  // idx = e * blocks + b
+        return a.hist + (idx % blocks) * a.experts + idx / blocks;
+    };
+    int local = 0;
+    for (int64_t x = lo; x < hi; ++x) local += *at(x);
+    int incl = local;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
-        const int n = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl += n;
+        const int v = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += v;
     }
     if (lane == kWave - 1) wsum[wave] = incl;
     __syncthreads();
-    int wbase = 0;
-    for (int w = 0; w < wave; ++w) wbase += wsum[w];
-    const int excl = wbase + incl - count;
-    scan[t] = excl;
+    int base = incl - local, total = 0;
+    for (int w = 0; w < 16; ++w) {
+        if (w < wave) base += wsum[w];
+        total += wsum[w];
+    }
+    for (int64_t x = lo; x < hi; ++x) {
+        int32_t* p = at(x);
+        const int c = *p;
+        *p = base;
+        if (x % blocks == 0) offs[x / blocks] = base;
+        base += c;
+    }
+    if (t == 0) offs[a.experts] = total;
     __syncthreads();
-    int total = 0;
-    for (int w = 0; w < 16; ++w) total += wsum[w];
-    if (t < owners) {
-        int pos = excl;
-        for (int i = begin; i < end; ++i)
-            if (sid[i] == e) a.order[pos++] = i;
+    for (int x = t; x < a.experts; x += 1024) {
+        a.offsets[x] = offs[x];
+        a.counts[x] = offs[x + 1] - offs[x];
     }
-    for (int i = total + t; i < a.pairs; i += 1024) a.order[i] = -1;  // invalid pairs
-    if (t < a.experts) {
-        const int start = scan[t * parts];
-        const int stop = t + 1 < a.experts ? scan[(t + 1) * parts] : total;
-        a.offsets[t] = start;
-        a.counts[t] = stop - start;
-        if (t == a.experts - 1) a.offsets[a.experts] = total;
-    }
+    if (t == 0) a.offsets[a.experts] = total;
+    for (int64_t x = total + t; x < a.pairs; x += 1024) a.order[x] = -1;  // invalid pairs
     if (a.tile_expert == nullptr) return;
-    // moe_align tile map: exclusive scan of per-expert tile counts
-    __syncthreads();  // every thread has read wsum
-    const int estart = t < a.experts ? scan[t * parts] : 0;
-    const int ecount = t < a.experts ? (t + 1 < a.experts ? scan[(t + 1) * parts] : total) - estart : 0;
+    // moe_align tile map: one expert per thread, exclusive scan of tile counts
+    __syncthreads();  // wsum is reused
+    const int ecount = t < a.experts ? offs[t + 1] - offs[t] : 0;
     const int ntiles = (ecount + a.block_m - 1) / a.block_m;
     int tincl = ntiles;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
-        const int n = __shfl_up(tincl, o, kWave);
-        if (lane >= o) tincl += n;
+        const int v = __shfl_up(tincl, o, kWave);
+        if (lane >= o) tincl += v;
     }
     if (lane == kWave - 1) wsum[wave] = tincl;
     __syncthreads();
@@ -434,13 +458,30 @@ __global__ __launch_bounds__(1024) void permute_kernel(PermuteArgs a) {
     const int tstart = tbase + tincl - ntiles;
     for (int j = 0; j < ntiles; ++j) {
         a.tile_expert[tstart + j] = t;
-        a.tile_m0[tstart + j] = estart + j * a.block_m;
+        a.tile_m0[tstart + j] = offs[t] + j * a.block_m;
     }
-    for (int i = ttotal + t; i < a.max_tiles; i += 1024) a.tile_expert[i] = -1;
+    for (int x = ttotal + t; x < a.max_tiles; x += 1024) a.tile_expert[x] = -1;
+}
+
+__global__ __launch_bounds__(kPermuteBlock) void permute_scatter_kernel(PermuteArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * kPermuteBlock + threadIdx.x;
+    if (i >= a.pairs) return;
+    const int code = a.rank[i];
+    if (code < 0) return;
+    const int e = code >> 16, r = code & 0xFFFF;
+    a.order[a.hist[(int64_t)blockIdx.x * a.experts + e] + r] = (int32_t)i;
+}
+
+size_t permute_scratch_bytes(int64_t pairs, int experts) {
+    const int64_t blocks = (pairs + kPermuteBlock - 1) / kPermuteBlock;
+    return (size_t)(pairs + blocks * experts) * 4;
 }
 
 void launch_permute(const PermuteArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, a);
+    const unsigned blocks = (unsigned)((a.pairs + kPermuteBlock - 1) / kPermuteBlock);
+    hipLaunchKernelGGL(permute_rank_kernel, dim3(blocks), dim3(kPermuteBlock), 0, stream, a);
+    hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL(permute_scatter_kernel, dim3(blocks), dim3(kPermuteBlock), 0, stream, a);
 }
 
 }  // namespace dmoe

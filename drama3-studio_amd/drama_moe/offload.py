@@ -26,7 +26,7 @@ from . import _lib
 from .formats import EXPERT_BUFFER_NAMES, FP8_DTYPE, StagedExperts, fp8_bank_struct
 
 DECODE_PAIRS = 256  # route pairs up to which a call runs the decode kernels
-MAX_PAIRS = 16384   # route pairs of one call (above DECODE_PAIRS: grouped GEMMs)
+MAX_PAIRS = 65536   # route pairs of one call (above DECODE_PAIRS: grouped GEMMs)
 
 
 class _DeviceState:

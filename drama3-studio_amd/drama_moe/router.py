@@ -39,10 +39,13 @@ def permute(ids: torch.Tensor, num_experts: int):
     order = torch.empty(pairs, dtype=torch.int32, device=ids.device)
     counts = torch.empty(num_experts, dtype=torch.int32, device=ids.device)
     offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=ids.device)
-    _lib.check(_lib.library().dmoe_permute(
+    lib = _lib.library()
+    scratch = torch.empty(max(1, lib.dmoe_permute_workspace_bytes(pairs, num_experts)), dtype=torch.uint8,
+                          device=ids.device)
+    _lib.check(lib.dmoe_permute(
         _lib.ptr(flat), _lib.dtype_code(flat.dtype), pairs, num_experts, _lib.ptr(order),
-        _lib.ptr(counts), _lib.ptr(offsets), _lib.ptr(device_state(ids.device).status),
-        _lib.stream_handle(ids.device)))
+        _lib.ptr(counts), _lib.ptr(offsets), _lib.ptr(scratch), scratch.numel(),
+        _lib.ptr(device_state(ids.device).status), _lib.stream_handle(ids.device)))
     return order, counts, offsets
 
 

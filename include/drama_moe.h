@@ -102,15 +102,21 @@ DMOE_API int dmoe_route_topk(const float* logits, int64_t row_stride, int tokens
                              int top_k, int renormalize, int64_t* ids, void* weights,
                              int weights_dtype, void* stream);
 
+/* Scratch bytes of dmoe_permute (0 outside pairs in [1, 2^20], experts in
+ * [1, 512]). */
+DMOE_API size_t dmoe_permute_workspace_bytes(int pairs, int experts);
+
 /* Stable expert-major permutation of pairs = tokens * top_k flattened route
  * ids (int32 or int64): order [pairs] (-1 past the valid pairs), counts
- * [experts], offsets [experts + 1].  Replaces the argsort(stable)/bincount/
- * starts of ExpertOffloadManager._forward_partitioned (offload.py:1206-1210). */
+ * [experts], offsets [experts + 1]; invalid ids are left out and flagged.
+ * Replaces the argsort(stable)/bincount/starts of
+ * ExpertOffloadManager._forward_partitioned (offload.py:1206-1210). */
 DMOE_API int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t* order,
-                          int32_t* counts, int32_t* offsets, int* status, void* stream);
+                          int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes,
+                          int* status, void* stream);
 
 /* Workspace bytes of an FP8 call over `pairs` route pairs (0 outside
- * [1, 16384]).  A workspace is zero-filled once when allocated (256-byte
+ * [1, 2^20]).  A workspace is zero-filled once when allocated (256-byte
  * aligned) and reused by later calls of any size it covers: its leading
  * region holds arrival counters that the decode kernels return to zero.
  * Calls sharing one workspace must not overlap. */
@@ -119,7 +125,7 @@ DMOE_API size_t dmoe_fp8_workspace_bytes(const DmoeFp8Bank* bank, int pairs);
 /* Whole routed-expert call: x [tokens, H] (bf16/fp16/fp32, row stride in
  * elements), ids/weights [tokens, top_k] contiguous, out [tokens, H] in
  * out_dtype = fp32 sum of the weighted expert partials in router slot order.
- * Up to 256 pairs (tokens * top_k) run the decode kernels; up to 16384 the
+ * Up to 256 pairs (tokens * top_k) run the decode kernels; up to 2^20 the
  * grouped path: moe_align permutation, grouped gate/up and down FP8 GEMMs on
  * MFMA and the slot-order combine.
  * x_group = 128 (reference contract) or H (one activation scale per token);

@@ -77,8 +77,8 @@ def test_forward_rejects_small_workspace_and_oversized_calls():
     assert "workspace too small" in _lib.library().dmoe_last_error().decode()
     assert _forward(_bank(), tokens=200, top_k=2, ws_bytes=16) == -1  # grouped path: its own workspace
     assert "workspace too small" in _lib.library().dmoe_last_error().decode()
-    assert _forward(_bank(), tokens=10000, top_k=2) == -1
-    assert "16384 route pairs" in _lib.library().dmoe_last_error().decode()
+    assert _forward(_bank(), tokens=600000, top_k=2) == -1
+    assert "1048576 route pairs" in _lib.library().dmoe_last_error().decode()
 
 
 def test_workspace_query_grows_with_pairs():
@@ -90,12 +90,18 @@ def test_workspace_query_grows_with_pairs():
     assert 0 < small < large < grouped
     # the grouped workspace holds at least the fp32 partials of every pair
     assert grouped >= 4096 * bank.w13.k * 4
-    assert lib.dmoe_fp8_workspace_bytes(ctypes.byref(bank), 16385) == 0
+    assert lib.dmoe_fp8_workspace_bytes(ctypes.byref(bank), (1 << 20) + 1) == 0
 
 
 def test_route_and_permute_validate_geometry():
     lib = _lib.library()
     assert lib.dmoe_route_topk(_fake(), 128, 4, 128, 0, 1, _fake(), _fake(), _lib.BF16, None) == -1
     assert "top_k" in lib.dmoe_last_error().decode()
-    assert lib.dmoe_permute(_fake(), _lib.I64, 20000, 128, _fake(), _fake(), _fake(), None, None) == -1
+    assert lib.dmoe_permute(_fake(), _lib.I64, 2_000_000, 128, _fake(), _fake(), _fake(), _fake(), 1 << 30,
+                            None, None) == -1
     assert "pair count" in lib.dmoe_last_error().decode()
+    need = lib.dmoe_permute_workspace_bytes(20000, 128)
+    assert need >= 20000 * 4 + 79 * 128 * 4
+    assert lib.dmoe_permute(_fake(), _lib.I64, 20000, 128, _fake(), _fake(), _fake(), _fake(), need - 4,
+                            None, None) == -1
+    assert "workspace too small" in lib.dmoe_last_error().decode()

@@ -134,7 +134,7 @@ def test_route_topk_ties_take_the_lower_index(cuda):
     np.testing.assert_array_equal(ids.cpu().numpy(), orc.route_topk(logits.numpy(), 4)[0])
 
 
-@pytest.mark.parametrize("tokens,experts", [(1, 128), (16, 128), (2048, 128), (300, 7), (64, 512)])
+@pytest.mark.parametrize("tokens,experts", [(1, 128), (16, 128), (2048, 128), (300, 7), (64, 512), (12500, 128)])
 def test_permute_bit_exact_against_stable_argsort(cuda, tokens, experts):
     print_case("permute", tokens, experts)
     g = torch.Generator().manual_seed(tokens + experts)
