@@ -356,8 +356,8 @@ void fp8_prefill_call(const BankGeom& g, Activations a, const void* ids, int ids
     const int tiles = dmoe::max_block_tiles(pairs, g.experts, dmoe::kGroupM);
 
     dmoe::PermuteArgs pa{ids, ids_dtype, pairs, g.experts, ws.order, ws.counts, ws.offsets, status,
-                         ws.permute_scratch, ws.permute_scratch + pairs, dmoe::kGroupM, tiles, ws.tile_expert,
-                         ws.tile_m0};
+                         ws.permute_scratch, ws.permute_scratch + pairs, nullptr, dmoe::kGroupM, tiles,
+                         ws.tile_expert, ws.tile_m0};
     dmoe::launch_permute(pa, stream);
     if (a.xq == nullptr) {
         const int rows = (pairs - 1) / a.row_div + 1;
@@ -424,6 +424,142 @@ void fp8_call(const BankGeom& g, Activations a, const dmoe::RouteSource& route, 
     else
         fp8_prefill_call(g, a, ids, ids_dtype, weights, weights_dtype, pairs, top_k, gu_dtype, out, out_dtype,
                          out_row_stride, out_pairs, workspace, workspace_bytes, status, stream);
+}
+
+
+// ------------------------------------------------------ packed-integer banks
+
+dmoe::QuantProjArgs check_quant_proj(const DmoeQuantProj& p, int mode, int experts) {
+    require(mode >= 0 && mode <= 3, "packed mode must be 0 (W4A16), 1 (INT8), 2 (W6A8) or 3 (W4A8)");
+    require(p.weight && p.scale, "packed weight and scale pointers are required");
+    require(p.n >= 16 && p.n % 16 == 0, "packed projection N must be a positive multiple of 16");
+    require(p.k >= 128 && p.k <= dmoe::kMaxQuantK && p.k % (mode == 0 ? 128 : 256) == 0,
+            mode == 0 ? "W4A16 K must be a multiple of 128, at most 4096"
+                      : "INT8/W6A8/W4A8 K must be a multiple of 256, at most 4096");
+    const int64_t wcols = mode == 0 ? (int64_t)p.k / 2 : mode == 1 ? p.k : mode == 2 ? (int64_t)p.k * 3 / 4 : p.k / 2;
+    const int64_t scols = mode == 0 ? (int64_t)p.k / 128 * 2 : mode == 1 ? 4 : p.k / 16 + (mode == 3 ? 8 : 4);
+    require(p.weight_stride_n >= wcols && p.weight_stride_n % 16 == 0 && p.weight_stride_e >= 0 &&
+                p.weight_stride_e % 16 == 0 && reinterpret_cast<uintptr_t>(p.weight) % 16 == 0,
+            "packed weight rows must be contiguous and 16-byte aligned");
+    require(p.scale_stride_n >= scols && p.scale_stride_e >= 0 && p.scale_stride_n % 4 == 0 &&
+                p.scale_stride_e % 4 == 0 && reinterpret_cast<uintptr_t>(p.scale) % 4 == 0,
+            "packed scale rows must be contiguous and 4-byte aligned");
+    require(p.zeros == nullptr || mode == 0, "zero points apply to W4A16 banks only");
+    require(p.zeros == nullptr || p.zeros_stride_e >= (int64_t)(p.k / 128) * (p.n / 8),
+            "W4A16 zero points must be [E, K/128, N/8] int32");
+    require(mode != 3 || p.n >= 16, "W4A8 codebook rows need N >= 16");
+    (void)experts;
+    dmoe::QuantProjArgs q{};
+    q.mode = mode;
+    q.w = static_cast<const uint8_t*>(p.weight);
+    q.s = static_cast<const uint8_t*>(p.scale);
+    q.z = p.zeros;
+    q.w_se = p.weight_stride_e;
+    q.w_sn = p.weight_stride_n;
+    q.s_se = p.scale_stride_e;
+    q.s_sn = p.scale_stride_n;
+    q.z_se = p.zeros_stride_e;
+    q.N = p.n;
+    q.K = p.k;
+    return q;
+}
+
+struct QuantWorkspace {
+    int32_t* permute_scratch;
+    int32_t* order;
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* active;
+    int8_t* xq;
+    float* xs;
+    uint16_t* act;
+    int8_t* actq;
+    float* acts;
+    float* partial;
+};
+
+size_t quant_workspace_layout(int rows, int pairs, int experts, int H, int I, char* base, QuantWorkspace* ws) {
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        const size_t o = off;
+        off = align256(off + n);
+        return base ? base + o : nullptr;
+    };
+    take(kCounterBytes);  // decode arrival counters: reserved, untouched here
+    char* scratch = take(dmoe::permute_scratch_bytes(pairs, experts));
+    char* order = take((size_t)pairs * 4);
+    char* counts = take((size_t)experts * 4);
+    char* offsets = take((size_t)(experts + 1) * 4);
+    char* active = take((size_t)(experts + 1) * 4);
+    char* xq = take((size_t)rows * H);
+    char* xs = take((size_t)rows * 4);
+    char* act = take((size_t)pairs * I * 2);
+    char* actq = take((size_t)pairs * I);
+    char* acts = take((size_t)pairs * 4);
+    char* partial = take((size_t)pairs * H * 4);
+    if (ws) {
+        ws->permute_scratch = reinterpret_cast<int32_t*>(scratch);
+        ws->order = reinterpret_cast<int32_t*>(order);
+        ws->counts = reinterpret_cast<int32_t*>(counts);
+        ws->offsets = reinterpret_cast<int32_t*>(offsets);
+        ws->active = reinterpret_cast<int32_t*>(active);
+        ws->xq = reinterpret_cast<int8_t*>(xq);
+        ws->xs = reinterpret_cast<float*>(xs);
+        ws->act = reinterpret_cast<uint16_t*>(act);
+        ws->actq = reinterpret_cast<int8_t*>(actq);
+        ws->acts = reinterpret_cast<float*>(acts);
+        ws->partial = reinterpret_cast<float*>(partial);
+    }
+    return off;
+}
+
+QuantWorkspace take_quant_workspace(int rows, int pairs, int experts, int H, int I, void* workspace,
+                                    size_t workspace_bytes) {
+    const size_t need = quant_workspace_layout(rows, pairs, experts, H, I, nullptr, nullptr);
+    require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+    require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+    QuantWorkspace ws{};
+    quant_workspace_layout(rows, pairs, experts, H, I, static_cast<char*>(workspace), &ws);
+    return ws;
+}
+
+void check_quant_rows(const void* x, int x_dtype, int64_t x_row_stride, int rows, int row_div, int pairs, int K,
+                      int mode) {
+    require(x != nullptr && is_float_dtype(x_dtype), "activations must be fp32, bf16 or fp16");
+    require(mode != 0 || x_dtype != DMOE_F32, "W4A16 activations must be bf16 or fp16");
+    require(rows >= 1 && x_row_stride >= K, "activation rows must be [rows, K] with contiguous columns");
+    const int esize = x_dtype == DMOE_F32 ? 4 : 2;
+    require(mode != 0 || ((x_row_stride * esize) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0),
+            "W4A16 activation rows must be 16-byte aligned");
+    require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 1048576]");
+    require(row_div >= 1 && (int64_t)(pairs - 1) / row_div < rows, "pairs read past the activation rows");
+}
+
+// Permutation with the active-expert list (the grouping of every packed call).
+void quant_group(const void* ids, int ids_dtype, int pairs, int experts, const QuantWorkspace& ws, int* status,
+                 hipStream_t stream) {
+    dmoe::PermuteArgs pa{ids, ids_dtype, pairs, experts, ws.order, ws.counts, ws.offsets, status,
+                         ws.permute_scratch, ws.permute_scratch + pairs, ws.active, 0, 0, nullptr, nullptr};
+    dmoe::launch_permute(pa, stream);
+}
+
+// Activation operand of a projection: mode 0 the rows as they are; modes 1-3
+// rotated + INT8 rows into (q, sc).
+void quant_operand(dmoe::QuantProjArgs& q, const void* x, int x_dtype, int64_t x_row_stride, int rows, int K,
+                   int8_t* xq, float* xs, hipStream_t stream) {
+    if (q.mode == 0) {
+        q.x = x;
+        q.x_f16 = x_dtype == DMOE_F16;
+        q.x_row_stride = x_row_stride;
+        q.sa = nullptr;
+    } else {
+        const dmoe::RotateArgs ra{x, x_dtype, x_row_stride, rows, K, xq, K, xs};
+        dmoe::launch_rotate_quant(ra, stream);
+        q.x = xq;
+        q.x_f16 = 0;
+        q.x_row_stride = K;
+        q.sa = xs;
+    }
 }
 
 }  // namespace
@@ -502,7 +638,7 @@ int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t
                 "workspace too small");
         int32_t* scratch = static_cast<int32_t*>(workspace);
         dmoe::PermuteArgs a{ids, ids_dtype, pairs, experts, order, counts, offsets, status,
-                            scratch, scratch + pairs, 0, 0, nullptr, nullptr};
+                            scratch, scratch + pairs, nullptr, 0, 0, nullptr, nullptr};
         dmoe::launch_permute(a, as_stream(stream));
     });
 }
@@ -640,6 +776,124 @@ int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
         }
         fp8_call(g, a, route, ids_out, DMOE_I64, weights_out, weights_dtype, pairs, top_k, gu_dtype, out, out_dtype,
                  out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
+    });
+}
+
+// ------------------------------------------------------ packed-integer banks
+
+int dmoe_rotate_quantize(const void* x, int x_dtype, int64_t x_row_stride, int rows, int k, int8_t* q,
+                         float* scales, void* stream) {
+    return checked([&] {
+        require(x && q && scales, "rotation buffers are required");
+        require(is_float_dtype(x_dtype), "activations must be fp32, bf16 or fp16");
+        require(rows >= 0 && k >= 256 && k % 256 == 0 && k <= dmoe::kMaxQuantK,
+                "K must be a multiple of 256, at most 4096");
+        require(x_row_stride >= k, "row stride smaller than the row");
+        const dmoe::RotateArgs ra{x, x_dtype, x_row_stride, rows, k, q, k, scales};
+        dmoe::launch_rotate_quant(ra, as_stream(stream));
+    });
+}
+
+size_t dmoe_quant_workspace_bytes(const DmoeQuantBank* bank, int rows, int pairs) {
+    if (!bank || rows < 1 || pairs < 1 || pairs > dmoe::kMaxPermutePairs || bank->experts < 1 ||
+        bank->experts > dmoe::kMaxExperts)
+        return 0;
+    const int H = std::max(bank->w13.k, bank->w2.n), I = std::max(bank->w2.k, bank->w13.n / 2);
+    return quant_workspace_layout(rows, pairs, bank->experts, H, I, nullptr, nullptr);
+}
+
+size_t dmoe_quant_projection_workspace_bytes(int experts, int k, int rows, int pairs) {
+    if (experts < 1 || experts > dmoe::kMaxExperts || k < 1 || rows < 1 || pairs < 1 ||
+        pairs > dmoe::kMaxPermutePairs)
+        return 0;
+    return quant_workspace_layout(rows, pairs, experts, k, 0, nullptr, nullptr);
+}
+
+int dmoe_quant_projection(const DmoeQuantProj* proj, int experts, int mode, const void* x, int x_dtype,
+                          int64_t x_row_stride, int rows, int row_div, const void* ids, int ids_dtype,
+                          const void* weights, int weights_dtype, int pairs, int weighted, void* out,
+                          int64_t out_row_stride, void* workspace, size_t workspace_bytes, int* status,
+                          void* stream) {
+    return checked([&] {
+        require(proj != nullptr, "packed projection descriptor is required");
+        require(experts >= 1 && experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        dmoe::QuantProjArgs q = check_quant_proj(*proj, mode, experts);
+        check_quant_rows(x, x_dtype, x_row_stride, rows, row_div, pairs, q.K, mode);
+        require(ids != nullptr && is_id_dtype(ids_dtype), "route ids must be int32 or int64");
+        require(!weighted || (weights != nullptr && is_float_dtype(weights_dtype)), "route weights are required");
+        require(out != nullptr && out_row_stride >= q.N, "output [pairs, N] is required");
+        const QuantWorkspace ws = take_quant_workspace(rows, pairs, experts, q.K, 0, workspace, workspace_bytes);
+        hipStream_t st = as_stream(stream);
+        quant_group(ids, ids_dtype, pairs, experts, ws, status, st);
+        quant_operand(q, x, x_dtype, x_row_stride, rows, q.K, ws.xq, ws.xs, st);
+        q.row_div = row_div;
+        q.order = ws.order;
+        q.offsets = ws.offsets;
+        q.active = ws.active;
+        q.gateup = 0;
+        q.weighted = weighted != 0;
+        q.weights = weights;
+        q.w_dtype = weights_dtype;
+        q.out = out;
+        q.out_row_stride = out_row_stride;
+        q.status = status;
+        dmoe::launch_quant_projection(q, std::min(pairs, experts), st);
+    });
+}
+
+int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype, int64_t x_row_stride, int rows,
+                           int row_div, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                           int pairs, int top_k, void* out, int out_dtype, int64_t out_row_stride, float* out_pairs,
+                           void* workspace, size_t workspace_bytes, int* status, void* stream) {
+    return checked([&] {
+        require(bank != nullptr, "packed bank descriptor is required");
+        const int E = bank->experts, mode = bank->mode;
+        require(E >= 1 && E <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        dmoe::QuantProjArgs up = check_quant_proj(bank->w13, mode, E);
+        dmoe::QuantProjArgs dn = check_quant_proj(bank->w2, mode, E);
+        const int H = up.K, I = up.N / 2;
+        require(dn.N == H && dn.K == I, "w2 must be [E, H, I] for w13 [E, 2I, H]");
+        require(I % 16 == 0, "intermediate size must be a multiple of 16");
+        check_quant_rows(x, x_dtype, x_row_stride, rows, row_div, pairs, H, mode);
+        check_routes(ids, ids_dtype, weights, weights_dtype);
+        if (out_pairs == nullptr) check_output(BankGeom{{}, {}, E, H, I}, out, out_dtype, out_row_stride, pairs, top_k);
+        const QuantWorkspace ws = take_quant_workspace(rows, pairs, E, H, I, workspace, workspace_bytes);
+        hipStream_t st = as_stream(stream);
+        quant_group(ids, ids_dtype, pairs, E, ws, status, st);
+        const int max_active = std::min(pairs, E);
+
+        quant_operand(up, x, x_dtype, x_row_stride, rows, H, ws.xq, ws.xs, st);
+        up.row_div = row_div;
+        up.order = ws.order;
+        up.offsets = ws.offsets;
+        up.active = ws.active;
+        up.gateup = 1;
+        up.act = ws.act;
+        up.status = status;
+        dmoe::launch_quant_projection(up, max_active, st);
+
+        quant_operand(dn, ws.act, DMOE_BF16, I, pairs, I, ws.actq, ws.acts, st);
+        dn.row_div = 1;
+        dn.order = ws.order;
+        dn.offsets = ws.offsets;
+        dn.active = ws.active;
+        dn.gateup = 0;
+        dn.weighted = 1;
+        dn.weights = weights;
+        dn.w_dtype = weights_dtype;
+        dn.out = out_pairs ? out_pairs : ws.partial;
+        dn.out_row_stride = H;
+        dn.status = status;
+        dmoe::launch_quant_projection(dn, max_active, st);
+
+        if (out_pairs) {
+            const dmoe::CombineArgs za{out_pairs, H, ids, ids_dtype, E, pairs, 1, H, nullptr, DMOE_F32, 0};
+            dmoe::launch_zero_invalid_rows(za, st);
+        } else {
+            const dmoe::CombineArgs ca{ws.partial, H, ids, ids_dtype, E, pairs / top_k, top_k, H,
+                                       out, out_dtype, out_row_stride};
+            dmoe::launch_combine(ca, st);
+        }
     });
 }
 

@@ -129,6 +129,9 @@ struct PermuteArgs {
     // scratch: rank [pairs] then hist [ceil(pairs / kPermuteBlock), experts]
     int32_t* rank;
     int32_t* hist;
+    // Optional ascending list of the experts that have pairs (nullptr: none):
+    // active[0] = count, active[1 + i] = i-th active expert.
+    int32_t* active;
     // Optional moe_align tile map (tile_expert == nullptr: none): the sorted
     // pairs of each expert cut into block_m-row tiles, expert-major; tile i
     // covers sorted positions [tile_m0[i], min(tile_m0[i] + block_m,
@@ -214,5 +217,51 @@ void launch_fp8_grouped_gateup(const GroupedGateUpArgs& a, hipStream_t stream);
 void launch_fp8_grouped_down(const GroupedDownArgs& a, hipStream_t stream);
 void launch_combine(const CombineArgs& a, hipStream_t stream);
 void launch_zero_invalid_rows(const CombineArgs& a, hipStream_t stream);
+
+// ---------------------------------------------------- packed-integer banks
+
+constexpr int kMaxQuantK = 4096;  // K of a packed projection (rotation rows, register tiles)
+
+struct RotateArgs {
+    const void* x;          // [rows, K] bf16 / fp16 / fp32
+    int x_dtype;            // also the type the rotation is rounded through
+    int64_t x_row_stride;
+    int rows, K;
+    int8_t* q;              // [rows, q_row_stride]
+    int64_t q_row_stride;
+    float* scales;          // [rows]
+};
+
+// One packed projection (w13 or w2) of a mode 0-3 bank over grouped pairs.
+struct QuantProjArgs {
+    int mode;
+    const uint8_t* w;       // packed codes, byte strides
+    const uint8_t* s;       // fp16 scales (0) | fp32 channel scales (1) | aux bytes (2, 3)
+    const int32_t* z;       // mode 0 qzeros [E, K/128, N/8] or nullptr (zero point 8)
+    int64_t w_se, w_sn, s_se, s_sn, z_se;
+    int N, K;
+    // activations: mode 0 bf16 / fp16 rows; modes 1-3 INT8 rows + row scales
+    const void* x;
+    int x_f16;
+    int64_t x_row_stride;   // elements
+    const float* sa;
+    int row_div;            // pair p reads activation row p / row_div
+    // expert grouping (permutation)
+    const int32_t* order;
+    const int32_t* offsets;
+    const int32_t* active;
+    // outputs
+    int gateup;             // 1: act = bf16(bf16(silu(gate)) * up) [pairs, N/2]
+    uint16_t* act;
+    int weighted;           // plain projection: fp32 * route weight, else bf16
+    const void* weights;
+    int w_dtype;
+    void* out;
+    int64_t out_row_stride;
+    int* status;
+};
+
+void launch_rotate_quant(const RotateArgs& a, hipStream_t stream);
+void launch_quant_projection(const QuantProjArgs& a, int max_active, hipStream_t stream);
 
 }  // namespace dmoe

@@ -437,6 +437,20 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(PermuteArgs a) {
     }
     if (t == 0) a.offsets[a.experts] = total;
     for (int64_t x = total + t; x < a.pairs; x += 1024) a.order[x] = -1;  // invalid pairs
+    if (a.active) {  // ascending experts that have pairs
+        __syncthreads();  // wsum is reused
+        const int on = t < a.experts && offs[t + 1] > offs[t];
+        const uint64_t bits = __ballot(on);
+        if (lane == 0) wsum[wave] = __popcll(bits);
+        __syncthreads();
+        int before = __popcll(bits & ((1ull << lane) - 1)), count = 0;
+        for (int w = 0; w < 16; ++w) {
+            if (w < wave) before += wsum[w];
+            count += wsum[w];
+        }
+        if (on) a.active[1 + before] = t;
+        if (t == 0) a.active[0] = count;
+    }
     if (a.tile_expert == nullptr) return;
     // moe_align tile map: one expert per thread, exclusive scan of tile counts
     __syncthreads();  // wsum is reused

@@ -216,6 +216,80 @@ DMOE_API int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dt
                                 int gu_dtype, void* out, int out_dtype, int64_t out_row_stride,
                                 void* workspace, size_t workspace_bytes, int* status, void* stream);
 
+/* ------------------------------------------------ packed-integer expert banks
+ *
+ * One projection bank of a packed mode (the reference's QuantizedStore,
+ * quantized_model.py:26-68), weight rows of K values:
+ *   mode 0 W4A16 GPTQ:   weight int32 [E, N, K/8] (nibble i of word w <-> k = 8w+i),
+ *                        scale fp16 [E, N, K/128]; zero point 8, or 4-bit
+ *                        zeros (GPTQ qzeros [E, K/128, N/8] int32) when set;
+ *   mode 1 INT8 ConvRot: weight int8 [E, N, K], scale fp32 [E, N, 1];
+ *   mode 2 W6A8:         weight int8 [E, N, 3K/4] (K/2 low-nibble bytes, even k
+ *                        low, then K/4 bytes of 2-bit high parts, LSB first),
+ *                        scale = aux uint8 [E, N, K/16 + 4] (E4M3 relative
+ *                        scale per 16 values, then the fp32 channel scale);
+ *   mode 3 W4A8 book:    weight int8 [E, N, K/2], aux uint8 [E, N, K/16 + 8]
+ *                        whose rows 0..15 hold the 16 fp32 levels at byte K/16+4.
+ * Strides are in bytes (zeros: int32 elements per expert).  K is a multiple
+ * of 128 (mode 0) or 256 (modes 1-3), at most 4096; N a multiple of 16. */
+typedef struct DmoeQuantProj {
+    const void* weight;
+    const void* scale;
+    const int32_t* zeros;
+    int64_t weight_stride_e, weight_stride_n;
+    int64_t scale_stride_e, scale_stride_n;
+    int64_t zeros_stride_e;
+    int32_t n, k;
+} DmoeQuantProj;
+
+typedef struct DmoeQuantBank {
+    DmoeQuantProj w13; /* [E, 2I, H]: gate rows 0..I-1, up rows I..2I-1 */
+    DmoeQuantProj w2;  /* [E, H, I] */
+    int32_t experts;
+    int32_t mode;      /* 0..3 as above */
+} DmoeQuantBank;
+
+/* ConvRot activation quantization: rows x [rows, k] (k % 256 == 0) rotated in
+ * 256-blocks by H4^{x4}/16 and rounded through x_dtype, then row INT8:
+ * scales[r] = max(amax, 1e-12)/127, q = clamp(rint(x/scale), +-127) int8
+ * [rows, k].  Replaces rotate_quantize (quantized_kernels.py:30-45). */
+DMOE_API int dmoe_rotate_quantize(const void* x, int x_dtype, int64_t x_row_stride, int rows, int k,
+                                  int8_t* q, float* scales, void* stream);
+
+/* Workspace bytes of a packed-bank call over `rows` activation rows and
+ * `pairs` route pairs (zero-filled once, reused; see dmoe_fp8_workspace_bytes). */
+DMOE_API size_t dmoe_quant_workspace_bytes(const DmoeQuantBank* bank, int rows, int pairs);
+
+/* Workspace bytes of dmoe_quant_projection over `rows` activation rows of K
+ * values and `pairs` route pairs into `experts` experts. */
+DMOE_API size_t dmoe_quant_projection_workspace_bytes(int experts, int k, int rows, int pairs);
+
+/* One packed projection over route pairs: out [pairs, N] (row stride in
+ * elements) = bf16(x_p . dequant(W[ids_p])) (bf16 storage), or with
+ * `weighted` fp32 bf16(...) * weights_p.  Pair p reads activation row
+ * p / row_div (row_div = pairs: one shared row).  Mode 0 takes bf16 / fp16 x;
+ * modes 1-3 rotate and INT8-quantize x first.  Replaces projection()
+ * (quantized_kernels.py:192-214) and its _quant_gemm launch. */
+DMOE_API int dmoe_quant_projection(const DmoeQuantProj* proj, int experts, int mode, const void* x,
+                                   int x_dtype, int64_t x_row_stride, int rows, int row_div,
+                                   const void* ids, int ids_dtype, const void* weights,
+                                   int weights_dtype, int pairs, int weighted, void* out,
+                                   int64_t out_row_stride, void* workspace, size_t workspace_bytes,
+                                   int* status, void* stream);
+
+/* Routed experts of a packed bank: gate/up projection, act =
+ * bf16(bf16(silu(gate)) * up), down projection * route weight (fp32 partials),
+ * then either the slot-order fp32 combine into out [pairs / top_k, H]
+ * (out_dtype) or, with out_pairs != NULL, the ordered partials [pairs, H].
+ * Pair p reads x row p / row_div.  Replaces QuantizedExpertBackend.forward /
+ * forward_pairs / _pairs (quantized_kernels.py:217-260). */
+DMOE_API int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype,
+                                    int64_t x_row_stride, int rows, int row_div, const void* ids,
+                                    int ids_dtype, const void* weights, int weights_dtype, int pairs,
+                                    int top_k, void* out, int out_dtype, int64_t out_row_stride,
+                                    float* out_pairs, void* workspace, size_t workspace_bytes,
+                                    int* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
