@@ -252,6 +252,102 @@ def run_prefill(reps: int = 10):
     return result
 
 
+QUANT_NAMES = {0: "w4a16_asym_g128", 1: "int8_convrot", 2: "w6a8", 3: "w4a8_codebook"}
+
+
+def quant_expert_bytes(mode: int) -> int:
+    """Packed bytes of one expert (w13 + w2 with their scales / aux / zeros)."""
+    total = 0
+    for n, k in ((2 * INTER, HIDDEN), (HIDDEN, INTER)):
+        if mode == 0:
+            total += n * k // 2 + n * (k // 128) * 2 + (k // 128) * (n // 8) * 4
+        elif mode == 1:
+            total += n * k + n * 4
+        elif mode == 2:
+            total += n * k * 3 // 4 + n * (k // 16 + 4)
+        else:
+            total += n * k // 2 + n * (k // 16 + 8)
+    return total
+
+
+def _graph_time_us(fn, steps_per_graph: int, replays: int, stream) -> float:
+    import torch
+
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) * 1e3 / (replays * steps_per_graph)
+
+
+def run_quant(layers: int = 24, window: int = 16, replays: int = 16):
+    """Packed-bank MoE layers (H 2048, 128 experts x I 768, top-8), all
+    experts resident.  Per mode: a hipGraph of `window` decode steps through
+    `layers` distinct layer banks, each (step, layer) with its own seeded
+    top-8 route (T=1), replayed so that `window * replays` steps run; plus
+    the 512-token W4A16 prefill."""
+    import torch
+
+    from drama_moe import router
+    from drama_moe.formats import random_quantized_bank
+    from drama_moe.quantized import QuantizedExpertBackend
+
+    device = torch.device("cuda", 0)
+    stream = torch.cuda.Stream(device)
+    result = {}
+    for mode in (0, 2, 3, 1):
+        n_layers = layers if mode in (2, 3) else LAYERS
+        banks = [random_quantized_bank(mode, EXPERTS, HIDDEN, INTER, asymmetric=mode == 0, device=device,
+                                       generator=torch.Generator(device=device).manual_seed(SEED + 1000 * mode + l))
+                 for l in range(n_layers)]
+        backend = QuantizedExpertBackend(mode)
+        g = torch.Generator(device=device).manual_seed(SEED + 7 * mode)
+        xs = torch.randn(window, n_layers, 1, HIDDEN, device=device, generator=g).bfloat16()
+        logits = torch.randn(window, n_layers, 1, EXPERTS, device=device, generator=g)
+        weights, ids = router.route_topk(logits.reshape(-1, EXPERTS), TOP_K)
+        weights = weights.reshape(window, n_layers, 1, TOP_K)
+        ids = ids.reshape(window, n_layers, 1, TOP_K)
+        outs = torch.empty_like(xs)
+
+        def steps():
+            for t in range(window):
+                for l in range(n_layers):
+                    backend.forward(xs[t, l], ids[t, l], weights[t, l], banks[l], out=outs[t, l])
+
+        layer_us = _graph_time_us(steps, window * n_layers, replays, stream)
+        uniq = [len(set(r)) for r in ids.reshape(-1, TOP_K).cpu().tolist()]
+        layer_bytes = sum(uniq) / len(uniq) * quant_expert_bytes(mode) + 2 * HIDDEN * 2
+        entry = {"layer_us": round(layer_us, 2), "expert_bytes": quant_expert_bytes(mode),
+                 "hbm_frac": round(layer_bytes / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if mode in (2, 3):
+            entry.update({"layers": n_layers, "step_us": round(layer_us * n_layers, 1),
+                          "steps_timed": window * replays})
+        if mode == 0:  # 512-token prefill
+            x = torch.randn(512, HIDDEN, device=device, generator=g).bfloat16()
+            w, i = router.route_topk(torch.randn(512, EXPERTS, device=device, generator=g), TOP_K)
+            out = torch.empty_like(x)
+            prefill_us = _graph_time_us(lambda: backend.forward(x, i, w, banks[0], out=out), 1, 10, stream)
+            flops = 2.0 * 512 * TOP_K * 3 * INTER * HIDDEN
+            nbytes = EXPERTS * quant_expert_bytes(0) + 2 * 512 * HIDDEN * 2
+            entry["prefill_512"] = {"us": round(prefill_us, 1), "tflops": round(flops / prefill_us / 1e6, 1),
+                                    "hbm_frac": round(nbytes / (prefill_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        result[QUANT_NAMES[mode]] = entry
+        del banks
+        torch.cuda.empty_cache()
+    return result
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The reference CPU expert executor (oracle/_ref), one token per call with
     8 route slots over 8 worker threads, block-128 FP8 banks of the same layer
@@ -312,6 +408,7 @@ def main():
     parser.add_argument("--warmup", type=int, default=256)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-prefill", action="store_true")
+    parser.add_argument("--no-quant", action="store_true")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path is built and "
@@ -325,6 +422,8 @@ def main():
     log("gpu", json.dumps(gpu))
     prefill = None if args.no_prefill else run_prefill()
     log("prefill", json.dumps(prefill))
+    quant = None if args.no_quant else run_quant()
+    log("quant", json.dumps(quant))
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log("cpu", json.dumps(cpu))
@@ -354,6 +453,7 @@ def main():
                      "alg_bytes_per_launch": round(gpu["kernel_bytes"])},
         "cpu_baseline": cpu,
         "prefill_fp8": prefill,
+        "packed_banks": quant,
     }
     print(json.dumps(line), flush=True)
 

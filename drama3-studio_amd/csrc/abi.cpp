@@ -789,6 +789,7 @@ int dmoe_rotate_quantize(const void* x, int x_dtype, int64_t x_row_stride, int r
         require(rows >= 0 && k >= 256 && k % 256 == 0 && k <= dmoe::kMaxQuantK,
                 "K must be a multiple of 256, at most 4096");
         require(x_row_stride >= k, "row stride smaller than the row");
+        require(reinterpret_cast<uintptr_t>(q) % 4 == 0, "INT8 output must be 4-byte aligned");
         const dmoe::RotateArgs ra{x, x_dtype, x_row_stride, rows, k, q, k, scales};
         dmoe::launch_rotate_quant(ra, as_stream(stream));
     });

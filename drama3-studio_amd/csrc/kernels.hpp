@@ -94,6 +94,7 @@ struct DownArgs {
 
 constexpr int kMaxPermutePairs = 1 << 20;  // route pairs of one permutation / grouped call
 constexpr int kPermuteBlock = 256;         // pairs per block of the permutation kernels
+constexpr int kSmallPermute = 1024;        // pairs permuted by a single workgroup
 constexpr int kRouteElems = 1024;   // logits one workgroup ranks at a time (tokens * experts)
 constexpr int kRouteTokens = 8;     // tokens one workgroup routes at a time
 

@@ -67,58 +67,83 @@ struct QuantLds {
 // ------------------------------------------------------ rotation + INT8 quant
 
 // Rows x[rows, K] (K % 256 == 0, K <= kMaxQuantK): rot = cd(x_blk @ H256),
-// H256 = H4^{x4} / 16, summed in K order per output (the oracle's order; the
-// +-1 entries are applied as sign flips and the 1/16 once, which is exact);
-// s = max(amax, 1e-12) / 127; q = clamp(rint(rot / s), +-127).  One workgroup
-// per row; thread j owns output j of every 256-block, four blocks at a time
-// (independent accumulators).  Reference: quantized_kernels.py:15-45.
+// H256 = H4^{x4} / 16, then row INT8: s = max(amax, 1e-12) / 127,
+// q = clamp(rint(rot / s), +-127).  Reference: quantized_kernels.py:15-45.
+// The product is taken in the oracle's fixed order: four fp32 stages, one per
+// base-4 digit of the block index, each output ((h0 v0 + h1 v1) + h2 v2) +
+// h3 v3 (h = +-1: exact sign flips), then * 1/16 (exact) and the rounding to
+// the activation type.  A wave owns whole 256-blocks, lane l positions
+// 4l .. 4l+3: digit 0 lives in the lane's registers, digits 1-3 in lane bits
+// (partners fetched with ds_bpermute).  One workgroup per row.
+__device__ __forceinline__ float neg_if(float v, bool neg) { return __uint_as_float(__float_as_uint(v) ^ (neg ? 0x80000000u : 0u)); }
+
 __global__ __launch_bounds__(256) void rotate_quant_kernel(RotateArgs a) {
-    __shared__ float xs[kMaxQuantK];
-    __shared__ float rot[kMaxQuantK];
     __shared__ float red[4];
-    const int row = blockIdx.x, j = threadIdx.x;
+    constexpr int kBlocksPerWave = kMaxQuantK / 256 / 4;
+    const int row = blockIdx.x, lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int chunks = a.K / 256;
-    for (int k = j; k < a.K; k += 256) xs[k] = load_as_f32(a.x, (int64_t)row * a.x_row_stride + k, a.x_dtype);
-    // H4(p, q) = -1 iff p + q == 3, so H4^{x4}(i, j) < 0 iff an odd number of
-    // base-4 digits have i_d == 3 - j_d: XOR of one bit pattern per digit.
-    const int t0 = 3 - (j & 3), t1 = 3 - ((j >> 2) & 3), t2 = 3 - ((j >> 4) & 3), t3 = 3 - ((j >> 6) & 3);
-    const uint32_t p01 = (0x11111111u << t0) ^ (0x000F000Fu << (4 * t1));
-    uint32_t neg[8];
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-        const uint32_t p2 = ((2 * w) % 4 == t2 ? 0x0000FFFFu : 0u) | ((2 * w + 1) % 4 == t2 ? 0xFFFF0000u : 0u);
-        const uint32_t p3 = (w / 2 == t3) ? 0xFFFFFFFFu : 0u;
-        neg[w] = p01 ^ p2 ^ p3;
-    }
-    __syncthreads();
+    float v[kBlocksPerWave][4];
     float amax = 0.0f;
-    for (int c0 = 0; c0 < chunks; c0 += 4) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int i = 0; i < 256; ++i) {
-            const uint32_t flip = ((neg[i / 32] >> (i % 32)) & 1u) << 31;
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                if (c0 + c < chunks) acc[c] += __uint_as_float(__float_as_uint(xs[(c0 + c) * 256 + i]) ^ flip);
+    for (int b = 0; b < kBlocksPerWave; ++b) {
+        const int c = wave + 4 * b;
+        if (c >= chunks) continue;  // wave-uniform
+        const int64_t base = (int64_t)row * a.x_row_stride + c * 256 + 4 * lane;
+        float in[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) in[r] = load_as_f32(a.x, base + r, a.x_dtype);
+        // digit 0: inside the lane, H4(i, j) = -1 iff i + j == 3
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float t = neg_if(in[0], j == 3);
+            t += neg_if(in[1], j == 2);
+            t += neg_if(in[2], j == 1);
+            t += neg_if(in[3], j == 0);
+            v[b][j] = t;
+        }
+        // digits 1..3: lane bits 2(d-1) .. 2(d-1)+1
+#pragma unroll
+        for (int d = 1; d < 4; ++d) {
+            const int shift = 2 * (d - 1);
+            const int jd = (lane >> shift) & 3;
+            const int rest = lane & ~(3 << shift);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float p[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    p[i] = __int_as_float(__builtin_amdgcn_ds_bpermute((rest | (i << shift)) * 4, __float_as_int(v[b][r])));
+                float t = neg_if(p[0], jd == 3);
+                t += neg_if(p[1], jd == 2);
+                t += neg_if(p[2], jd == 1);
+                t += neg_if(p[3], jd == 0);
+                v[b][r] = t;
+            }
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            if (c0 + c < chunks) {
-                const float v = round_through(acc[c] * 0.0625f, a.x_dtype);
-                rot[(c0 + c) * 256 + j] = v;
-                amax = fmaxf(amax, fabsf(v));
-            }
+        for (int r = 0; r < 4; ++r) {
+            v[b][r] = round_through(v[b][r] * 0.0625f, a.x_dtype);
+            amax = fmaxf(amax, fabsf(v[b][r]));
         }
     }
     amax = wave_max_dpp(amax);
-    if (j % kWave == 0) red[j / kWave] = amax;
+    if (lane == 0) red[wave] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float sc = fmaxf(amax, 1e-12f) / 127.0f;
-    for (int c = 0; c < chunks; ++c) {
-        const float t = fminf(fmaxf(__builtin_rintf(rot[c * 256 + j] / sc), -127.0f), 127.0f);
-        a.q[(int64_t)row * a.q_row_stride + c * 256 + j] = (int8_t)(int)t;
+#pragma unroll
+    for (int b = 0; b < kBlocksPerWave; ++b) {
+        const int c = wave + 4 * b;
+        if (c >= chunks) continue;
+        uint32_t packed = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float t = fminf(fmaxf(__builtin_rintf(v[b][r] / sc), -127.0f), 127.0f);
+            packed |= (uint32_t)(uint8_t)(int8_t)(int)t << (8 * r);
+        }
+        *(uint32_t*)(a.q + (int64_t)row * a.q_row_stride + c * 256 + 4 * lane) = packed;
     }
-    if (j == 0) a.scales[row] = sc;
+    if (threadIdx.x == 0) a.scales[row] = sc;
 }
 
 void launch_rotate_quant(const RotateArgs& a, hipStream_t stream) {

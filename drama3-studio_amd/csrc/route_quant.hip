@@ -393,44 +393,11 @@ __global__ __launch_bounds__(kPermuteBlock) void permute_rank_kernel(PermuteArgs
     for (int x = t; x < a.experts; x += kPermuteBlock) a.hist[(int64_t)blockIdx.x * a.experts + x] = hist[x];
 }
 
-// Exclusive scan of the [blocks, experts] histogram table in (expert, block)
-// order, in place: hist[b][e] becomes the first output position of block b's
-// pairs of expert e.
-__global__ __launch_bounds__(1024) void permute_scan_kernel(PermuteArgs a) {
-    __shared__ int wsum[16];
-    __shared__ int offs[kMaxExperts + 1];
+// Shared tail of the permutation kernels (1024 threads): offsets / counts from
+// the per-expert starts `offs` [experts + 1] (LDS), -1 past the valid pairs,
+// the active-expert list and the moe_align tile map.
+__device__ void finish_permute(const PermuteArgs& a, const int* offs, int total, int* wsum) {
     const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
-    const int blocks = (a.pairs + kPermuteBlock - 1) / kPermuteBlock;
-    const int64_t n = (int64_t)blocks * a.experts;
-    const int64_t per = (n + 1023) / 1024;
-    const int64_t lo = min(n, t * per), hi = min(n, lo + per);
-    auto at = [&](int64_t idx) -> int32_t* {  // idx = e * blocks + b
-        return a.hist + (idx % blocks) * a.experts + idx / blocks;
-    };
-    int local = 0;
-    for (int64_t x = lo; x < hi; ++x) local += *at(x);
-    int incl = local;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const int v = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl += v;
-    }
-    if (lane == kWave - 1) wsum[wave] = incl;
-    __syncthreads();
-    int base = incl - local, total = 0;
-    for (int w = 0; w < 16; ++w) {
-        if (w < wave) base += wsum[w];
-        total += wsum[w];
-    }
-    for (int64_t x = lo; x < hi; ++x) {
-        int32_t* p = at(x);
-        const int c = *p;
-        *p = base;
-        if (x % blocks == 0) offs[x / blocks] = base;
-        base += c;
-    }
-    if (t == 0) offs[a.experts] = total;
-    __syncthreads();
     for (int x = t; x < a.experts; x += 1024) {
         a.offsets[x] = offs[x];
         a.counts[x] = offs[x + 1] - offs[x];
@@ -477,6 +444,94 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(PermuteArgs a) {
     for (int x = ttotal + t; x < a.max_tiles; x += 1024) a.tile_expert[x] = -1;
 }
 
+// Exclusive scan of the [blocks, experts] histogram table in (expert, block)
+// order, in place: hist[b][e] becomes the first output position of block b's
+// pairs of expert e.
+__global__ __launch_bounds__(1024) void permute_scan_kernel(PermuteArgs a) {
+    __shared__ int wsum[16];
+    __shared__ int offs[kMaxExperts + 1];
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    const int blocks = (a.pairs + kPermuteBlock - 1) / kPermuteBlock;
+    const int64_t n = (int64_t)blocks * a.experts;
+    const int64_t per = (n + 1023) / 1024;
+    const int64_t lo = min(n, t * per), hi = min(n, lo + per);
+    auto at = [&](int64_t idx) -> int32_t* {  // idx = e * blocks + b
+        return a.hist + (idx % blocks) * a.experts + idx / blocks;
+    };
+    int local = 0;
+    for (int64_t x = lo; x < hi; ++x) local += *at(x);
+    int incl = local;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += v;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int base = incl - local, total = 0;
+    for (int w = 0; w < 16; ++w) {
+        if (w < wave) base += wsum[w];
+        total += wsum[w];
+    }
+    for (int64_t x = lo; x < hi; ++x) {
+        int32_t* p = at(x);
+        const int c = *p;
+        *p = base;
+        if (x % blocks == 0) offs[x / blocks] = base;
+        base += c;
+    }
+    if (t == 0) offs[a.experts] = total;
+    __syncthreads();
+    finish_permute(a, offs, total, wsum);
+}
+
+// Whole permutation in one workgroup for small calls (pairs <= 1024, one per
+// thread): histogram by LDS atomics, scan, stable rank among the earlier pairs
+// of the same expert, scatter, and the shared tail.
+__global__ __launch_bounds__(1024) void permute_small_kernel(PermuteArgs a) {
+    __shared__ int16_t sid[kSmallPermute];
+    __shared__ int hist[kMaxExperts];
+    __shared__ int offs[kMaxExperts + 1];
+    __shared__ int wsum[16];
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    int e = -1;
+    if (t < a.pairs) {
+        const int64_t id = load_id(a.ids, t, a.ids_dtype);
+        if (id >= 0 && id < a.experts) e = (int)id;
+        else raise_status(a.status, kBadExpertId);
+    }
+    sid[t] = (int16_t)e;
+    for (int x = t; x < a.experts; x += 1024) hist[x] = 0;
+    __syncthreads();
+    if (e >= 0) atomicAdd(&hist[e], 1);
+    __syncthreads();
+    // exclusive scan of hist over experts (<= 512: threads 0..511)
+    const int c = t < a.experts ? hist[t] : 0;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += v;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int base = incl - c, total = 0;
+    for (int w = 0; w < 16; ++w) {
+        if (w < wave) base += wsum[w];
+        total += wsum[w];
+    }
+    if (t < a.experts) offs[t] = base;
+    if (t == 0) offs[a.experts] = total;
+    __syncthreads();
+    if (e >= 0) {
+        int r = 0;
+        for (int j = 0; j < t; ++j) r += (int)(sid[j] == e);
+        a.order[offs[e] + r] = t;
+    }
+    __syncthreads();  // wsum is reused by the tail
+    finish_permute(a, offs, total, wsum);
+}
+
 __global__ __launch_bounds__(kPermuteBlock) void permute_scatter_kernel(PermuteArgs a) {
     const int64_t i = (int64_t)blockIdx.x * kPermuteBlock + threadIdx.x;
     if (i >= a.pairs) return;
@@ -492,6 +547,10 @@ size_t permute_scratch_bytes(int64_t pairs, int experts) {
 }
 
 void launch_permute(const PermuteArgs& a, hipStream_t stream) {
+    if (a.pairs <= kSmallPermute) {
+        hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(1024), 0, stream, a);
+        return;
+    }
     const unsigned blocks = (unsigned)((a.pairs + kPermuteBlock - 1) / kPermuteBlock);
     hipLaunchKernelGGL(permute_rank_kernel, dim3(blocks), dim3(kPermuteBlock), 0, stream, a);
     hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, stream, a);

@@ -306,18 +306,34 @@ ORC_API int orc_permute(const int64_t* ids, int64_t pairs, int64_t experts, int3
  * 256-point rotation H4 (x) H4 (x) H4 (x) H4 / 16.
  * Reference: src/drama_low_vram/quantized_kernels.py:30-45 and 52-62. */
 static int h4(int i, int j) { return (i + j == 3) ? -1 : 1; }
-static float h256(int i, int j) {
-    int s = 1;
-    for (int d = 0; d < 4; ++d) { s *= h4(i & 3, j & 3); i >>= 2; j >>= 2; }
-    return (float)s / 16.0f;
+
+/* rotated = round(x[rows, K] reshaped to [-1, 256] @ H256), then row INT8:
+ * s = max(amax, 1e-12) / 127, q = clamp(rint(x / s), -127, 127).
+ * Reference: quantized_kernels.py:15-23 (_row_quant), 30-45 (rotate_quantize),
+ * whose torch.matmul fixes no summation order.  This restatement fixes one:
+ * the product by H4 (x) H4 (x) H4 (x) H4 is taken as four fp32 stages, one per
+ * base-4 digit d = 0..3 of the 256-block index (i = i0 + 4 i1 + 16 i2 + 64 i3),
+ * each output of a stage being ((h0 v0 + h1 v1) + h2 v2) + h3 v3 over that
+ * digit's four inputs in order (h = +-1, exact); then * 1/16 (exact) and the
+ * rounding to the storage type.  x holds the compute-dtype activation values
+ * as fp32; `rot_dtype` is the storage type of the rotated tensor (0 fp32,
+ * 1 bf16, 2 fp16). */
+static void h256_staged(const float* in, float* out) {
+    float a[256], b[256];
+    memcpy(a, in, sizeof(a));
+    for (int d = 0; d < 4; ++d) {
+        const int stride = 1 << (2 * d);
+        for (int p = 0; p < 256; ++p) {
+            const int j = (p / stride) & 3, base = p - j * stride;
+            float t = (float)h4(0, j) * a[base];
+            for (int i = 1; i < 4; ++i) t += (float)h4(i, j) * a[base + i * stride];
+            b[p] = t;
+        }
+        memcpy(a, b, sizeof(a));
+    }
+    for (int p = 0; p < 256; ++p) out[p] = a[p] * 0.0625f;
 }
 
-/* rotated = round_bf16(x[rows, K] reshaped to [-1, 256] @ H256) with an fp32
- * sequential accumulation, then row INT8: s = max(amax, 1e-12) / 127,
- * q = clamp(rint(x / s), -127, 127).
- * Reference: quantized_kernels.py:15-23 (_row_quant), 30-45 (rotate_quantize).
- * x holds the compute-dtype activation values as fp32; `rot_dtype` is the
- * storage type of the rotated tensor (1 bf16, 2 fp16). */
 ORC_API int orc_rotate_quantize(const float* x, int64_t rows, int64_t K, int rot_dtype,
                                 int8_t* q, float* scales, float* rotated_out) {
     if (K % 256) return -1;
@@ -325,12 +341,10 @@ ORC_API int orc_rotate_quantize(const float* x, int64_t rows, int64_t K, int rot
     if (!rot) return -3;
     for (int64_t r = 0; r < rows; ++r) {
         const float* v = x + r * K;
-        for (int64_t c = 0; c < K; c += 256)
-            for (int j = 0; j < 256; ++j) {
-                float acc = 0.0f;
-                for (int i = 0; i < 256; ++i) acc += v[c + i] * h256(i, j);
-                rot[c + j] = round_through(acc, rot_dtype);
-            }
+        for (int64_t c = 0; c < K; c += 256) {
+            h256_staged(v + c, rot + c);
+            for (int j = 0; j < 256; ++j) rot[c + j] = round_through(rot[c + j], rot_dtype);
+        }
         float amax = 0.0f;
         for (int64_t k = 0; k < K; ++k) if (fabsf(rot[k]) > amax) amax = fabsf(rot[k]);
         float s = (amax > 1e-12f ? amax : 1e-12f) / 127.0f;
