@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -41,6 +42,10 @@ int checked(F&& body) {
 }
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Process-wide switch of the single-launch decode (dmoe_set_fused_decode).
+std::atomic<int> g_fused_decode{1};
+bool fused_enabled() { return g_fused_decode.load(std::memory_order_relaxed) != 0; }
 
 bool is_float_dtype(int d) { return d == DMOE_F32 || d == DMOE_BF16 || d == DMOE_F16; }
 bool is_id_dtype(int d) { return d == DMOE_I32 || d == DMOE_I64; }
@@ -94,18 +99,22 @@ BankGeom check_bank(const DmoeFp8Bank* bank) {
 
 struct Fp8Workspace {
     int* counters;
+    int* sync;
     dmoe::Grouping* grouping;
     uint8_t* xq;
     float* xs;
     float* h32;
+    uint64_t* ht;
     uint8_t* hq;
     float* hs;
 };
 
 // Workspace: the arrival counters come first at a fixed size, so one
 // zero-filled workspace serves calls of any pair count and bank geometry;
-// the grouping and the per-call buffers follow.
-constexpr size_t kCounterBytes = (size_t)dmoe::kMaxDecodePairs * (dmoe::kMaxInter / 128) * 4;
+// the grouping and the per-call buffers follow.  The counter region ends with
+// the two grid counters of the fused decode.
+constexpr size_t kArrivalBytes = (size_t)dmoe::kMaxDecodePairs * (dmoe::kMaxInter / 128) * 4;
+constexpr size_t kCounterBytes = kArrivalBytes + 32 * 256;
 
 size_t fp8_workspace_layout(int pairs, int H, int I, char* base, Fp8Workspace* ws) {
     size_t off = 0;
@@ -119,14 +128,17 @@ size_t fp8_workspace_layout(int pairs, int H, int I, char* base, Fp8Workspace* w
     char* xq = take((size_t)pairs * H);
     char* xs = take((size_t)pairs * (H / 128) * 4);
     char* h32 = take((size_t)pairs * I * 4);
+    char* ht = take(pairs <= dmoe::kFusedMaxPairs ? (size_t)pairs * I * 8 : 0);
     char* hq = take((size_t)pairs * I);
     char* hs = take((size_t)pairs * (I / 128) * 4);
     if (ws) {
         ws->counters = reinterpret_cast<int*>(counters);
+        ws->sync = reinterpret_cast<int*>(counters + kArrivalBytes);
         ws->grouping = reinterpret_cast<dmoe::Grouping*>(grouping);
         ws->xq = reinterpret_cast<uint8_t*>(xq);
         ws->xs = reinterpret_cast<float*>(xs);
         ws->h32 = reinterpret_cast<float*>(h32);
+        ws->ht = reinterpret_cast<uint64_t*>(ht);
         ws->hq = reinterpret_cast<uint8_t*>(hq);
         ws->hs = reinterpret_cast<float*>(hs);
     }
@@ -268,12 +280,56 @@ void check_output(const BankGeom& g, void* out, int out_dtype, int64_t out_row_s
     require(top_k >= 1 && pairs % top_k == 0, "pairs must be tokens * top_k");
 }
 
-// The three launches of a whole decode FP8 call (<= 256 pairs).
+// Single-launch decode of a small call (fp8_fused.hip); false when the call
+// does not fit it (nothing enqueued).
+bool fp8_fused_call(const BankGeom& g, const Activations& a, const dmoe::RouteSource& route, const void* weights,
+                    int weights_dtype, int pairs, int top_k, int gu_dtype, void* out, int out_dtype,
+                    int64_t out_row_stride, float* out_pairs, const Fp8Workspace& ws, int* status,
+                    hipStream_t stream) {
+    const int rows = (pairs - 1) / a.row_div + 1;
+    const int route_k = route.logits ? route.top_k : top_k;
+    const int x_esize = a.xq ? 0 : a.x_dtype == DMOE_F32 ? 4 : 2;
+    if (!dmoe::fused_decode_fits(pairs, rows, g.H, g.I, g.experts, route_k, x_esize)) return false;
+    dmoe::FusedDecodeArgs fa{};
+    fa.w13 = g.w13;
+    fa.w2 = g.w2;
+    fa.experts = g.experts;
+    fa.route = route;
+    fa.weights = weights;
+    fa.w_dtype = weights_dtype;
+    fa.pairs = pairs;
+    fa.top_k = top_k;
+    fa.row_div = a.row_div;
+    fa.x = a.x;
+    fa.x_dtype = a.x_dtype;
+    fa.x_row_stride = a.x_row_stride;
+    fa.xq = a.xq;
+    fa.xs = a.xs;
+    fa.xq_row_stride = a.xq_row_stride;
+    fa.xs_row_stride = a.xs_row_stride;
+    fa.rows = rows;
+    fa.x_group = a.x_group;
+    fa.gu_dtype = gu_dtype;
+    fa.ht = ws.ht;
+    fa.sync = ws.sync;
+    fa.out = out;
+    fa.out_dtype = out_dtype;
+    fa.out_row_stride = out_row_stride;
+    fa.out_pairs = out_pairs;
+    fa.status = status;
+    return dmoe::launch_fp8_fused_decode(fa, stream);
+}
+
+// A whole decode FP8 call (<= 256 pairs): one fused launch when it fits,
+// else three launches (prep, gate/up, down).
 void fp8_decode_call(const BankGeom& g, Activations a, const dmoe::RouteSource& route, const void* weights,
                  int weights_dtype, int pairs, int top_k, int gu_dtype, void* out, int out_dtype,
                  int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes, int* status,
                  hipStream_t stream) {
     const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
+    if (fused_enabled() && fp8_fused_call(g, a, route, weights, weights_dtype, pairs, top_k, gu_dtype, out,
+                                          out_dtype, out_row_stride, out_pairs, ws, status, stream))
+        return;
     const bool in_down = down_quantizes(g, pairs);
     launch_prep(g, a, route, pairs, ws, status, stream);
     launch_gate_up(g, a, pairs, gu_dtype, ws.hq, ws.hs, ws, status, stream, !in_down);
@@ -567,6 +623,8 @@ void quant_operand(dmoe::QuantProjArgs& q, const void* x, int x_dtype, int64_t x
 extern "C" {
 
 int dmoe_abi_version(void) { return DMOE_ABI_VERSION; }
+
+int dmoe_set_fused_decode(int enabled) { return g_fused_decode.exchange(enabled != 0 ? 1 : 0); }
 
 const char* dmoe_last_error(void) { return g_last_error.c_str(); }
 

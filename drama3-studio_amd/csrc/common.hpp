@@ -30,6 +30,7 @@ enum StatusBits : int {
     kBadExpertId = 1,     // a route id outside [0, experts): the pair contributes 0
     kNonFinite = 2,       // non-finite activation met by a quantizer
     kTooManyRows = 4,     // a per-expert row count exceeded a kernel limit
+    kSyncTimeout = 8,     // a grid-wide wait of the fused decode gave up (results invalid)
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }

@@ -31,6 +31,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "fp8_util.hpp"
 
 namespace dmoe {
 
@@ -39,54 +40,6 @@ namespace {
 constexpr int kUpWaves = 8, kUpThreads = kUpWaves * kWave;
 constexpr int kDnWaves = 4, kDnThreads = kDnWaves * kWave;
 constexpr int kRowsPerPass = 4;  // activation rows per MFMA pass of the gate/up kernel
-
-__device__ __forceinline__ float proj_scale(const Fp8Proj& p, int e, int n, int kb) {
-    return p.s[(int64_t)e * p.s_se + (int64_t)(n / p.n_div) * p.s_sn + (int64_t)(kb / p.kb_div) * p.s_sk];
-}
-
-__device__ __forceinline__ v8i load32(const uint8_t* p) {
-    const v4i lo = *(const v4i*)p, hi = *(const v4i*)(p + 16);
-    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-// Weight stream: read once per call, marked non-temporal so the streamed bank
-// does not evict the small per-call data (grouping, activations) and code from L2.
-__device__ __forceinline__ v8i load32_stream(const uint8_t* p) {
-    const v4i lo = __builtin_nontemporal_load((const v4i*)p), hi = __builtin_nontemporal_load((const v4i*)(p + 16));
-    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-__device__ __forceinline__ bool finite(float v) { return fabsf(v) <= 3.402823466e38f; }
-
-struct F8 {
-    float v[8];
-};
-
-__device__ __forceinline__ F8 zero8() {
-    F8 r;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r.v[j] = 0.0f;
-    return r;
-}
-
-__device__ __forceinline__ uint64_t encode8(const F8& x, float scale) {
-    uint64_t q = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) q |= (uint64_t)fp8_encode(x.v[j] / scale) << (8 * j);
-    return q;
-}
-
-__device__ __forceinline__ float absmax8(const F8& x, int* status) {
-    float m = 0.0f;
-    bool ok = true;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        m = fmaxf(m, fabsf(x.v[j]));
-        ok = ok && finite(x.v[j]);
-    }
-    if (!ok) raise_status(status, kNonFinite);
-    return m;
-}
 
 // Pairs of active expert `ai` in ascending order into `out` (one whole wave);
 // returns the count.  The pair set is the grouping's bitmask.

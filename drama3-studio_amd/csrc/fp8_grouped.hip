@@ -30,6 +30,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "fp8_util.hpp"
 
 namespace dmoe {
 
@@ -38,22 +39,6 @@ namespace {
 constexpr int kGThreads = 256;
 constexpr int kXcds = 8;
 constexpr int kMaxKb = kMaxHidden / 128;  // 128-column K blocks, gate/up (H) or down (I)
-
-__device__ __forceinline__ float proj_scale(const Fp8Proj& p, int e, int n, int kb) {
-    return p.s[(int64_t)e * p.s_se + (int64_t)(n / p.n_div) * p.s_sn + (int64_t)(kb / p.kb_div) * p.s_sk];
-}
-
-__device__ __forceinline__ v8i load32(const uint8_t* p) {
-    const v4i lo = *(const v4i*)p, hi = *(const v4i*)(p + 16);
-    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-__device__ __forceinline__ v8i load32_stream(const uint8_t* p) {
-    const v4i lo = __builtin_nontemporal_load((const v4i*)p), hi = __builtin_nontemporal_load((const v4i*)(p + 16));
-    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-__device__ __forceinline__ bool finite(float v) { return fabsf(v) <= 3.402823466e38f; }
 
 // Workgroup -> logical tile: XCD x (workgroups x, x + 8, ...) receives the
 // contiguous logical range [x * G / 8, (x + 1) * G / 8).  G is a multiple of 8.

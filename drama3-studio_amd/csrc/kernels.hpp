@@ -205,6 +205,45 @@ struct PrepArgs {
     int* status;
 };
 
+// Single-launch decode (fp8_fused.hip): routing, activation quantization,
+// gate/up + SiLU, hidden quantization, down * route weight and the slot-order
+// combine in one persistent launch of at most one workgroup per CU.
+constexpr int kFusedMaxPairs = 64;     // route pairs of one fused call
+constexpr int kFusedXBytes = 16384;    // FP8 activation rows (rows * H) a workgroup stages
+constexpr int kFusedRawBytes = 32768;  // the same rows as given (bf16 / fp16 / fp32)
+constexpr int kFusedHBytes = 49152;    // FP8 hidden (pairs * I) a workgroup stages
+constexpr int kFusedMaxH = 2048;
+constexpr int kFusedMaxI = 1024;
+
+struct FusedDecodeArgs {
+    Fp8Proj w13, w2;
+    int experts;
+    RouteSource route;          // caller ids (route.ids) or router logits (route.logits)
+    const void* weights;        // caller route weights [pairs] when routing from ids
+    int w_dtype;
+    int pairs, top_k, row_div;  // pair p reads activation row p / row_div
+    const void* x;              // raw activation rows ...
+    int x_dtype;
+    int64_t x_row_stride;
+    const uint8_t* xq;          // ... or FP8 rows and scales quantized by the caller
+    const float* xs;
+    int64_t xq_row_stride, xs_row_stride;
+    int rows, x_group;
+    int gu_dtype;
+    uint64_t* ht;               // [pairs, I] hand-off words: fp32 h bits | call epoch << 32
+    int* sync;                  // 32 64-bit call counters, 256 bytes apart, zero at first use
+    void* out;                  // [pairs / top_k, H] layer output ...
+    int out_dtype;
+    int64_t out_row_stride;
+    float* out_pairs;           // ... or [pairs, H] ordered fp32 partials when non-null
+    int* status;
+};
+
+bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize);
+// Launches the fused decode; false (nothing enqueued) when the device cannot
+// hold the grid the kernel needs.
+bool launch_fp8_fused_decode(const FusedDecodeArgs& a, hipStream_t stream);
+
 void launch_moe_prep(const PrepArgs& a, hipStream_t stream);
 int quantize_blocks(const QuantArgs& a);
 void launch_fp8_gateup_decode(const GateUpArgs& a, int max_active, hipStream_t stream);

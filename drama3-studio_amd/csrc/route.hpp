@@ -1,0 +1,122 @@
+// Workgroup router shared by the router, decode-prep and fused decode kernels.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace dmoe {
+
+// Router for a chunk of tokens by a whole workgroup, without serial rounds:
+// rank(t, e) = #{e' : l[e'] > l[e] or (l[e'] == l[e] and e' < e)}; the
+// experts of rank < k are the winners, rank = router slot.  Each logit gets a
+// unique 64-bit key (order-preserving logit bits, then the inverted expert
+// index), so the rank is a branch-free count of larger keys.  Softmax max and
+// sum are workgroup reductions; weights = exp(l - max) / sum of the winners,
+// renormalised by their slot-order sum.  Reference: backbone_graph.py:317-323.
+// Results: ids_lds[t * k + slot] (local token t), when `wts_lds` is set the
+// route weights rounded through the weights dtype at wts_lds[t * k + slot],
+// and -- when `publish` -- the global ids / weights of token t0 + t.
+struct RouteScratch {
+    alignas(16) uint64_t key[kRouteElems];  // (ordered logit << 32) | ~expert; read 16 bytes at a time
+    float lv[kRouteElems];      // logits of the chunk
+    float ex[kRouteElems];      // exp(l - max)
+    float red[16][kRouteTokens];
+    float pk[kRouteTokens][64];
+    int ik[kRouteTokens][64];
+};
+
+// Order-preserving map of a float to uint32 (-0 and +0 compare equal).
+__device__ __forceinline__ uint32_t ordered_bits(float v) {
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int THREADS>
+__device__ void block_route(RouteScratch& rs, const RouteSource& src, int t0, int tcount, int experts,
+                            int16_t* ids_lds, bool publish, float* wts_lds = nullptr) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    constexpr int kWavesB = THREADS / kWave;
+    const int elems = tcount * experts;
+    for (int i = threadIdx.x; i < elems; i += THREADS) {
+        const int t = i / experts, e = i % experts;
+        const float l = src.logits[(int64_t)(t0 + t) * src.logits_row_stride + e];
+        rs.lv[i] = l;
+        rs.key[i] = ((uint64_t)ordered_bits(l) << 32) | (uint32_t)~e;
+    }
+    __syncthreads();
+    // per-token max: one wave per token
+    for (int t = wave; t < tcount; t += kWavesB) {
+        float m = -INFINITY;
+#pragma unroll 4
+        for (int e = lane; e < experts; e += kWave) m = fmaxf(m, rs.lv[t * experts + e]);
+        m = wave_max_dpp(m);
+        if (lane == 0) rs.red[0][t] = m;
+    }
+    __syncthreads();
+    // ranks: TPE threads share one element's comparisons (neighbour lanes)
+    const int tpe = elems * 4 <= THREADS ? 4 : elems * 2 <= THREADS ? 2 : 1;
+    const int sub = threadIdx.x % tpe;
+    for (int base = 0; base < elems; base += THREADS / tpe) {
+        const int i = base + threadIdx.x / tpe;
+        const bool live = i < elems;
+        const int t = live ? i / experts : 0, e = live ? i % experts : 0;
+        const uint64_t mine = live ? rs.key[i] : ~0ull;
+        int rank = 0;
+        if (live) {
+            // this thread's contiguous share of the row, 8 keys per step
+            const uint64_t* row = rs.key + t * experts;
+            const int per = (experts + tpe - 1) / tpe;
+            const int o0 = sub * per, o1 = min(experts, o0 + per);
+            int o = o0;
+            if (((t * experts + o0) & 1) == 0) {
+                for (; o + 8 <= o1; o += 8) {
+                    const v4i q0 = *(const v4i*)(row + o), q1 = *(const v4i*)(row + o + 2);
+                    const v4i q2 = *(const v4i*)(row + o + 4), q3 = *(const v4i*)(row + o + 6);
+                    const v4i q[4] = {q0, q1, q2, q3};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint64_t k0 = ((uint64_t)(uint32_t)q[j][1] << 32) | (uint32_t)q[j][0];
+                        const uint64_t k1 = ((uint64_t)(uint32_t)q[j][3] << 32) | (uint32_t)q[j][2];
+                        rank += (int)(k0 > mine) + (int)(k1 > mine);
+                    }
+                }
+            }
+            for (; o < o1; ++o) rank += (int)(row[o] > mine);
+        }
+        if (tpe >= 2) rank += __builtin_bit_cast(int, dpp_f32<kDppXor1>(__builtin_bit_cast(float, rank)));
+        if (tpe >= 4) rank += __builtin_bit_cast(int, dpp_f32<kDppXor2>(__builtin_bit_cast(float, rank)));
+        if (live && sub == 0) {
+            const float x = expf(rs.lv[i] - rs.red[0][t]);
+            rs.ex[i] = x;
+            if (rank < src.top_k) {
+                rs.ik[t][rank] = e;
+                rs.pk[t][rank] = x;  // divided by the sum below
+            }
+        }
+    }
+    __syncthreads();
+    // per-token sum of exp: one wave per token
+    for (int t = wave; t < tcount; t += kWavesB) {
+        float sum = 0.0f;
+#pragma unroll 4
+        for (int e = lane; e < experts; e += kWave) sum += rs.ex[t * experts + e];
+        sum = wave_sum_dpp(sum);
+        // winners: p = exp / sum, then the slot-order renormalisation
+        const float p = lane < src.top_k ? rs.pk[t][lane] / sum : 0.0f;
+        float wtot = 0.0f;
+        for (int j = 0; j < src.top_k; ++j) wtot += readlane_f32(p, j);
+        if (lane < src.top_k) {
+            const int id = rs.ik[t][lane];
+            const float w = src.renormalize ? p / wtot : p;
+            ids_lds[t * src.top_k + lane] = (int16_t)id;
+            if (wts_lds) wts_lds[t * src.top_k + lane] = round_through(w, src.w_dtype);
+            if (publish) {
+                src.ids_out[(int64_t)(t0 + t) * src.top_k + lane] = id;
+                store_from_f32(src.weights_out, (int64_t)(t0 + t) * src.top_k + lane, src.w_dtype, w);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+}  // namespace dmoe

@@ -4,186 +4,10 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "fp8_util.hpp"
+#include "route.hpp"
 
 namespace dmoe {
-
-namespace {
-
-__device__ __forceinline__ bool finite(float v) { return fabsf(v) <= 3.402823466e38f; }
-
-struct F8 {
-    float v[8];
-};
-
-__device__ __forceinline__ F8 load8(const void* x, int64_t i, int dtype) {
-    F8 r;
-    if (dtype == kF32) {
-        const v4f a = *(const v4f*)((const float*)x + i), b = *(const v4f*)((const float*)x + i + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            r.v[j] = a[j];
-            r.v[4 + j] = b[j];
-        }
-    } else {
-        const v4i w = *(const v4i*)((const uint16_t*)x + i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t u = (uint32_t)w[j];
-            if (dtype == kBF16) {
-                r.v[2 * j] = __uint_as_float(u << 16);
-                r.v[2 * j + 1] = __uint_as_float(u & 0xFFFF0000u);
-            } else {
-                r.v[2 * j] = f16_to_f32((uint16_t)(u & 0xFFFFu));
-                r.v[2 * j + 1] = f16_to_f32((uint16_t)(u >> 16));
-            }
-        }
-    }
-    return r;
-}
-
-// E4M3 bytes of v / scale (true division), packed little-endian.
-__device__ __forceinline__ uint64_t encode8(const F8& x, float scale) {
-    uint64_t q = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) q |= (uint64_t)fp8_encode(x.v[j] / scale) << (8 * j);
-    return q;
-}
-
-__device__ __forceinline__ float absmax8(const F8& x, int* status) {
-    float m = 0.0f;
-    bool ok = true;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        m = fmaxf(m, fabsf(x.v[j]));
-        ok = ok && finite(x.v[j]);
-    }
-    if (!ok) raise_status(status, kNonFinite);
-    return m;
-}
-
-// One DPP step of a (value desc, index asc) argmax within 16-lane rows.
-template <int CTRL>
-__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
-    const float ov = dpp_f32<CTRL>(bv);
-    const int oi = dpp_i32<CTRL>(bi);
-    if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-    }
-}
-// Router for a chunk of tokens by a whole workgroup, without serial rounds:
-// rank(t, e) = #{e' : l[e'] > l[e] or (l[e'] == l[e] and e' < e)}; the
-// experts of rank < k are the winners, rank = router slot.  Each logit gets a
-// unique 64-bit key (order-preserving logit bits, then the inverted expert
-// index), so the rank is a branch-free count of larger keys.  Softmax max and
-// sum are workgroup reductions; weights = exp(l - max) / sum of the winners,
-// renormalised by their slot-order sum.  Reference: backbone_graph.py:317-323.
-// Results: ids_lds[t * k + slot] (local token t), and -- when `publish` -- the
-// global ids / weights of token t0 + t.
-struct RouteScratch {
-    uint64_t key[kRouteElems];  // (ordered logit << 32) | ~expert
-    float lv[kRouteElems];      // logits of the chunk
-    float ex[kRouteElems];      // exp(l - max)
-    float red[16][kRouteTokens];
-    float pk[kRouteTokens][64];
-    int ik[kRouteTokens][64];
-};
-
-// Order-preserving map of a float to uint32 (-0 and +0 compare equal).
-__device__ __forceinline__ uint32_t ordered_bits(float v) {
-    const uint32_t u = __float_as_uint(v + 0.0f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-template <int THREADS>
-__device__ void block_route(RouteScratch& rs, const RouteSource& src, int t0, int tcount, int experts,
-                            int16_t* ids_lds, bool publish) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    constexpr int kWavesB = THREADS / kWave;
-    const int elems = tcount * experts;
-    for (int i = threadIdx.x; i < elems; i += THREADS) {
-        const int t = i / experts, e = i % experts;
-        const float l = src.logits[(int64_t)(t0 + t) * src.logits_row_stride + e];
-        rs.lv[i] = l;
-        rs.key[i] = ((uint64_t)ordered_bits(l) << 32) | (uint32_t)~e;
-    }
-    __syncthreads();
-    // per-token max: one wave per token
-    for (int t = wave; t < tcount; t += kWavesB) {
-        float m = -INFINITY;
-#pragma unroll 4
-        for (int e = lane; e < experts; e += kWave) m = fmaxf(m, rs.lv[t * experts + e]);
-        m = wave_max_dpp(m);
-        if (lane == 0) rs.red[0][t] = m;
-    }
-    __syncthreads();
-    // ranks: TPE threads share one element's comparisons (neighbour lanes)
-    const int tpe = elems * 4 <= THREADS ? 4 : elems * 2 <= THREADS ? 2 : 1;
-    const int sub = threadIdx.x % tpe;
-    for (int base = 0; base < elems; base += THREADS / tpe) {
-        const int i = base + threadIdx.x / tpe;
-        const bool live = i < elems;
-        const int t = live ? i / experts : 0, e = live ? i % experts : 0;
-        const uint64_t mine = live ? rs.key[i] : ~0ull;
-        int rank = 0;
-        if (live) {
-            // this thread's contiguous share of the row, 8 keys per step
-            const uint64_t* row = rs.key + t * experts;
-            const int per = (experts + tpe - 1) / tpe;
-            const int o0 = sub * per, o1 = min(experts, o0 + per);
-            int o = o0;
-            if (((t * experts + o0) & 1) == 0) {
-                for (; o + 8 <= o1; o += 8) {
-                    const v4i q0 = *(const v4i*)(row + o), q1 = *(const v4i*)(row + o + 2);
-                    const v4i q2 = *(const v4i*)(row + o + 4), q3 = *(const v4i*)(row + o + 6);
-                    const v4i q[4] = {q0, q1, q2, q3};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint64_t k0 = ((uint64_t)(uint32_t)q[j][1] << 32) | (uint32_t)q[j][0];
-                        const uint64_t k1 = ((uint64_t)(uint32_t)q[j][3] << 32) | (uint32_t)q[j][2];
-                        rank += (int)(k0 > mine) + (int)(k1 > mine);
-                    }
-                }
-            }
-            for (; o < o1; ++o) rank += (int)(row[o] > mine);
-        }
-        if (tpe >= 2) rank += __builtin_bit_cast(int, dpp_f32<kDppXor1>(__builtin_bit_cast(float, rank)));
-        if (tpe >= 4) rank += __builtin_bit_cast(int, dpp_f32<kDppXor2>(__builtin_bit_cast(float, rank)));
-        if (live && sub == 0) {
-            const float x = expf(rs.lv[i] - rs.red[0][t]);
-            rs.ex[i] = x;
-            if (rank < src.top_k) {
-                rs.ik[t][rank] = e;
-                rs.pk[t][rank] = x;  // divided by the sum below
-            }
-        }
-    }
-    __syncthreads();
-    // per-token sum of exp: one wave per token
-    for (int t = wave; t < tcount; t += kWavesB) {
-        float sum = 0.0f;
-#pragma unroll 4
-        for (int e = lane; e < experts; e += kWave) sum += rs.ex[t * experts + e];
-        sum = wave_sum_dpp(sum);
-        // winners: p = exp / sum, then the slot-order renormalisation
-        const float p = lane < src.top_k ? rs.pk[t][lane] / sum : 0.0f;
-        float wtot = 0.0f;
-        for (int j = 0; j < src.top_k; ++j) wtot += readlane_f32(p, j);
-        if (lane < src.top_k) {
-            const int id = rs.ik[t][lane];
-            ids_lds[t * src.top_k + lane] = (int16_t)id;
-            if (publish) {
-                src.ids_out[(int64_t)(t0 + t) * src.top_k + lane] = id;
-                store_from_f32(src.weights_out, (int64_t)(t0 + t) * src.top_k + lane, src.w_dtype,
-                               src.renormalize ? p / wtot : p);
-            }
-        }
-    }
-    __syncthreads();
-}
-
-
-}  // namespace
 
 // ------------------------------------------------------------ FP8 quantizers
 

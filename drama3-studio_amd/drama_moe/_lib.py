@@ -21,6 +21,8 @@ _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16,
 
 STATUS_BAD_EXPERT_ID = 1
 STATUS_NON_FINITE = 2
+STATUS_TOO_MANY_ROWS = 4
+STATUS_SYNC_TIMEOUT = 8
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -49,6 +51,7 @@ _L = ctypes.c_int64
 
 _SIGNATURES = {
     "dmoe_abi_version": ([], _I),
+    "dmoe_set_fused_decode": ([_I], _I),
     "dmoe_last_error": ([], ctypes.c_char_p),
     "dmoe_decode_fp8": ([_P, _P, _L, _P], _I),
     "dmoe_fp8_quantize": ([_P, _I, _L, _I, _I, _I, _P, _P, _P, _P], _I),

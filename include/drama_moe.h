@@ -40,7 +40,8 @@ enum { DMOE_F32 = 0, DMOE_BF16 = 1, DMOE_F16 = 2, DMOE_I32 = 3, DMOE_I64 = 4 };
 enum {
     DMOE_STATUS_BAD_EXPERT_ID = 1, /* route id outside [0, experts): that pair contributes 0 */
     DMOE_STATUS_NON_FINITE = 2,    /* non-finite value met by an FP8 quantizer */
-    DMOE_STATUS_TOO_MANY_ROWS = 4
+    DMOE_STATUS_TOO_MANY_ROWS = 4,
+    DMOE_STATUS_SYNC_TIMEOUT = 8   /* the single-launch decode's grid-wide wait gave up: outputs invalid */
 };
 
 /* One FP8 E4M3 projection bank: weight [E, N, K] with K contiguous (row and
@@ -68,6 +69,18 @@ typedef struct DmoeFp8Bank {
 /* ABI version (DMOE_ABI_VERSION).  Replaces drama_native_abi
  * (native/include/drama_native.h:16; runtime.cpp:288). */
 DMOE_API int dmoe_abi_version(void);
+
+/* Process-wide switch of the single-launch decode (default on): decode calls
+ * of at most 64 route pairs whose activation rows (rows * H <= 16 KiB) and
+ * hidden (pairs * I <= 48 KiB) fit run as ONE persistent launch of one
+ * workgroup per CU that routes, projects and combines with a grid-wide
+ * hand-off inside; 0 selects the three-launch decode for every call (A/B
+ * measurement).  Returns the previous setting.  The fused launch occupies
+ * every CU and waits on its own workgroups: work on other streams of the
+ * same device delays it, and a wait that exceeds 200 ms gives up with
+ * DMOE_STATUS_SYNC_TIMEOUT.  No counterpart in the reference (its decode is
+ * per-route-slot Triton launches, fp8_decode.py:114-147). */
+DMOE_API int dmoe_set_fused_decode(int enabled);
 
 /* Last error message of the calling thread.  Replaces drama_native_error
  * (native/include/drama_native.h:19; runtime.cpp:290). */

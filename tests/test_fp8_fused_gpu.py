@@ -1,0 +1,148 @@
+"""The single-launch decode (one persistent kernel per call) against the
+three-launch decode and the oracle.
+
+The two decodes share the arithmetic of the contract step by step (FP8
+activation groups, per-128-block fma chains, cross-wave sums in wave order,
+gate/up rounding, SiLU, FP8 hidden groups, the down K chain in one wave, the
+slot-order combine), so their outputs must be bit-identical; both must also be
+within the 2e-2 bar of the oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import print_case
+from drama_moe import _lib, fp8_decode, fp8_moe
+from drama_moe.formats import random_fp8_bank
+from drama_moe.offload import HipExpertBackend
+from oracle import oracle as orc
+from test_fp8_gpu import TOL, _layer_case, oracle_banks, rel_inf, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def decode_mode():
+    lib = _lib.library()
+
+    def set_mode(fused: bool) -> None:
+        lib.dmoe_set_fused_decode(1 if fused else 0)
+
+    yield set_mode
+    lib.dmoe_set_fused_decode(1)
+
+
+def both(decode_mode, fn):
+    decode_mode(True)
+    fused = fn()
+    torch.cuda.synchronize()
+    decode_mode(False)
+    staged = fn()
+    torch.cuda.synchronize()
+    decode_mode(True)
+    return fused, staged
+
+
+@pytest.mark.parametrize("experts,hidden,inter,tokens,top_k,layout,dtype,x_group", [
+    (128, 2048, 768, 1, 8, "channel", torch.bfloat16, 128),   # the decode benchmark layer
+    (128, 2048, 768, 1, 8, "block", torch.bfloat16, 128),
+    (32, 2048, 768, 4, 8, "block", torch.bfloat16, 128),
+    (64, 2048, 768, 8, 8, "channel", torch.bfloat16, 128),     # 64 pairs: the fused limit
+    (32, 2048, 768, 4, 8, "channel", torch.bfloat16, "token"),
+    (16, 1024, 512, 3, 4, "block", torch.float16, 128),
+    (8, 256, 256, 2, 8, "block", torch.float32, 128),
+    (1, 2048, 1024, 1, 1, "channel", torch.bfloat16, 128),     # single expert, I 1024
+    (8, 4096, 512, 1, 4, "block", torch.bfloat16, 128),        # H 4096: three-launch in both modes
+    (512, 1024, 256, 2, 8, "channel", torch.bfloat16, 128),    # 512 experts
+    (16, 256, 512, 64, 1, "block", torch.bfloat16, 128),       # 64 tokens, top-1
+])
+def test_fused_equals_three_launch_and_oracle(cuda, decode_mode, experts, hidden, inter, tokens, top_k, layout,
+                                              dtype, x_group):
+    print_case("fused vs staged", experts, hidden, inter, tokens, top_k, layout, dtype, x_group)
+    group = 128 if x_group == 128 else hidden
+    staged, x, ids, weights, expected = _layer_case(cuda, experts, hidden, inter, tokens, top_k, layout, dtype,
+                                                    31337 + tokens * 7 + experts, x_group=group,
+                                                    bank_on_device=experts * hidden * inter > (1 << 26))
+    backend = HipExpertBackend(x_group=x_group)
+    fused, three = both(decode_mode, lambda: backend.forward(x, ids, weights, staged))
+    assert torch.equal(fused, three)
+    assert rel_inf(fused.float().cpu().numpy(), expected) < TOL
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 8])
+def test_fused_router_layer_equals_three_launch(cuda, decode_mode, tokens):
+    print_case("fused routed layer", tokens)
+    g = torch.Generator().manual_seed(777 + tokens)
+    staged = to_device(random_fp8_bank(128, 2048, 768, layout="channel", generator=g), cuda)
+    x = torch.randn(tokens, 2048, generator=g).bfloat16().to(cuda)
+    logits = torch.randn(tokens, 128, generator=g).to(cuda)
+    backend = HipExpertBackend()
+    (fo, fw, fi), (so, sw, si) = both(decode_mode, lambda: backend.forward_routed(x, logits, 8, staged))
+    assert torch.equal(fi, si) and torch.equal(fw, sw)
+    assert torch.equal(fo, so)
+    eids, _ = orc.route_topk(logits.cpu().numpy(), 8)
+    np.testing.assert_array_equal(fi.cpu().numpy(), eids)
+
+
+def test_fused_pairs_shared_row_and_quantized_handoff(cuda, decode_mode):
+    print_case("fused pairs")
+    g = torch.Generator().manual_seed(4040)
+    staged = to_device(random_fp8_bank(16, 2048, 768, generator=g), cuda)
+    x = torch.randn(1, 2048, generator=g).bfloat16().to(cuda)
+    ids = torch.tensor([3, 9, 3, 0, 15, 2], device=cuda)
+    weights = torch.softmax(torch.randn(6, generator=g), -1).to(cuda)
+    backend = HipExpertBackend()
+    fused, three = both(decode_mode, lambda: backend.forward_pairs(x.expand(6, -1), ids[:, None], weights[:, None],
+                                                                   staged))
+    assert torch.equal(fused, three)
+    b13, b2 = oracle_banks(staged)
+    ref = orc.fp8_expert_pairs(b13, b2, x[0].float().cpu().numpy(), ids.cpu().numpy(), weights.cpu().numpy())
+    assert rel_inf(fused.cpu().numpy(), ref) < TOL
+    q, s = fp8_moe.quantize_groups(fp8_moe.quant_kernel, x, 2048)
+    hf, hs = both(decode_mode, lambda: fp8_decode.quantized_pairs(fp8_moe, q, s, ids, weights, staged))
+    assert torch.equal(hf, hs) and torch.equal(hf, fused)
+
+
+def test_fused_invalid_ids_contribute_zero_and_raise_status(cuda, decode_mode):
+    print_case("fused invalid ids")
+    staged = to_device(random_fp8_bank(4, 256, 256, generator=torch.Generator().manual_seed(3)), cuda)
+    backend = HipExpertBackend()
+    backend.status(cuda)
+    x = torch.randn(1, 256, device=cuda).bfloat16()
+    good = backend.forward(x, torch.tensor([[2, 1]], device=cuda), torch.tensor([[0.5, 0.5]], device=cuda), staged)
+    assert backend.status(cuda) == 0
+    bad = backend.forward(x, torch.tensor([[2, 1, 7]], device=cuda), torch.tensor([[0.5, 0.5, 0.5]], device=cuda),
+                          staged)
+    assert backend.status(cuda) & _lib.STATUS_BAD_EXPERT_ID
+    torch.testing.assert_close(bad, good, rtol=0, atol=0)
+
+
+def test_fused_repeated_calls_rearm_the_grid_counters(cuda):
+    """Hundreds of back-to-back single-launch calls (eager and graph-replayed)
+    stay identical: the grid counters return to zero after every call and no
+    wait times out."""
+    print_case("fused repeated calls")
+    g = torch.Generator().manual_seed(99)
+    staged = to_device(random_fp8_bank(128, 2048, 768, layout="channel", generator=g), cuda)
+    backend = HipExpertBackend()
+    backend.status(cuda)
+    x = torch.randn(1, 2048, generator=g).bfloat16().to(cuda)
+    logits = torch.randn(1, 128, generator=g).to(cuda)
+    first, _, _ = backend.forward_routed(x, logits, 8, staged)
+    out = torch.empty_like(x)
+    for _ in range(200):
+        backend.forward_routed(x, logits, 8, staged, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, first)
+    stream = torch.cuda.Stream(cuda)
+    stream.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(16):
+            backend.forward_routed(x, logits, 8, staged, out=out)
+    for _ in range(8):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+    assert backend.status(cuda) == 0
