@@ -289,7 +289,8 @@ bool fp8_fused_call(const BankGeom& g, const Activations& a, const dmoe::RouteSo
     const int rows = (pairs - 1) / a.row_div + 1;
     const int route_k = route.logits ? route.top_k : top_k;
     const int x_esize = a.xq ? 0 : a.x_dtype == DMOE_F32 ? 4 : 2;
-    if (!dmoe::fused_decode_fits(pairs, rows, g.H, g.I, g.experts, route_k, x_esize)) return false;
+    const int routed_tokens = route.logits ? pairs / route.top_k : 0;
+    if (!dmoe::fused_decode_fits(pairs, rows, g.H, g.I, g.experts, route_k, x_esize, routed_tokens)) return false;
     dmoe::FusedDecodeArgs fa{};
     fa.w13 = g.w13;
     fa.w2 = g.w2;

@@ -70,6 +70,9 @@ struct FzLds {
     int plist[kFusedMaxPairs];        // pairs grouped by active expert, ascending
     int prow[kFusedMaxPairs];         // activation row of each plist entry (pair / row_div)
     int ucoord[kMaxUnitDepth][3];     // (first column, pair-list start, pair count) of each batch unit
+    alignas(16) uint32_t rkey[kRouteElems];  // ordered logit bits of every (token, expert)
+    float rmax[kFusedMaxPairs], rsum[kFusedMaxPairs];  // softmax max / sum per token
+    float rp[kFusedMaxPairs];         // softmax probability of each routed slot
     int num_active;
     uint32_t epoch;
     alignas(16) uint8_t xq[kFusedXBytes];   // FP8 activation rows [rows, H]
@@ -94,17 +97,6 @@ __device__ __forceinline__ uint64_t load_coherent_u64(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wave-wide maximum of a 32-bit unsigned value (uniform result).
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)dpp_i32<kDppXor1>((int)v));
-    v = max(v, (uint32_t)dpp_i32<kDppXor2>((int)v));
-    v = max(v, (uint32_t)dpp_i32<kDppHalfMirror>((int)v));
-    v = max(v, (uint32_t)dpp_i32<kDppMirror>((int)v));
-    const uint32_t a = __builtin_amdgcn_readlane((int)v, 0), b = __builtin_amdgcn_readlane((int)v, 16);
-    const uint32_t c = __builtin_amdgcn_readlane((int)v, 32), d = __builtin_amdgcn_readlane((int)v, 48);
-    return max(max(a, b), max(c, d));
-}
-
 constexpr int kRouteJ = kMaxExperts / kWave;  // logits per lane (experts l + 64 j)
 
 __device__ __forceinline__ void wave_route_load(const RouteSource& src, int t, int experts, float* l) {
@@ -114,80 +106,6 @@ __device__ __forceinline__ void wave_route_load(const RouteSource& src, int t, i
     for (int j = 0; j < kRouteJ; ++j) {
         const int e = lane + j * kWave;
         l[j] = e < experts ? row[e] : 0.0f;
-    }
-}
-
-// Router of one token by one wave (lane l holds experts l + 64 j).  Same
-// order statistics and float operations as block_route (route.hpp), so ids,
-// order and weights are bit-identical to the router kernel: max by fmaxf over
-// j then the DPP wave max; exp(l - max) summed over j then the DPP wave sum;
-// slot r = the r-th largest logit in (ordered bits desc, expert asc) order:
-// one wave-wide maximum of the 32-bit ordered bits per slot, ties to the
-// lowest expert index by ballot (e = lane + 64 j grows with (j, lane));
-// weights p = exp / sum renormalized by their slot-order sum and rounded
-// through the weights type.
-__device__ void wave_route_token(const RouteSource& src, int t, int experts, const float* l, int16_t* sid, float* wt,
-                                 bool publish) {
-    constexpr int kJ = kRouteJ;
-    const int lane = threadIdx.x % kWave;
-    const int ej = (experts + kWave - 1) / kWave;
-    uint32_t ob[kJ];
-    uint32_t alive = 0;
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-        const bool ok = lane + j * kWave < experts;
-        ob[j] = ordered_bits(l[j]);
-        alive |= ok ? 1u << j : 0u;
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kJ; ++j)
-        if (j < ej && lane + j * kWave < experts) m = fmaxf(m, l[j]);
-    m = wave_max_dpp(m);
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kJ; ++j)
-        if (j < ej && lane + j * kWave < experts) sum += expf(l[j] - m);
-    sum = wave_sum_dpp(sum);
-    int my_id = 0;
-    float my_logit = 0.0f;
-    for (int r = 0; r < src.top_k; ++r) {
-        uint32_t best = 0;
-#pragma unroll
-        for (int j = 0; j < kJ; ++j)
-            if (j < ej && ((alive >> j) & 1u)) best = max(best, ob[j]);
-        best = wave_max_u32(best);
-        int id = 0;
-        float lv = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-            if (j < ej) {
-                const uint64_t hit = __ballot(((alive >> j) & 1u) && ob[j] == best);
-                if (hit) {
-                    const int wl = __builtin_ctzll(hit);
-                    id = wl + j * kWave;
-                    lv = readlane_f32(l[j], wl);
-                    if (lane == wl) alive &= ~(1u << j);
-                    break;
-                }
-            }
-        }
-        if (lane == r) {
-            my_id = id;
-            my_logit = lv;
-        }
-    }
-    const float p = lane < src.top_k ? expf(my_logit - m) / sum : 0.0f;
-    float wtot = 0.0f;
-    for (int j = 0; j < src.top_k; ++j) wtot += readlane_f32(p, j);
-    if (lane < src.top_k) {
-        const float w = src.renormalize ? p / wtot : p;
-        sid[t * src.top_k + lane] = (int16_t)my_id;
-        wt[t * src.top_k + lane] = round_through(w, src.w_dtype);
-        if (publish) {
-            src.ids_out[(int64_t)t * src.top_k + lane] = my_id;
-            store_from_f32(src.weights_out, (int64_t)t * src.top_k + lane, src.w_dtype, w);
-        }
     }
 }
 
@@ -217,10 +135,6 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     // quantization unit.  Units are dealt to 16-lane groups from the last
     // wave down, so at batch 1 the routing wave quantizes nothing.
     const int eslot = B % kEpochSlots;
-    const uint64_t ticket =
-        tid == 0 ? __hip_atomic_fetch_add((unsigned long long*)(a.sync + eslot * (kEpochStride / 4)), 1ull,
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                 : 0;
     const RouteSource& src = a.route;
     const int rtokens = src.logits ? P / src.top_k : 0;
     float lg[kRouteJ];
@@ -242,6 +156,15 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             }
         }
     }
+    // The ticket goes out from the last wave after its activation loads and is
+    // read only once the weight loads are out: loads retire in issue order, so
+    // nothing on the routing path waits behind the atomic.
+    constexpr int kTicketThread = kFzThreads - kWave;
+    const uint64_t ticket =
+        tid == kTicketThread
+            ? __hip_atomic_fetch_add((unsigned long long*)(a.sync + eslot * (kEpochStride / 4)), 1ull,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+            : 0;
     if (a.xq) {  // caller-quantized rows
         for (int i = tid; i < a.rows * (H / 16); i += kFzThreads) {
             const int r = i / (H / 16), c = (i % (H / 16)) * 16;
@@ -254,10 +177,86 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     }
 
     // -------------------------------------------------------- routing
+    // The router's order statistics in parallel: per token (one wave) the
+    // softmax max and sum exactly as the router kernel forms them, every
+    // logit's ordered bits into LDS; then every (token, expert) counts the
+    // experts ranked above it in (ordered bits desc, expert asc) order --
+    // rank = router slot -- with tpe neighbouring threads sharing the count;
+    // then one wave per token renormalizes its slots in slot order.
     if (src.logits) {
         for (int t = wave; t < rtokens; t += kFzWaves) {
             if (t != wave) wave_route_load(src, t, E, lg);
-            wave_route_token(src, t, E, lg, s.sid, s.wt, B == 0);
+            float m = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kRouteJ; ++j)
+                if (lane + j * kWave < E) m = fmaxf(m, lg[j]);
+            m = wave_max_dpp(m);
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRouteJ; ++j)
+                if (lane + j * kWave < E) sum += expf(lg[j] - m);
+            sum = wave_sum_dpp(sum);
+#pragma unroll
+            for (int j = 0; j < kRouteJ; ++j)
+                if (lane + j * kWave < E) s.rkey[t * E + lane + j * kWave] = ordered_bits(lg[j]);
+            if (lane == 0) {
+                s.rmax[t] = m;
+                s.rsum[t] = sum;
+            }
+        }
+        __syncthreads();
+        const int elems = rtokens * E;
+        const int tpe = elems * 4 <= kFzThreads ? 4 : elems * 2 <= kFzThreads ? 2 : 1;
+        const int sub = tid % tpe;
+        for (int base = 0; base < elems; base += kFzThreads / tpe) {
+            const int i = base + tid / tpe;
+            const bool live = i < elems;
+            const int t = live ? i / E : 0, e = live ? i % E : 0;
+            const uint32_t mine = s.rkey[live ? i : 0];
+            const uint32_t* row = s.rkey + t * E;
+            const int per = (E + tpe - 1) / tpe, o0 = sub * per, o1 = min(E, o0 + per);
+            int rank = 0;
+            if (live) {
+                int o = o0;
+                if (((t * E + o0) & 3) == 0) {  // 16-byte reads, 8 keys per step, several in flight
+#pragma unroll 2
+                    for (; o + 8 <= o1; o += 8) {
+                        const v4i q0 = *(const v4i*)(row + o), q1 = *(const v4i*)(row + o + 4);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const uint32_t k0 = (uint32_t)q0[j], k1 = (uint32_t)q1[j];
+                            rank += (int)(k0 > mine || (k0 == mine && o + j < e));
+                            rank += (int)(k1 > mine || (k1 == mine && o + 4 + j < e));
+                        }
+                    }
+                }
+                for (; o < o1; ++o) {
+                    const uint32_t k = row[o];
+                    rank += (int)(k > mine || (k == mine && o < e));
+                }
+            }
+            if (tpe >= 2) rank += dpp_i32<kDppXor1>(rank);
+            if (tpe >= 4) rank += dpp_i32<kDppXor2>(rank);
+            if (live && sub == 0 && rank < src.top_k) {
+                const uint32_t o = mine;  // the logit back from its ordered bits (-0 -> +0, same exp)
+                const float l = __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+                s.sid[t * src.top_k + rank] = (int16_t)e;
+                s.rp[t * src.top_k + rank] = expf(l - s.rmax[t]) / s.rsum[t];
+            }
+        }
+        __syncthreads();
+        for (int t = wave; t < rtokens; t += kFzWaves) {
+            const float p = lane < src.top_k ? s.rp[t * src.top_k + lane] : 0.0f;
+            float wtot = 0.0f;
+            for (int j = 0; j < src.top_k; ++j) wtot += readlane_f32(p, j);
+            if (lane < src.top_k) {
+                const float w = src.renormalize ? p / wtot : p;
+                s.wt[t * src.top_k + lane] = round_through(w, src.w_dtype);
+                if (B == 0) {
+                    src.ids_out[(int64_t)t * src.top_k + lane] = s.sid[t * src.top_k + lane];
+                    store_from_f32(src.weights_out, (int64_t)t * src.top_k + lane, src.w_dtype, w);
+                }
+            }
         }
     } else {
         for (int p = tid; p < P; p += kFzThreads) {
@@ -286,10 +285,6 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 s.gmax[u] = xamax[q];
             }
         }
-    }
-    if (tid == 0) {
-        const int n_slot = (G - eslot + kEpochSlots - 1) / kEpochSlots;  // workgroups sharing the slot
-        s.epoch = (uint32_t)(ticket / (uint64_t)n_slot) + 1u;
     }
     __syncthreads();
     if (a.x_group != 128) {  // per-row scale: the maximum of the row's group maxima
@@ -339,7 +334,6 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     }
     __syncthreads();
     const int num_active = s.num_active;
-    const uint32_t epoch = s.epoch;
 
     // ------------------------------------------------- weight loads
     // Every load is issued unconditionally (clamped to valid rows: units past
@@ -392,12 +386,17 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         }
     };
     load_job(B, wave);
+    if (tid == kTicketThread) {
+        const int n_slot = (G - eslot + kEpochSlots - 1) / kEpochSlots;  // workgroups sharing the slot
+        s.epoch = (uint32_t)(ticket / (uint64_t)n_slot) + 1u;
+    }
 
     // ------------------------------------------------------ gate / up
     // Units in batches of kUnitDepth: every wave's partial of every unit of
     // the batch into LDS (each unit as soon as its own bytes land), one
     // barrier, then one thread per (unit, row, column) sums the eight waves in
     // order, rounds gate / up, applies SiLU and publishes h with the epoch.
+    uint32_t epoch = 0;  // read from LDS after the first gate/up barrier
     auto unit_batch = [&](int j0) {
         // unit coordinates once per wave (uniform), and for the reducing threads in LDS
         int uc0[kUnitDepth], ust[kUnitDepth], um[kUnitDepth];
@@ -421,23 +420,28 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         for (int pass = 0; pass < passes; ++pass) {
 #pragma unroll
             for (int d = 0; d < kUnitDepth; ++d) {
+                // branch-free operand reads (clamped rows, values selected after the read)
                 const int* pr = s.prow + ust[d] + pass * 16;
                 const int mc = min(16, um[d] - pass * 16);
                 const bool live = col < mc;
-                const int arow = live ? pr[col] : 0;
+                const int arow = pr[min(col, max(mc - 1, 0))];
+                bool cl[4];
                 int crow[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) crow[r] = (grp * 4 + r < mc) ? pr[grp * 4 + r] : -1;
+                for (int r = 0; r < 4; ++r) {
+                    cl[r] = grp * 4 + r < mc;
+                    crow[r] = pr[min(grp * 4 + r, max(mc - 1, 0))];
+                }
                 v4f acc = zero;
 #pragma unroll
                 for (int i = 0; i < KBW; ++i) {
                     const int kb = wave + i * kFzWaves;
                     if (kb < KB) {
-                        const v8i af = live ? lds32(&s.xq[arow * H + kb * 128 + grp * 32]) : zero8i;
-                        const v4f dq = mfma_fp8(af, ub[d][i], zero);
+                        const v8i ar = lds32(&s.xq[arow * H + kb * 128 + grp * 32]);
+                        const v4f dq = mfma_fp8(live ? ar : zero8i, ub[d][i], zero);
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const float sx = crow[r] >= 0 ? s.xs[crow[r] * gpr + kb] : 0.0f;
+                            const float sx = cl[r] ? s.xs[crow[r] * gpr + kb] : 0.0f;
                             acc[r] = fmaf(dq[r] * sx, us[d][i], acc[r]);
                         }
                     }
@@ -446,6 +450,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 for (int r = 0; r < 4; ++r) s.v.red[d][wave][lane][r] = acc[r];
             }
             __syncthreads();
+            epoch = s.epoch;
             {
                 const int d = tid / (16 * kUnitCols), m = (tid / kUnitCols) % 16, c = tid % kUnitCols;
                 if (d < kUnitDepth && j0 + d < my_units && pass * 16 + m < s.ucoord[d][2]) {
@@ -476,6 +481,8 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         for (int d = 0; d < kUnitDepth; ++d) load_unit(j0 + d, d);
         unit_batch(j0);
     }
+    if (my_units == 0) __syncthreads();  // no gate/up barrier ran: order the epoch's LDS write
+    epoch = s.epoch;
     if (B >= tiles) return;  // no down rows for this workgroup
 
     // rows of this wave's first down job (pass 0), looked up before the wait
@@ -580,16 +587,35 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 crow[r] = pre ? pre_crow[r]
                               : ((m < 8) == (col < 8)) ? a_pair(m < 8 ? ai0 : ai1, pass * 8 + (m & 7)) : -1;
             }
+            // branch-free operand reads: every LDS read issued up front, the
+            // MFMAs back to back, then the per-block fma chain in block order
+            const int arc = max(ar, 0);
+            int crc[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) crc[r] = max(crow[r], 0);
+            constexpr int kChunk = KBJ <= 6 ? KBJ : 4;  // K blocks per batch of reads (register budget)
             v4f acc = zero;
 #pragma unroll
-            for (int kb = 0; kb < KBJ; ++kb) {
-                if (kb < KBd) {
-                    const v8i af = ar >= 0 ? lds32(&s.h.q[ar * I + kb * 128 + grp * 32]) : zero8i;
-                    const v4f dq = mfma_fp8(af, live_col ? db[kb] : zero8i, zero);
+            for (int k0 = 0; k0 < KBJ; k0 += kChunk) {
+                v8i af[kChunk];
+                float sh[kChunk][4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float sh = crow[r] >= 0 ? s.h.s[crow[r] * KBd + kb] : 0.0f;
-                        acc[r] = fmaf(dq[r] * sh, dsw[kb], acc[r]);
+                for (int i = 0; i < kChunk; ++i) {
+                    const int kbc = min(k0 + i, KBd - 1);
+                    af[i] = lds32(&s.h.q[arc * I + kbc * 128 + grp * 32]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sh[i][r] = s.h.s[crc[r] * KBd + kbc];
+                }
+                v4f dq[kChunk];
+#pragma unroll
+                for (int i = 0; i < kChunk; ++i)
+                    dq[i] = mfma_fp8(ar >= 0 ? af[i] : zero8i, live_col ? db[k0 + i] : zero8i, zero);
+#pragma unroll
+                for (int i = 0; i < kChunk; ++i) {
+                    if (k0 + i < KBd) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[r] = fmaf(dq[i][r] * (crow[r] >= 0 ? sh[i][r] : 0.0f), dsw[k0 + i], acc[r]);
                     }
                 }
             }
@@ -633,9 +659,10 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     }
 }
 
-bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize) {
+bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize, int routed_tokens) {
     const int KBd = I / 128;
     return pairs >= 1 && pairs <= kFusedMaxPairs && rows >= 1 && (int64_t)rows * H <= kFusedXBytes &&
+           (int64_t)routed_tokens * experts <= kRouteElems &&
            (int64_t)rows * H * x_esize <= kFusedRawBytes && (int64_t)pairs * I <= kFusedHBytes &&
            H <= kFusedMaxH && I <= kFusedMaxI && H % kTileRows == 0 && experts <= kMaxExperts && top_k >= 1 &&
            top_k <= 64 && KBd >= 1 && KBd <= 8;

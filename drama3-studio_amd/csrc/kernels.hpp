@@ -239,7 +239,7 @@ struct FusedDecodeArgs {
     int* status;
 };
 
-bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize);
+bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize, int routed_tokens);
 // Launches the fused decode; false (nothing enqueued) when the device cannot
 // hold the grid the kernel needs.
 bool launch_fp8_fused_decode(const FusedDecodeArgs& a, hipStream_t stream);
