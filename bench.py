@@ -8,9 +8,14 @@ rotate over LAYERS distinct layer banks (16 x 606 MB, far above the 256 MB
 Infinity Cache) with fresh seeded logits per step, all inputs resident in HBM,
 and are replayed from hipGraphs.
 
-Reported: value = microseconds per layer decode step (lower is better); the
-dominant kernel's roofline (gate/up GEMV, HBM-bound) from HIP events around a
-graph of back-to-back launches of that kernel alone; the reference's own CPU
+Reported: value = microseconds per layer decode step (lower is better).  The
+step is one launch of the single-launch decode kernel (fp8_fused_decode_kernel),
+so the roofline line is that kernel's: algorithmic bytes of the step (distinct
+experts' FP8 rows and scales, activations, logits) over its average launch
+duration from HIP events on the launch stream; traffic = its copy-calibrated
+FETCH_SIZE + WRITE_SIZE from the committed counter summary.  Beside it: the
+same steps through the three-launch decode, 4- and 8-token decode, the
+2048-token FP8 prefill, the packed-bank formats, and the reference's own CPU
 expert executor (compiled from its sources into oracle/_ref) timed on this
 host's cores on a bounded sample of the same layer shape.
 
@@ -58,16 +63,84 @@ def make_layer_bank(layer: int, device):
     return StagedExperts(*parts)
 
 
-def unique_experts(ids) -> list[int]:
-    return [len(set(row)) for row in ids]
+def decode_graph_us(backend, xs, logits, banks, outs, stream, steps: int, warmup: int) -> tuple[float, float]:
+    """Replays a hipGraph of one routed decode step per layer bank (all inputs
+    resident) until `steps` steps ran; HIP events on the launch stream.
+    Returns (microseconds per step, total milliseconds)."""
+    import torch
+
+    layers = len(banks)
+
+    def step(i):
+        backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
+
+    with torch.cuda.stream(stream):  # workspace and descriptor caches, outside capture
+        for i in range(layers):
+            step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(layers):
+            step(i)
+    remainder = steps % layers
+    tail = None
+    if remainder:
+        tail = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(tail, stream=stream):
+            for i in range(remainder):
+                step(i)
+    for _ in range(max(1, warmup // layers)):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(steps // layers):
+            graph.replay()
+        if tail is not None:
+            tail.replay()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+    return total_ms * 1e3 / steps, total_ms
+
+
+def decode_inputs(tokens: int, device, seed: int):
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    xs = torch.randn(LAYERS, tokens, HIDDEN, device=device, generator=g).bfloat16()
+    logits = torch.randn(LAYERS, tokens, EXPERTS, device=device, generator=g)
+    return xs, logits, torch.empty_like(xs)
+
+
+def step_bytes(logits, tokens: int) -> tuple[float, float]:
+    """Algorithmic HBM bytes of one decode step, averaged over the layers:
+    the distinct experts' FP8 rows and per-channel scales, the bf16 input and
+    output rows, the fp32 logits.  Returns (bytes, mean distinct experts)."""
+    import torch
+
+    from drama_moe import router
+
+    with torch.no_grad():
+        ids = [router.route_topk(logits[i], TOP_K)[1].reshape(-1).tolist() for i in range(logits.shape[0])]
+    uniq = [len(set(r)) for r in ids]
+    return sum(u * EXPERT_BYTES + 2 * tokens * HIDDEN * 2 + tokens * EXPERTS * 4 for u in uniq) / len(uniq), \
+        sum(uniq) / len(uniq)
+
+
+# one expert's FP8 rows (w13 + w2) and per-output-channel fp32 scales
+EXPERT_BYTES = 2 * INTER * HIDDEN + HIDDEN * INTER + (2 * INTER + HIDDEN) * 4
 
 
 def run_gpu(steps: int, warmup: int):
+    """The headline decode (1 token) through the single-launch kernel, the
+    same steps through the three-launch decode, and multi-token decode."""
     import torch
 
-    from drama_moe import _lib, router
-    from drama_moe.formats import fp8_bank_struct
-    from drama_moe.offload import HipExpertBackend, device_state
+    from drama_moe import _lib
+    from drama_moe.offload import HipExpertBackend
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
@@ -75,123 +148,60 @@ def run_gpu(steps: int, warmup: int):
     banks = [make_layer_bank(layer, device) for layer in range(LAYERS)]
     torch.cuda.synchronize()
     log("banks ready:", LAYERS, "layers x", round(banks[0].nbytes / 1e6, 1), "MB")
-
-    g = torch.Generator(device=device).manual_seed(SEED)
     backend = HipExpertBackend()
     stream = torch.cuda.Stream(device)
-    # per-step inputs, resident in HBM
-    xs = torch.randn(LAYERS, 1, HIDDEN, device=device, generator=g).bfloat16()
-    logits = torch.randn(LAYERS, 1, EXPERTS, device=device, generator=g)
-    outs = torch.empty(LAYERS, 1, HIDDEN, device=device, dtype=torch.bfloat16)
-
-    def step(i):
-        backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
-
-    # warm up the workspace and descriptor caches outside capture
-    with torch.cuda.stream(stream):
-        for i in range(LAYERS):
-            step(i)
-    torch.cuda.synchronize()
-
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for i in range(LAYERS):
-            step(i)
-    remainder = steps % LAYERS
-    tail = None
-    if remainder:
-        tail = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(tail, stream=stream):
-            for i in range(remainder):
-                step(i)
-    full = steps // LAYERS
-
-    for _ in range(max(1, warmup // LAYERS)):
-        graph.replay()
-    torch.cuda.synchronize()
-
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        torch.cuda.synchronize()
-        start.record(stream)
-        for _ in range(full):
-            graph.replay()
-        if tail is not None:
-            tail.replay()
-        stop.record(stream)
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(stop)
-    us_per_step = total_ms * 1e3 / steps
-
-    # routing of the timed steps (same logits every replay): distinct experts
-    with torch.no_grad():
-        ids_all = torch.stack([router.route_topk(logits[i], TOP_K)[1][0] for i in range(LAYERS)])
-    uniq = unique_experts(ids_all.cpu().tolist())
-    per_expert = 2 * INTER * HIDDEN + HIDDEN * INTER + (2 * INTER + HIDDEN) * 4
-    step_bytes = [u * per_expert + 2 * HIDDEN * 2 + EXPERTS * 4 for u in uniq]
-    alg_bytes_step = sum(step_bytes) / len(step_bytes)
-    step_gbs = alg_bytes_step / (us_per_step * 1e-6) / 1e9
-
-    # dominant kernel: gate/up alone, back-to-back over the rotating layers
     lib = _lib.library()
-    state = device_state(device)
-    ids_dev = ids_all.contiguous()
-    w_dev = torch.full((LAYERS, TOP_K), 1.0 / TOP_K, device=device)
-    # gate/up stage bytes: weights + per-channel scales of the distinct experts,
-    # the FP8 activation row + scales, the FP8 hidden + scales written
-    gu_bytes = [u * (2 * INTER * HIDDEN + 2 * INTER * 4) + HIDDEN + (HIDDEN // 128) * 4 + TOP_K * INTER
-                + TOP_K * (INTER // 128) * 4 for u in uniq]
-    kstream = torch.cuda.Stream(device)
-    hq = torch.empty(TOP_K, INTER, dtype=torch.uint8, device=device)
-    hs = torch.empty(TOP_K, INTER // 128, device=device)
 
-    # one prepared workspace per layer (grouping + quantized x), then the
-    # gate/up stage alone: a single kernel launch per layer
-    workspaces = []
-    for i in range(LAYERS):
-        bank = fp8_bank_struct(banks[i])
-        nbytes = lib.dmoe_fp8_workspace_bytes(bank, TOP_K)
-        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        _lib.check(lib.dmoe_fp8_prepare(
-            bank, _lib.ptr(xs[i]), _lib.BF16, HIDDEN, 1, TOP_K, _lib.ptr(ids_dev[i]), _lib.I64, TOP_K, 128,
-            _lib.ptr(ws), nbytes, _lib.ptr(state.status), _lib.stream_handle(device)))
-        workspaces.append(ws)
-    torch.cuda.synchronize()
-
-    def gateup_only(i):
-        bank = fp8_bank_struct(banks[i])
-        ws = workspaces[i]
-        _lib.check(lib.dmoe_fp8_gate_up(
-            bank, TOP_K, TOP_K, 128, _lib.BF16, _lib.ptr(hq), _lib.ptr(hs), _lib.ptr(ws), ws.numel(),
-            _lib.ptr(state.status), _lib.stream_handle(device)))
-
-    kgraph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(kstream):
-        for i in range(LAYERS):
-            gateup_only(i)
-    torch.cuda.synchronize()
-    with torch.cuda.graph(kgraph, stream=kstream):
-        for i in range(LAYERS):
-            gateup_only(i)
-    reps = max(1, steps // LAYERS)
-    kgraph.replay()
-    torch.cuda.synchronize()
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(kstream):
-        k0.record(kstream)
-        for _ in range(reps):
-            kgraph.replay()
-        k1.record(kstream)
-    torch.cuda.synchronize()
-    k_us = k0.elapsed_time(k1) * 1e3 / (reps * LAYERS)
-    k_bytes = sum(gu_bytes) / len(gu_bytes)
-    k_gbs = k_bytes / (k_us * 1e-6) / 1e9
+    xs, logits, outs = decode_inputs(1, device, SEED)
+    # The graph holds one fp8_fused_decode_kernel launch per step and nothing
+    # else, so the per-step time is that kernel's average launch duration.
+    us_per_step, total_ms = decode_graph_us(backend, xs, logits, banks, outs, stream, steps, warmup)
+    alg_bytes, uniq = step_bytes(logits, 1)
+    fused_out = outs.clone()
+    lib.dmoe_set_fused_decode(0)
+    try:
+        staged_us, _ = decode_graph_us(backend, xs, logits, banks, outs, stream, min(steps, 1024), warmup)
+    finally:
+        lib.dmoe_set_fused_decode(1)
+    same = bool(torch.equal(outs, fused_out))
+    multi = {}
+    for tokens in (4, 8):
+        mx, ml, mo = decode_inputs(tokens, device, SEED + tokens)
+        t_us, _ = decode_graph_us(backend, mx, ml, banks, mo, stream, min(steps, 1024), warmup)
+        mbytes, muniq = step_bytes(ml, tokens)
+        multi[f"tokens_{tokens}"] = {"us": round(t_us, 2), "unique_experts_mean": round(muniq, 2),
+                                     "hbm_frac": round(mbytes / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     return {
-        "us_per_step": us_per_step, "total_ms": total_ms, "alg_bytes_step": alg_bytes_step,
-        "step_gbs": step_gbs, "unique_experts_mean": sum(uniq) / len(uniq),
-        "kernel_us": k_us, "kernel_bytes": k_bytes, "kernel_gbs": k_gbs,
+        "us_per_step": us_per_step, "total_ms": total_ms, "alg_bytes_step": alg_bytes,
+        "step_gbs": alg_bytes / (us_per_step * 1e-6) / 1e9, "unique_experts_mean": uniq,
+        "three_launch_us": staged_us, "three_launch_identical": same, "multi_token": multi,
         "device": torch.cuda.get_device_name(device),
     }
+
+
+def pmc_pass(rounds: int = 8, copy_mib: int = 256):
+    """Eager workload for hardware-counter runs: `rounds` passes of the
+    decode step over the layer banks, then a plain fp32 copy of `copy_mib`
+    MiB (read once, written once) whose counter readings calibrate the
+    bytes-per-count of the HBM counters."""
+    import torch
+
+    from drama_moe.offload import HipExpertBackend
+
+    device = torch.device("cuda", 0)
+    banks = [make_layer_bank(layer, device) for layer in range(LAYERS)]
+    xs, logits, outs = decode_inputs(1, device, SEED)
+    backend = HipExpertBackend()
+    for _ in range(rounds):
+        for i in range(LAYERS):
+            backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
+    src = torch.ones(copy_mib << 18, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": {"decode_steps": rounds * LAYERS, "copy_bytes_read": src.numel() * 4,
+                                   "copy_bytes_written": dst.numel() * 4}}), flush=True)
 
 
 PREFILL_TOKENS = 2048
@@ -401,6 +411,21 @@ def cpu_baseline(budget_s: float = 12.0):
             "sample": sample}
 
 
+TRAFFIC_SUMMARY = ROOT / "profiles" / "fp8_fused_decode_kernel_moe_layer_b1_hbm_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the fused decode kernel from the committed
+    FETCH_SIZE / WRITE_SIZE counter summary (copy-calibrated), or None."""
+    try:
+        for text in TRAFFIC_SUMMARY.read_text().splitlines():
+            if text.startswith("traffic_bytes_per_launch:"):
+                return int(text.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -409,6 +434,8 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-prefill", action="store_true")
     parser.add_argument("--no-quant", action="store_true")
+    parser.add_argument("--pmc-pass", action="store_true",
+                        help="run the eager counter-collection workload instead of the benchmark")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path is built and "
@@ -417,6 +444,9 @@ def main():
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs as a single process on one GPU", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_pass:
+        pmc_pass()
+        return
     steps = max(1, args.steps)
     gpu = run_gpu(steps, args.warmup)
     log("gpu", json.dumps(gpu))
@@ -427,7 +457,7 @@ def main():
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log("cpu", json.dumps(cpu))
-    frac = gpu["kernel_gbs"] / HBM_PEAK_GBS
+    frac = gpu["step_gbs"] / HBM_PEAK_GBS
     line = {
         "metric": "MoE-layer decode us + % peak HBM GB/s (B=1); FP8 prefill TFLOPS @2048 tok",
         "value": round(gpu["us_per_step"], 3),
@@ -446,11 +476,15 @@ def main():
                    "tokens": 1, "experts": EXPERTS, "hidden": HIDDEN, "intermediate": INTER,
                    "top_k": TOP_K, "layers_rotated": LAYERS},
         "hbm_gbs_step": round(gpu["step_gbs"], 1),
-        "pct_peak_hbm_step": round(100 * gpu["step_gbs"] / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "achieved": round(gpu["kernel_gbs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(frac, 4), "traffic": None,
-                     "kernel": "fp8_gateup_decode_kernel", "kernel_us": round(gpu["kernel_us"], 3),
-                     "alg_bytes_per_launch": round(gpu["kernel_bytes"])},
+        "pct_peak_hbm_step": round(100 * frac, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gpu["step_gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(frac, 4), "traffic": measured_traffic(),
+                     "kernel": "fp8_fused_decode_kernel", "kernel_us": round(gpu["us_per_step"], 3),
+                     "alg_bytes_per_launch": round(gpu["alg_bytes_step"]),
+                     "unique_experts_mean": round(gpu["unique_experts_mean"], 3)},
+        "decode_three_launch_us": round(gpu["three_launch_us"], 3),
+        "decode_three_launch_identical": gpu["three_launch_identical"],
+        "decode_multi_token": gpu["multi_token"],
         "cpu_baseline": cpu,
         "prefill_fp8": prefill,
         "packed_banks": quant,

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kGThreads) void fp8_grouped_gateup_kernel(GroupedGa
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) ac[mi] = alive[mi] ? load32(arow[mi]) : zero8i;
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) bc[ni] = load32_stream(brow[ni]);
+    for (int ni = 0; ni < 4; ++ni) bc[ni] = load32(brow[ni]);
     for (int kb = 0; kb < KB; ++kb) {
         const bool more = kb + 1 < KB;
         v8i an[4], bnx[4];
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(kGThreads) void fp8_grouped_gateup_kernel(GroupedGa
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi) an[mi] = alive[mi] ? load32(arow[mi] + (kb + 1) * 128) : zero8i;
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) bnx[ni] = load32_stream(brow[ni] + (kb + 1) * 128);
+            for (int ni = 0; ni < 4; ++ni) bnx[ni] = load32(brow[ni] + (kb + 1) * 128);
         }
         if constexpr (SCALE_PER_KB) {
 #pragma unroll
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(kGThreads) void fp8_grouped_down_kernel(GroupedDown
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) ac[mi] = alive[mi] ? load32(arow[mi]) : zero8i;
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) bc[ni] = load32_stream(brow[ni]);
+    for (int ni = 0; ni < 4; ++ni) bc[ni] = load32(brow[ni]);
     for (int kb = 0; kb < KB; ++kb) {
         const bool more = kb + 1 < KB;
         v8i an[4], bnx[4];
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(kGThreads) void fp8_grouped_down_kernel(GroupedDown
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi) an[mi] = alive[mi] ? load32(arow[mi] + (kb + 1) * 128) : zero8i;
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) bnx[ni] = load32_stream(brow[ni] + (kb + 1) * 128);
+            for (int ni = 0; ni < 4; ++ni) bnx[ni] = load32(brow[ni] + (kb + 1) * 128);
         }
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {

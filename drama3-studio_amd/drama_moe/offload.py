@@ -130,9 +130,10 @@ class HipExpertBackend:
     def forward_routed(self, x: Tensor, logits: Tensor, top_k: int, staged: StagedExperts, *,
                        renormalize: bool = True, weights_dtype: torch.dtype | None = None,
                        out: Tensor | None = None):
-        """Router + routed experts in one call, no host sync (decode: three
-        kernels; prefill: router, permutation, quantization, two grouped GEMMs
-        and the combine).  Returns (out [T, H], weights [T, top_k], ids [T, top_k])."""
+        """Router + routed experts in one call, no host sync (decode of up to
+        64 route pairs: one kernel, else three; prefill: router, permutation,
+        quantization, two grouped GEMMs and the combine).  Returns
+        (out [T, H], weights [T, top_k], ids [T, top_k])."""
         self._check(x)
         if x.ndim != 2 or logits.ndim != 2 or logits.shape[0] != x.shape[0]:
             raise ValueError("Expected x [T, H] and router logits [T, E]")
