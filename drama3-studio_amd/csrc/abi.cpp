@@ -350,6 +350,7 @@ struct PrefillWorkspace {
     int32_t* offsets;
     int32_t* tile_expert;
     int32_t* tile_m0;
+    int32_t* tile_count;
     uint8_t* xq;
     float* xs;
     uint8_t* hq;
@@ -372,6 +373,7 @@ size_t prefill_workspace_layout(int pairs, int experts, int H, int I, char* base
     char* offsets = take((size_t)(experts + 1) * 4);
     char* tile_expert = take((size_t)tiles * 4);
     char* tile_m0 = take((size_t)tiles * 4);
+    char* tile_count = take(4);
     char* xq = take((size_t)pairs * H);
     char* xs = take((size_t)pairs * (H / 128) * 4);
     char* hq = take((size_t)pairs * I);
@@ -384,6 +386,7 @@ size_t prefill_workspace_layout(int pairs, int experts, int H, int I, char* base
         ws->offsets = reinterpret_cast<int32_t*>(offsets);
         ws->tile_expert = reinterpret_cast<int32_t*>(tile_expert);
         ws->tile_m0 = reinterpret_cast<int32_t*>(tile_m0);
+        ws->tile_count = reinterpret_cast<int32_t*>(tile_count);
         ws->xq = reinterpret_cast<uint8_t*>(xq);
         ws->xs = reinterpret_cast<float*>(xs);
         ws->hq = reinterpret_cast<uint8_t*>(hq);
@@ -408,13 +411,16 @@ void fp8_prefill_call(const BankGeom& g, Activations a, const void* ids, int ids
     const size_t need = prefill_workspace_layout(pairs, g.experts, g.H, g.I, nullptr, nullptr);
     require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
     require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+    // the grouped GEMMs address a tile's weight rows as 32-bit offsets from the expert base
+    require((int64_t)g.w13.N * g.w13.w_sn < (int64_t(1) << 32) && (int64_t)g.w2.N * g.w2.w_sn < (int64_t(1) << 32),
+            "grouped path: rows x row stride of one expert must stay below 4 GiB");
     PrefillWorkspace ws{};
     prefill_workspace_layout(pairs, g.experts, g.H, g.I, static_cast<char*>(workspace), &ws);
     const int tiles = dmoe::max_block_tiles(pairs, g.experts, dmoe::kGroupM);
 
     dmoe::PermuteArgs pa{ids, ids_dtype, pairs, g.experts, ws.order, ws.counts, ws.offsets, status,
                          ws.permute_scratch, ws.permute_scratch + pairs, nullptr, dmoe::kGroupM, tiles,
-                         ws.tile_expert, ws.tile_m0};
+                         ws.tile_expert, ws.tile_m0, ws.tile_count};
     dmoe::launch_permute(pa, stream);
     if (a.xq == nullptr) {
         const int rows = (pairs - 1) / a.row_div + 1;
@@ -431,6 +437,7 @@ void fp8_prefill_call(const BankGeom& g, Activations a, const void* ids, int ids
     ga.offsets = ws.offsets;
     ga.tile_expert = ws.tile_expert;
     ga.tile_m0 = ws.tile_m0;
+    ga.tile_count = ws.tile_count;
     ga.max_tiles = tiles;
     ga.xq = a.xq;
     ga.xs = a.xs;
@@ -450,6 +457,7 @@ void fp8_prefill_call(const BankGeom& g, Activations a, const void* ids, int ids
     da.offsets = ws.offsets;
     da.tile_expert = ws.tile_expert;
     da.tile_m0 = ws.tile_m0;
+    da.tile_count = ws.tile_count;
     da.max_tiles = tiles;
     da.hq = ws.hq;
     da.hs = ws.hs;

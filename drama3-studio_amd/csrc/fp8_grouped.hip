@@ -13,19 +13,31 @@
 // scales are constant along K, so the MFMA accumulates all of K and the
 // product of the two scales is applied once (same value up to fp32 rounding).
 //
-// Workgroup = 4 waves on a tile of 64 sorted pairs (4 m16 tiles) of one
-// expert:
-//   gate/up: 128 hidden columns; wave w owns 32 of them, i.e. two gate and the
-//            two matching up 16-column MFMA tiles, so SiLU * up and the FP8
-//            128-group quantization of h fuse into the epilogue (one LDS
+// Work unit = a tile of 64 sorted pairs of one expert x 256 weight rows:
+//   gate/up: 128 hidden columns = 128 gate + the matching 128 up rows; wave w
+//            owns gate and up columns [32 w, 32 w + 32), so SiLU * up and the
+//            FP8 128-group quantization of h fuse into the epilogue (one LDS
 //            exchange of row maxima across the four waves).
-//   down:    256 output columns, 64 per wave; epilogue = * route weight and a
-//            store of the fp32 partial row of the original pair.
-// Operands go straight from global memory into MFMA registers (each lane
-// reads 32 contiguous bytes of a row), the next K block in flight while the
-// current one is multiplied.  Workgroups are remapped so that each XCD gets a
-// contiguous range of (column tile, expert tile) work: the tiles of one expert
-// that share a weight tile run on the same XCD and share its L2.
+//   down:    256 output columns, 64 per wave; epilogue = * route weight and
+//            16-byte stores of the fp32 partial rows of the original pairs.
+//
+// Persistent launch: one workgroup per CU walks its list of tiles as one
+// continuous stream of 128-column K blocks.  The work is split by role: two
+// copy waves issue every global -> LDS copy (a CU moves only about 50 bytes
+// per clock into LDS, so issuing a block's 40 KB stalls the issuing wave for
+// longer than the block's MFMAs take) and four waves only multiply and run the
+// epilogues, so copying and multiplying overlap.  Operands move global ->
+// LDS with the direct-to-LDS copies of gfx950 (no registers in between)
+// through a 3-stage ring: block i + 2 is in flight while block i is
+// multiplied, one barrier per block, and the first blocks of the next tile
+// are already in flight while the epilogue of the current one runs.  Each
+// wave-wide copy instruction writes 8 rows x 128 bytes; the 16-byte chunk c of
+// tile row r is stored at chunk c ^ (r % 8), so the 16 rows an MFMA operand
+// read touches spread over the banks.  The scales of each K block (activation
+// or hidden groups, weight channels or 128x128 blocks) ride in the same
+// stages.  Tile lists are XCD-aware: each XCD takes a contiguous range of
+// (column tile, expert tile) work, so the tiles of one expert that share a
+// weight tile run on the same XCD at the same time and share its L2.
 #include <algorithm>
 
 #include "common.hpp"
@@ -36,299 +48,463 @@ namespace dmoe {
 
 namespace {
 
-constexpr int kGThreads = 256;
+constexpr int kMmaWaves = 4;                        // waves that multiply (and run the epilogues)
+constexpr int kCopyWaves = 2;                       // waves that issue every global -> LDS copy
+constexpr int kGThreads = (kMmaWaves + kCopyWaves) * kWave;
 constexpr int kXcds = 8;
-constexpr int kMaxKb = kMaxHidden / 128;  // 128-column K blocks, gate/up (H) or down (I)
+constexpr int kTileN = 256;                         // weight rows of a tile
+constexpr int kStages = 3;                          // K-block ring depth
+constexpr int kAInst = kGroupM / 8 / kCopyWaves;    // A copy instructions per copy wave per block (4)
+constexpr int kBInst = kTileN / 8 / kCopyWaves;     // B copy instructions per copy wave per block (16)
+constexpr int kScaleInst = 4 / kCopyWaves;          // weight-scale (and row-scale) copies per copy wave (2)
+constexpr int kCopies = kAInst + kBInst + 2 * kScaleInst;  // vector-memory instructions per copy wave per block
+constexpr int kChunk = 16;                          // tiles whose metadata a workgroup holds at once
+static_assert(2 * kCopies <= 63, "two blocks of copies must fit the wave's vmcnt range");
 
-// Workgroup -> logical tile: XCD x (workgroups x, x + 8, ...) receives the
-// contiguous logical range [x * G / 8, (x + 1) * G / 8).  G is a multiple of 8.
-__device__ __forceinline__ int xcd_tile(int bid, int grid) {
-    return (bid % kXcds) * (grid / kXcds) + bid / kXcds;
+typedef __attribute__((address_space(3))) void lds_t;
+
+// One wave-wide direct-to-LDS copy: lane i reads `bytes` at src and writes
+// them to dst + i * bytes (dst wave-uniform).
+__device__ __forceinline__ void copy16_to_lds(const void* src, void* dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_t*)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void copy4_to_lds(const void* src, void* dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_t*)dst, 4, 0, 0);
+}
+
+// wait_copies<N>: at most N vector-memory operations of this wave remain in
+// flight.  Vector loads (direct-to-LDS copies included) complete in issue
+// order, so with the youngest N-instruction copy group allowed in flight every
+// older copy has landed.  lds_barrier: this wave's LDS accesses are done, then
+// the workgroup synchronizes.  The memory clobbers keep the compiler from
+// moving LDS accesses across them.
+template <int N>
+__device__ __forceinline__ void wait_copies() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+struct TileMeta {
+    int nt, e, m0, mend;   // column tile, expert, sorted rows [m0, mend) (mend clipped to m0 + 64)
+};
+
+struct alignas(16) GemmLds {
+    uint8_t a[kStages][kGroupM * 128];   // A tile rows, swizzled 16-byte chunks
+    uint8_t b[kStages][kTileN * 128];    // B tile rows, swizzled
+    float ws[kStages][4][64];            // weight scale of B row 64 q + l at the stage's K block
+    float rs[kStages][4][64];            // row scale of A row 16 q + l % 16 (lanes >= 16 repeat)
+    TileMeta meta[kChunk];
+    int rowv[kChunk][kGroupM];           // gate/up: activation row; down: original pair (-1: none)
+    float rowx[kChunk][kGroupM];         // down: route weight of the row
+    float amax[kMmaWaves][kGroupM];      // gate/up epilogue: per-wave row maxima of |h|
+    uint8_t hbuf[kGroupM * 128];         // gate/up epilogue: the FP8 hidden tile
+    float xt[kMmaWaves][16][16];         // down epilogue: per-wave 16x16 transpose of an MFMA result
+};
+
+// A copy wave's global sources for one tile.
+struct TilePlan {
+    const uint8_t* a[kAInst];   // A row of copy j, already offset to this lane's chunk
+    const uint8_t* bbase;       // the tile's weight rows (expert base)
+    uint32_t b[kBInst];         // byte offset of copy j's row + chunk from bbase
+    const float* wsrc[kScaleInst];  // scale of B row 64 q + l at K block 0
+    const float* rsrc[kScaleInst];  // scale of A row 16 q + l % 16 at K block 0
+    int64_t ws_k;               // weight-scale stride per (kb / kb_div)
+    int kb_div;
+    int rs_k;                   // row-scale stride per K block (0: constant)
+};
+
+// Lane l of copy instruction q writes tile row 8 q + l / 8, physical chunk
+// l % 8, which holds logical chunk (l % 8) ^ (l / 8).
+__device__ __forceinline__ int copy_row(int q, int lane) { return q * 8 + lane / 8; }
+__device__ __forceinline__ int copy_chunk_bytes(int lane) { return ((lane % 8) ^ (lane / 8)) * 16; }
+// The instructions of copy wave cw: A copies cw * kAInst + j, B copies
+// cw * kBInst + j, scale copies q = cw * kScaleInst + j.
+__device__ __forceinline__ int a_copy(int cw, int j) { return cw * kAInst + j; }
+__device__ __forceinline__ int b_copy(int cw, int j) { return cw * kBInst + j; }
+__device__ __forceinline__ int s_copy(int cw, int j) { return cw * kScaleInst + j; }
+
+__device__ __forceinline__ void issue_stage(GemmLds& s, const TilePlan& p, int kb, int stage, int cw) {
+    const int64_t koff = (int64_t)kb * 128;
+#pragma unroll
+    for (int j = 0; j < kAInst; ++j) copy16_to_lds(p.a[j] + koff, &s.a[stage][a_copy(cw, j) * 1024]);
+#pragma unroll
+    for (int j = 0; j < kBInst; ++j) copy16_to_lds(p.bbase + p.b[j] + koff, &s.b[stage][b_copy(cw, j) * 1024]);
+    const int64_t wk = (int64_t)(kb / p.kb_div) * p.ws_k, rk = (int64_t)kb * p.rs_k;
+#pragma unroll
+    for (int j = 0; j < kScaleInst; ++j) {
+        copy4_to_lds(p.wsrc[j] + wk, &s.ws[stage][s_copy(cw, j)][0]);
+        copy4_to_lds(p.rsrc[j] + rk, &s.rs[stage][s_copy(cw, j)][0]);
+    }
+}
+
+__device__ __forceinline__ v8i lds_operand(const uint8_t* tile, int o0, int o1) {
+    const v4i lo = *(const v4i*)(tile + o0), hi = *(const v4i*)(tile + o1);
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// One K block: acc[mi][ni] += rows 16 mi.. x B rows brow[ni]..  PER_KB:
+// acc = fma(dot * rs[row], ws[col], acc), the 16 block dot products issued
+// back to back before their scaling; otherwise the MFMA accumulates.  The
+// four B operands stay in registers; the A operands are read one row tile
+// ahead of the MFMAs that use them.
+template <bool PER_KB>
+__device__ __forceinline__ void compute_block(const GemmLds& s, int stage, const int (&brow)[4], int o0, int o1,
+                                              v4f (&acc)[4][4]) {
+    const int lane = threadIdx.x % kWave, grp = lane / 16, col = lane % 16;
+    const v4f zero = {0, 0, 0, 0};
+    const uint8_t* at = s.a[stage];
+    const uint8_t* bt = s.b[stage];
+    v8i bf[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) bf[ni] = lds_operand(bt + brow[ni] * 128, o0, o1);
+    v8i af = lds_operand(at, o0, o1);
+    if constexpr (PER_KB) {
+        v4f d[4][4];
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+            v8i an = af;
+            if (mi < 3) an = lds_operand(at + (mi + 1) * 16 * 128, o0, o1);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) d[mi][ni] = mfma_fp8(af, bf[ni], zero);
+            af = an;
+        }
+        float wsv[4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const int r = brow[ni] + col;
+            wsv[ni] = s.ws[stage][r / 64][r % 64];
+        }
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+            const v4f rsv = *(const v4f*)&s.rs[stage][mi][grp * 4];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mi][ni][i] = fmaf(d[mi][ni][i] * rsv[i], wsv[ni], acc[mi][ni][i]);
+        }
+    } else {
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+            v8i an = af;
+            if (mi < 3) an = lds_operand(at + (mi + 1) * 16 * 128, o0, o1);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma_fp8(af, bf[ni], acc[mi][ni]);
+            af = an;
+        }
+    }
+}
+
+template <int GU>
+__device__ __forceinline__ float round_gu(float v) {
+    if constexpr (GU == kBF16) return (float)(__bf16)v;
+    else if constexpr (GU == kF16) return (float)(_Float16)v;
+    else return v;
+}
+
+// E4M3 byte of v (|v| saturated to 448, NaN -> 448 with its sign, then the
+// hardware round-to-nearest-even conversion, equal to fp8_encode).
+__device__ __forceinline__ uint32_t fp8_byte(float v) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fp8_saturate(v), 0.0f, 0, false) & 0xFFu;
+}
+
+// The persistent tile loop shared by the two GEMMs.  OP supplies: col_tiles,
+// kblocks, load_row (chunk metadata), plan (a copy wave's sources for a
+// tile), brow (B rows of a multiplying wave's column tiles) and epilogue.
+template <class OP>
+__device__ __forceinline__ void grouped_tiles(const typename OP::Args& a) {
+    __shared__ GemmLds s;
+    const int lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: branches on it are scalar
+    const bool mma = wave < kMmaWaves;
+    const int cw = wave - kMmaWaves;  // copy wave index (copy waves only)
+    const int nvt = *a.tile_count;
+    const int T = OP::col_tiles(a) * nvt;
+    if (T <= 0) return;
+    const int KB = OP::kblocks(a);
+    const int nwx = gridDim.x / kXcds;  // workgroups per XCD
+    const int xcd = blockIdx.x % kXcds, li = blockIdx.x / kXcds;
+    const int xbeg = (int)((int64_t)T * xcd / kXcds), xend = (int)((int64_t)T * (xcd + 1) / kXcds);
+    int brow[4];
+    OP::brow(mma ? wave : 0, brow);
+    int o0, o1;
+    {
+        const int r = lane % 16, g = lane / 16;
+        o0 = r * 128 + (((2 * g) ^ (r % 8)) * 16);
+        o1 = r * 128 + (((2 * g + 1) ^ (r % 8)) * 16);
+    }
+    for (int c0 = xbeg + li; c0 < xend; c0 += kChunk * nwx) {
+        const int ntc = min(kChunk, (xend - c0 + nwx - 1) / nwx);
+        __syncthreads();  // the previous chunk is done with the metadata
+        if (threadIdx.x < ntc) {
+            const int L = c0 + threadIdx.x * nwx;
+            const int mt = L % nvt, e = a.tile_expert[mt], m0 = a.tile_m0[mt];
+            s.meta[threadIdx.x] = TileMeta{L / nvt, e, m0, min(a.offsets[e + 1], m0 + kGroupM)};
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < ntc * kGroupM; i += kGThreads)
+            OP::load_row(a, s.meta[i / kGroupM], i % kGroupM, s.rowv[i / kGroupM][i % kGroupM],
+                         s.rowx[i / kGroupM][i % kGroupM]);
+        __syncthreads();
+
+        const int n_it = ntc * KB;
+        // Both roles pass the same barriers: one per block (copies of block it
+        // visible; nobody reads the stage block it + 2 overwrites) and the
+        // epilogue's OP::kEpilogueBarriers after each tile's last block.
+        if (mma) {
+            const v4f zero = {0, 0, 0, 0};
+            v4f acc[4][4];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = zero;
+            int stage = 0, ct = 0, ckb = 0;
+            for (int it = 0; it < n_it; ++it) {
+                lds_barrier();
+                compute_block<OP::kPerKb>(s, stage, brow, o0, o1, acc);
+                if (++ckb == KB) {
+                    OP::epilogue(a, s, ct, stage, brow, acc);
+#pragma unroll
+                    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = zero;
+                    ckb = 0;
+                    ++ct;
+                }
+                stage = stage == kStages - 1 ? 0 : stage + 1;
+            }
+        } else {
+            TilePlan p;
+            int iss_t = 0, iss_kb = 0;
+            auto issue_next = [&](int stage) {
+                if (iss_kb == 0) OP::plan(a, s, iss_t, cw, lane, KB, p);
+                issue_stage(s, p, iss_kb, stage, cw);
+                if (++iss_kb == KB) {
+                    iss_kb = 0;
+                    ++iss_t;
+                }
+            };
+            // the copy groups must reach the memory pipeline in ring order (the
+            // waits count instructions): keep the compiler from interleaving them
+            asm volatile("" ::: "memory");
+            issue_next(0);
+            asm volatile("" ::: "memory");
+            if (n_it > 1) issue_next(1);
+            asm volatile("" ::: "memory");
+            int stage = 0, ckb = 0;
+            for (int it = 0; it < n_it; ++it) {
+                // this wave's copies of block it have landed (block it + 1 may
+                // still be in flight)
+                if (it + 1 < n_it) wait_copies<kCopies>();
+                else wait_copies<0>();
+                lds_barrier();
+                if (it + 2 < n_it) issue_next(stage == 0 ? 2 : stage - 1);
+                if (++ckb == KB) {
+                    for (int b = 0; b < OP::kEpilogueBarriers; ++b) lds_barrier();
+                    ckb = 0;
+                }
+                stage = stage == kStages - 1 ? 0 : stage + 1;
+            }
+        }
+    }
 }
 
 }  // namespace
 
 // ---------------------------------------------------------------- gate / up
 
-struct GroupedGateUpLds {
-    float sx[kMaxKb][kGroupM];       // activation scales of the tile rows per K block
-    float amax[4][kGroupM];          // per-wave row maxima of |h| over its 32 columns
-};
-
-// SCALE_PER_KB: per-128 activation scales or block weight scales (the fma
-// chain per K block); otherwise both scales are constant along K.
-template <bool SCALE_PER_KB>
-__global__ __launch_bounds__(kGThreads) void fp8_grouped_gateup_kernel(GroupedGateUpArgs a) {
-    __shared__ GroupedGateUpLds s;
-    const int L = xcd_tile(blockIdx.x, gridDim.x);
-    const int nt = L / a.max_tiles, mt = L % a.max_tiles;
-    const int I = a.w13.N / 2, H = a.w13.K, KB = H / 128;
-    if (nt >= I / 128) return;
-    const int e = a.tile_expert[mt];
-    if (e < 0) return;
-    const int m0 = a.tile_m0[mt], mend = a.offsets[e + 1];
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int col = lane % 16, grp = lane / 16;
-    const int hc = nt * 128 + wave * 32;  // first hidden column of this wave
-
-    // activation rows of the four m16 tiles (A operand rows: lane's row = col)
-    const uint8_t* arow[4];
-    bool alive[4];
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-        const int pos = m0 + mi * 16 + col;
-        alive[mi] = pos < mend;
-        const int64_t row = alive[mi] ? a.order[pos] / a.row_div : 0;
-        arow[mi] = a.xq + row * a.xq_row_stride + grp * 32;
+// PER_KB: per-128 activation scales or block weight scales (the fma chain per
+// K block); otherwise both scales are constant along K.  GU: compute dtype the
+// gate and up values are rounded through.
+template <bool PER_KB, int GU>
+struct GateUpOp {
+    using Args = GroupedGateUpArgs;
+    static constexpr bool kPerKb = PER_KB;
+    __device__ static int col_tiles(const Args& a) { return a.w13.N / 2 / 128; }
+    __device__ static int kblocks(const Args& a) { return a.w13.K / 128; }
+    __device__ static void brow(int wave, int (&b)[4]) {
+        b[0] = wave * 32;
+        b[1] = wave * 32 + 16;
+        b[2] = 128 + wave * 32;
+        b[3] = 128 + wave * 32 + 16;
     }
-    // activation scales of the 64 tile rows into LDS
-    for (int i = threadIdx.x; i < kGroupM * (a.x_group == 128 ? KB : 1); i += kGThreads) {
-        const int r = i % kGroupM, kb = i / kGroupM;
-        const int pos = m0 + r;
-        const int64_t row = pos < mend ? a.order[pos] / a.row_div : -1;
-        s.sx[kb][r] = row >= 0 ? a.xs[row * a.xs_row_stride + kb] : 0.0f;
+    // activation row of tile row r (rows past the expert repeat the first)
+    __device__ static void load_row(const Args& a, const TileMeta& m, int r, int& rowv, float&) {
+        const int pos = m.m0 + r < m.mend ? m.m0 + r : m.m0;
+        rowv = a.order[pos] / a.row_div;
     }
-    // weight rows: tiles 0, 1 = gate columns hc .. hc + 31, tiles 2, 3 = up
-    const uint8_t* brow[4];
-    int bn[4];
+    __device__ static void plan(const Args& a, const GemmLds& s, int t, int cw, int lane, int KB, TilePlan& p) {
+        const TileMeta m = s.meta[t];
+        const int I = a.w13.N / 2;
+        auto w_row = [&](int r) { return (r < 128 ? 0 : I) + m.nt * 128 + (r & 127); };
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-        bn[ni] = (ni < 2 ? 0 : I) + hc + (ni & 1) * 16 + col;
-        brow[ni] = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)bn[ni] * a.w13.w_sn + grp * 32;
-    }
-    __syncthreads();
-
-    const v4f zero = {0, 0, 0, 0};
-    v4f acc[4][4];
+        for (int j = 0; j < kAInst; ++j)
+            p.a[j] = a.xq + (int64_t)s.rowv[t][copy_row(a_copy(cw, j), lane)] * a.xq_row_stride + copy_chunk_bytes(lane);
+        p.bbase = a.w13.w + (int64_t)m.e * a.w13.w_se;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+        for (int j = 0; j < kBInst; ++j)
+            p.b[j] = (uint32_t)(w_row(copy_row(b_copy(cw, j), lane)) * a.w13.w_sn) + copy_chunk_bytes(lane);
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = zero;
-    const v8i zero8i = {0, 0, 0, 0, 0, 0, 0, 0};
-
-    // K pipeline: block kb + 1 (weight scales first, then operands) is in
-    // flight while block kb is multiplied; loads retire in issue order.
-    v8i ac[4], bc[4];
-    float swc[4];
-    if constexpr (SCALE_PER_KB) {
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) swc[ni] = proj_scale(a.w13, e, bn[ni], 0);
-    }
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) ac[mi] = alive[mi] ? load32(arow[mi]) : zero8i;
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) bc[ni] = load32(brow[ni]);
-    for (int kb = 0; kb < KB; ++kb) {
-        const bool more = kb + 1 < KB;
-        v8i an[4], bnx[4];
-        float swn[4];
-        if (more) {
-            if constexpr (SCALE_PER_KB) {
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni) swn[ni] = proj_scale(a.w13, e, bn[ni], kb + 1);
-            }
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) an[mi] = alive[mi] ? load32(arow[mi] + (kb + 1) * 128) : zero8i;
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) bnx[ni] = load32(brow[ni] + (kb + 1) * 128);
+        for (int j = 0; j < kScaleInst; ++j) {
+            const int q = s_copy(cw, j);
+            p.wsrc[j] = a.w13.s + (int64_t)m.e * a.w13.s_se + (int64_t)(w_row(q * 64 + lane) / a.w13.n_div) * a.w13.s_sn;
+            p.rsrc[j] = a.xs + (int64_t)s.rowv[t][q * 16 + lane % 16] * a.xs_row_stride;
         }
-        if constexpr (SCALE_PER_KB) {
+        p.ws_k = a.w13.s_sk;
+        p.kb_div = a.w13.kb_div;
+        p.rs_k = a.x_group == 128 ? 1 : 0;
+    }
+    // gate/up -> compute dtype, h = silu(gate) * up, FP8 per row over the
+    // tile's 128 columns, 16-byte stores of the hidden rows (multiplying
+    // waves; the copy waves pass the same two barriers).
+    static constexpr int kEpilogueBarriers = 2;
+    __device__ static void epilogue(const Args& a, GemmLds& s, int t, int stage, const int (&brow)[4],
+                                    const v4f (&acc)[4][4]) {
+        const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+        const int col = lane % 16, grp = lane / 16;
+        const TileMeta m = s.meta[t];
+        const int I = a.w13.N / 2;
+        float h[4][2][4];
+        {
+            float sw[4];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const int r = brow[ni] + col;
+                sw[ni] = s.ws[stage][r / 64][r % 64];
+            }
+            bool ok = true;
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi) {
-                const v4f sxv = *(const v4f*)&s.sx[a.x_group == 128 ? kb : 0][mi * 16 + grp * 4];
+                const v4f sxv = *(const v4f*)&s.rs[stage][mi][grp * 4];
 #pragma unroll
-                for (int ni = 0; ni < 4; ++ni) {
-                    const v4f d = mfma_fp8(ac[mi], bc[ni], zero);
+                for (int i = 0; i < 4; ++i) {
+                    float mx = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[mi][ni][i] = fmaf(d[i] * sxv[i], swc[ni], acc[mi][ni][i]);
+                    for (int tt = 0; tt < 2; ++tt) {
+                        float g = acc[mi][tt][i], u = acc[mi][tt + 2][i];
+                        if constexpr (!PER_KB) {
+                            g = g * sxv[i] * sw[tt];
+                            u = u * sxv[i] * sw[tt + 2];
+                        }
+                        g = round_gu<GU>(g);
+                        u = round_gu<GU>(u);
+                        const float hv = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+                        h[mi][tt][i] = hv;
+                        ok = ok && finite(hv);
+                        mx = fmaxf(mx, fabsf(hv));
+                    }
+                    mx = row_max(mx);  // over the 16 columns of the row
+                    if (col == 0) s.amax[wave][mi * 16 + grp * 4 + i] = mx;
                 }
             }
-        } else {
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma_fp8(ac[mi], bc[ni], acc[mi][ni]);
+            if (!ok) raise_status(a.status, kNonFinite);
         }
-        if (more) {
+        lds_barrier();
+        {
+            const int groups = I / 128;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ac[i] = an[i];
-                bc[i] = bnx[i];
-                swc[i] = swn[i];
+            for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = mi * 16 + grp * 4 + i;
+                    const float amax = fmaxf(fmaxf(s.amax[0][r], s.amax[1][r]), fmaxf(s.amax[2][r], s.amax[3][r]));
+                    const float scale = fp8_group_scale(amax);
+                    const float inv = 1.0f / scale;
+                    uint8_t* dst = s.hbuf + r * 128 + wave * 32 + col;
+                    dst[0] = (uint8_t)fp8_byte(h[mi][0][i] * inv);
+                    dst[16] = (uint8_t)fp8_byte(h[mi][1][i] * inv);
+                    if (wave == 0 && col == 0 && m.m0 + r < m.mend) a.hs[(int64_t)(m.m0 + r) * groups + m.nt] = scale;
+                }
+            }
+        }
+        lds_barrier();
+        {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int idx = threadIdx.x + k * kMmaWaves * kWave;
+                const int r = idx / 8, c = idx % 8;
+                const v4i v = *(const v4i*)(s.hbuf + r * 128 + c * 16);
+                if (m.m0 + r < m.mend) *(v4i*)(a.hq + (int64_t)(m.m0 + r) * I + m.nt * 128 + c * 16) = v;
             }
         }
     }
+};
 
-    // epilogue: gate/up -> compute dtype, h = silu(gate) * up, row maxima
-    float sw_end[4];
-    if constexpr (!SCALE_PER_KB) {
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) sw_end[ni] = proj_scale(a.w13, e, bn[ni], 0);
-    }
-    float h[4][2][4];
-    float rmax[4][4];
-    bool ok = true;
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-        const v4f sxv = *(const v4f*)&s.sx[0][mi * 16 + grp * 4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float m = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                float g = acc[mi][t][i], u = acc[mi][t + 2][i];
-                if constexpr (!SCALE_PER_KB) {
-                    g = g * sxv[i] * sw_end[t];
-                    u = u * sxv[i] * sw_end[t + 2];
-                }
-                g = round_through(g, a.gu_dtype);
-                u = round_through(u, a.gu_dtype);
-                const float hv = g / (1.0f + __expf(-g)) * u;
-                h[mi][t][i] = hv;
-                ok = ok && finite(hv);
-                m = fmaxf(m, fabsf(hv));
-            }
-            rmax[mi][i] = row_max(m);  // over the 16 columns of this lane row
-        }
-    }
-    if (!ok) raise_status(a.status, kNonFinite);
-    if (col == 0) {
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s.amax[wave][mi * 16 + grp * 4 + i] = rmax[mi][i];
-    }
-    __syncthreads();
-    const int groups = I / 128;
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = mi * 16 + grp * 4 + i;
-            const int pos = m0 + r;
-            if (pos >= mend) continue;
-            const float amax = fmaxf(fmaxf(s.amax[0][r], s.amax[1][r]), fmaxf(s.amax[2][r], s.amax[3][r]));
-            const float scale = fmaxf(amax, 1e-10f) * (1.0f / 448.0f);
-            uint8_t* dst = a.hq + (int64_t)pos * I + hc + col;
-            dst[0] = (uint8_t)fp8_encode(h[mi][0][i] / scale);
-            dst[16] = (uint8_t)fp8_encode(h[mi][1][i] / scale);
-            if (wave == 0 && col == 0) a.hs[(int64_t)pos * groups + nt] = scale;
-        }
-    }
+template <bool PER_KB, int GU>
+__global__ __launch_bounds__(kGThreads, 1) void fp8_grouped_gateup_kernel(GroupedGateUpArgs a) {
+    grouped_tiles<GateUpOp<PER_KB, GU>>(a);
 }
 
 // ---------------------------------------------------------------------- down
 
-struct GroupedDownLds {
-    float sh[kMaxInter / 128][kGroupM];  // hidden scales of the tile rows per K block
-    float wt[kGroupM];                   // route weights of the tile rows
-    int pair[kGroupM];                   // original pair index of the tile rows
-};
-
-constexpr int kDownCols = 256;  // output columns per workgroup (64 per wave)
-
-__global__ __launch_bounds__(kGThreads) void fp8_grouped_down_kernel(GroupedDownArgs a) {
-    __shared__ GroupedDownLds s;
-    const int L = xcd_tile(blockIdx.x, gridDim.x);
-    const int nt = L / a.max_tiles, mt = L % a.max_tiles;
-    const int H = a.w2.N, I = a.w2.K, KB = I / 128;
-    if (nt * kDownCols >= H) return;
-    const int e = a.tile_expert[mt];
-    if (e < 0) return;
-    const int m0 = a.tile_m0[mt], mend = a.offsets[e + 1];
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int col = lane % 16, grp = lane / 16;
-    const int n0 = nt * kDownCols + wave * 64;
-    const bool wave_live = n0 < H;  // H is a multiple of 128: whole waves drop out
-
-    for (int i = threadIdx.x; i < kGroupM * KB; i += kGThreads) {
-        const int r = i % kGroupM, kb = i / kGroupM;
-        const int pos = m0 + r;
-        s.sh[kb][r] = pos < mend ? a.hs[(int64_t)pos * KB + kb] : 0.0f;
+struct DownOp {
+    using Args = GroupedDownArgs;
+    static constexpr bool kPerKb = true;  // hidden scales change every 128-column block
+    __device__ static int col_tiles(const Args& a) { return (a.w2.N + kTileN - 1) / kTileN; }
+    __device__ static int kblocks(const Args& a) { return a.w2.K / 128; }
+    __device__ static void brow(int wave, int (&b)[4]) {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) b[ni] = wave * 64 + ni * 16;
     }
-    if (threadIdx.x < kGroupM) {
-        const int pos = m0 + threadIdx.x;
-        const int p = pos < mend ? a.order[pos] : -1;
-        s.pair[threadIdx.x] = p;
-        s.wt[threadIdx.x] = p >= 0 ? load_as_f32(a.weights, p, a.w_dtype) : 0.0f;
+    __device__ static void load_row(const Args& a, const TileMeta& m, int r, int& rowv, float& rowx) {
+        const int pos = m.m0 + r;
+        const int pr = pos < m.mend ? a.order[pos] : -1;
+        rowv = pr;
+        rowx = pr >= 0 ? load_as_f32(a.weights, pr, a.w_dtype) : 0.0f;
     }
-    const uint8_t* arow[4];
-    bool alive[4];
+    __device__ static void plan(const Args& a, const GemmLds& s, int t, int cw, int lane, int KB, TilePlan& p) {
+        const TileMeta m = s.meta[t];
+        const int H = a.w2.N, I = a.w2.K, n0 = m.nt * kTileN;
+        auto w_row = [&](int r) { return min(n0 + r, H - 1); };  // rows past H repeat the last
+        auto pos_of = [&](int r) { return m.m0 + r < m.mend ? m.m0 + r : m.m0; };
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-        const int pos = m0 + mi * 16 + col;
-        alive[mi] = pos < mend;
-        arow[mi] = a.hq + (int64_t)(alive[mi] ? pos : 0) * I + grp * 32;
-    }
-    const uint8_t* brow[4];
-    int bn[4];
+        for (int j = 0; j < kAInst; ++j)
+            p.a[j] = a.hq + (int64_t)pos_of(copy_row(a_copy(cw, j), lane)) * I + copy_chunk_bytes(lane);
+        p.bbase = a.w2.w + (int64_t)m.e * a.w2.w_se;
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-        bn[ni] = wave_live ? n0 + ni * 16 + col : 0;
-        brow[ni] = a.w2.w + (int64_t)e * a.w2.w_se + (int64_t)bn[ni] * a.w2.w_sn + grp * 32;
-    }
-    __syncthreads();
-    if (!wave_live) return;
-
-    const v4f zero = {0, 0, 0, 0};
-    const v8i zero8i = {0, 0, 0, 0, 0, 0, 0, 0};
-    v4f acc[4][4];
+        for (int j = 0; j < kBInst; ++j)
+            p.b[j] = (uint32_t)(w_row(copy_row(b_copy(cw, j), lane)) * a.w2.w_sn) + copy_chunk_bytes(lane);
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = zero;
-    v8i ac[4], bc[4];
-    float swc[4];
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) swc[ni] = proj_scale(a.w2, e, bn[ni], 0);
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) ac[mi] = alive[mi] ? load32(arow[mi]) : zero8i;
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) bc[ni] = load32(brow[ni]);
-    for (int kb = 0; kb < KB; ++kb) {
-        const bool more = kb + 1 < KB;
-        v8i an[4], bnx[4];
-        float swn[4];
-        if (more) {
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) swn[ni] = proj_scale(a.w2, e, bn[ni], kb + 1);
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) an[mi] = alive[mi] ? load32(arow[mi] + (kb + 1) * 128) : zero8i;
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) bnx[ni] = load32(brow[ni] + (kb + 1) * 128);
+        for (int j = 0; j < kScaleInst; ++j) {
+            const int q = s_copy(cw, j);
+            p.wsrc[j] = a.w2.s + (int64_t)m.e * a.w2.s_se + (int64_t)(w_row(q * 64 + lane) / a.w2.n_div) * a.w2.s_sn;
+            p.rsrc[j] = a.hs + (int64_t)pos_of(q * 16 + lane % 16) * KB;
         }
+        p.ws_k = a.w2.s_sk;
+        p.kb_div = a.w2.kb_div;
+        p.rs_k = 1;
+    }
+    // * route weight, then 16-byte stores of each pair's fp32 partial row: each
+    // 16x16 MFMA result goes through a per-wave LDS square so that a lane holds
+    // 4 consecutive columns of one row.
+    static constexpr int kEpilogueBarriers = 0;
+    __device__ static void epilogue(const Args& a, GemmLds& s, int t, int, const int (&brow)[4],
+                                    const v4f (&acc)[4][4]) {
+        const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+        const int col = lane % 16, grp = lane / 16;
+        const int rr = grp * 4 + lane % 4, cc = (col / 4) * 4;  // the row and first column a lane stores
+        const TileMeta m = s.meta[t];
+        const int H = a.w2.N, n0 = m.nt * kTileN;
+        float (*xt)[16] = s.xt[wave];
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
-            const v4f shv = *(const v4f*)&s.sh[kb][mi * 16 + grp * 4];
+            const int pr = s.rowv[t][mi * 16 + rr];
+            const float w = s.rowx[t][mi * 16 + rr];
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni) {
-                const v4f d = mfma_fp8(ac[mi], bc[ni], zero);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[mi][ni][i] = fmaf(d[i] * shv[i], swc[ni], acc[mi][ni][i]);
-            }
-        }
-        if (more) {
+                for (int i = 0; i < 4; ++i) xt[grp * 4 + i][col] = acc[mi][ni][i];
+                v4f o = *(const v4f*)&xt[rr][cc];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ac[i] = an[i];
-                bc[i] = bnx[i];
-                swc[i] = swn[i];
+                for (int i = 0; i < 4; ++i) o[i] *= w;
+                const int n = n0 + brow[ni] + cc;
+                if (pr >= 0 && n < H) *(v4f*)(a.partial + (int64_t)pr * a.partial_row_stride + n) = o;
             }
         }
     }
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = mi * 16 + grp * 4 + i;
-            const int p = s.pair[r];
-            if (p < 0) continue;
-            float* dst = a.partial + (int64_t)p * a.partial_row_stride + n0 + col;
-            const float w = s.wt[r];
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) dst[ni * 16] = acc[mi][ni][i] * w;
-        }
-    }
+};
+
+__global__ __launch_bounds__(kGThreads, 1) void fp8_grouped_down_kernel(GroupedDownArgs a) {
+    grouped_tiles<DownOp>(a);
 }
 
 // ------------------------------------------------------------------ combine
@@ -383,24 +559,37 @@ __global__ __launch_bounds__(256) void zero_invalid_rows_kernel(CombineArgs a) {
 
 // ----------------------------------------------------------------- launchers
 
-static unsigned grid_of(int col_tiles, int max_tiles) {
-    const int64_t g = (int64_t)col_tiles * max_tiles;
-    return (unsigned)((g + kXcds - 1) / kXcds * kXcds);
+// Persistent grid: one workgroup per CU, a multiple of the 8 XCDs.
+static unsigned persistent_grid() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+        cached[dev] = std::max(kXcds, cus / kXcds * kXcds);
+    }
+    return (unsigned)cached[dev];
 }
 
 void launch_fp8_grouped_gateup(const GroupedGateUpArgs& a, hipStream_t stream) {
-    const int col_tiles = a.w13.N / 2 / 128;
     // scales vary along K: per-128 activation groups or 128-column weight blocks
     const bool per_kb = a.x_group == 128 || a.w13.kb_div < a.w13.K / 128;
-    const dim3 grid(grid_of(col_tiles, a.max_tiles)), block(kGThreads);
-    if (per_kb) hipLaunchKernelGGL(fp8_grouped_gateup_kernel<true>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(fp8_grouped_gateup_kernel<false>, grid, block, 0, stream, a);
+    const dim3 grid(persistent_grid()), block(kGThreads);
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
+    if (per_kb) {
+        if (a.gu_dtype == kBF16) go(fp8_grouped_gateup_kernel<true, kBF16>);
+        else if (a.gu_dtype == kF16) go(fp8_grouped_gateup_kernel<true, kF16>);
+        else go(fp8_grouped_gateup_kernel<true, kF32>);
+    } else {
+        if (a.gu_dtype == kBF16) go(fp8_grouped_gateup_kernel<false, kBF16>);
+        else if (a.gu_dtype == kF16) go(fp8_grouped_gateup_kernel<false, kF16>);
+        else go(fp8_grouped_gateup_kernel<false, kF32>);
+    }
 }
 
 void launch_fp8_grouped_down(const GroupedDownArgs& a, hipStream_t stream) {
-    const int col_tiles = (a.w2.N + kDownCols - 1) / kDownCols;
-    hipLaunchKernelGGL(fp8_grouped_down_kernel, dim3(grid_of(col_tiles, a.max_tiles)), dim3(kGThreads), 0, stream,
-                       a);
+    hipLaunchKernelGGL(fp8_grouped_down_kernel, dim3(persistent_grid()), dim3(kGThreads), 0, stream, a);
 }
 
 void launch_zero_invalid_rows(const CombineArgs& a, hipStream_t stream) {

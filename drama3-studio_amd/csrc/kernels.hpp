@@ -141,6 +141,7 @@ struct PermuteArgs {
     int max_tiles;
     int32_t* tile_expert;
     int32_t* tile_m0;
+    int32_t* tile_count;    // optional: number of valid tiles
 };
 
 // Tile-map capacity for `pairs` route pairs over `experts` experts.
@@ -157,6 +158,7 @@ struct GroupedGateUpArgs {
     const int32_t* offsets;
     const int32_t* tile_expert;
     const int32_t* tile_m0;
+    const int32_t* tile_count;
     int max_tiles;
     const uint8_t* xq;      // [rows, H] FP8 activations, row = pair / row_div
     const float* xs;
@@ -175,6 +177,7 @@ struct GroupedDownArgs {
     const int32_t* offsets;
     const int32_t* tile_expert;
     const int32_t* tile_m0;
+    const int32_t* tile_count;
     int max_tiles;
     const uint8_t* hq;      // [pairs (sorted position), I]
     const float* hs;

@@ -266,6 +266,7 @@ __device__ void finish_permute(const PermuteArgs& a, const int* offs, int total,
         a.tile_m0[tstart + j] = offs[t] + j * a.block_m;
     }
     for (int x = ttotal + t; x < a.max_tiles; x += 1024) a.tile_expert[x] = -1;
+    if (t == 0 && a.tile_count) *a.tile_count = ttotal;
 }
 
 // Exclusive scan of the [blocks, experts] histogram table in (expert, block)
