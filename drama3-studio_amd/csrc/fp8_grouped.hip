@@ -49,7 +49,7 @@ namespace dmoe {
 namespace {
 
 constexpr int kMmaWaves = 4;                        // waves that multiply (and run the epilogues)
-constexpr int kCopyWaves = 2;                       // waves that issue every global -> LDS copy
+constexpr int kCopyWaves = 4;                       // waves that issue every global -> LDS copy
 constexpr int kGThreads = (kMmaWaves + kCopyWaves) * kWave;
 constexpr int kXcds = 8;
 constexpr int kTileN = 256;                         // weight rows of a tile
@@ -96,9 +96,11 @@ struct alignas(16) GemmLds {
     TileMeta meta[kChunk];
     int rowv[kChunk][kGroupM];           // gate/up: activation row; down: original pair (-1: none)
     float rowx[kChunk][kGroupM];         // down: route weight of the row
-    float amax[kMmaWaves][kGroupM];      // gate/up epilogue: per-wave row maxima of |h|
-    uint8_t hbuf[kGroupM * 128];         // gate/up epilogue: the FP8 hidden tile
-    float xt[kMmaWaves][16][16];         // down epilogue: per-wave 16x16 transpose of an MFMA result
+    float amax[kGroupM][kMmaWaves];      // gate/up epilogue: per-wave row maxima of |h|
+    union {
+        uint8_t hbuf[kGroupM * 128];     // gate/up epilogue: the FP8 hidden tile
+        float xt[kMmaWaves][4][16][16];  // down epilogue: per-wave transposes of four 16x16 MFMA results
+    };
 };
 
 // A copy wave's global sources for one tile.
@@ -142,14 +144,35 @@ __device__ __forceinline__ v8i lds_operand(const uint8_t* tile, int o0, int o1) 
     return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// One K block: acc[mi][ni] += rows 16 mi.. x B rows brow[ni]..  PER_KB:
-// acc = fma(dot * rs[row], ws[col], acc), the 16 block dot products issued
-// back to back before their scaling; otherwise the MFMA accumulates.  The
-// four B operands stay in registers; the A operands are read one row tile
-// ahead of the MFMAs that use them.
-template <bool PER_KB>
+// Block dot products waiting for their scaling (PER_KB): d[mi][ni] with the
+// row scales rs[mi] and column scales ws[ni] of their K block.
+struct PendingBlock {
+    v4f d[4][4];
+    v4f rs[4];
+    float ws[4];
+};
+
+// acc = fma(d * rs[row], ws[col], acc) for a pending block (row tile mi).
+__device__ __forceinline__ void apply_scaled(v4f (&acc)[4][4], const PendingBlock& p, int mi) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mi][ni][i] = fmaf(p.d[mi][ni][i] * p.rs[mi][i], p.ws[ni], acc[mi][ni][i]);
+}
+
+// One K block: acc[mi][ni] += rows 16 mi.. x B rows brow[ni]..  PER_KB: the
+// block's dot products are kept pending and scaled into acc while the next
+// block's MFMAs run (acc = fma(dot * rs[row], ws[col], acc), blocks in K
+// order; `pending` says whether the previous block's are waiting); otherwise
+// the MFMA accumulates.  The four B operands stay in registers; the A
+// operands are read one row tile ahead of the MFMAs that use them.
+//
+// SCALE: 0 = none (per-token x per-channel), 1 = per block, applied at once
+// (16 dot products issued back to back, then scaled), 2 = per block, deferred
+// into the next block as above (needs the PendingBlock registers).
+template <int SCALE>
 __device__ __forceinline__ void compute_block(const GemmLds& s, int stage, const int (&brow)[4], int o0, int o1,
-                                              v4f (&acc)[4][4]) {
+                                              v4f (&acc)[4][4], PendingBlock& pb, bool pending) {
     const int lane = threadIdx.x % kWave, grp = lane / 16, col = lane % 16;
     const v4f zero = {0, 0, 0, 0};
     const uint8_t* at = s.a[stage];
@@ -158,7 +181,7 @@ __device__ __forceinline__ void compute_block(const GemmLds& s, int stage, const
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) bf[ni] = lds_operand(bt + brow[ni] * 128, o0, o1);
     v8i af = lds_operand(at, o0, o1);
-    if constexpr (PER_KB) {
+    if constexpr (SCALE == 1) {
         v4f d[4][4];
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
@@ -182,15 +205,33 @@ __device__ __forceinline__ void compute_block(const GemmLds& s, int stage, const
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[mi][ni][i] = fmaf(d[mi][ni][i] * rsv[i], wsv[ni], acc[mi][ni][i]);
         }
-    } else {
+        return;
+    }
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-            v8i an = af;
-            if (mi < 3) an = lds_operand(at + (mi + 1) * 16 * 128, o0, o1);
+    for (int mi = 0; mi < 4; ++mi) {
+        v8i an = af;
+        if (mi < 3) an = lds_operand(at + (mi + 1) * 16 * 128, o0, o1);
+        if constexpr (SCALE == 2) {
+            v4f dn[4];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) dn[ni] = mfma_fp8(af, bf[ni], zero);
+            if (pending) apply_scaled(acc, pb, mi);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) pb.d[mi][ni] = dn[ni];
+        } else {
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma_fp8(af, bf[ni], acc[mi][ni]);
-            af = an;
         }
+        af = an;
+    }
+    if constexpr (SCALE == 2) {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const int r = brow[ni] + col;
+            pb.ws[ni] = s.ws[stage][r / 64][r % 64];
+        }
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) pb.rs[mi] = *(const v4f*)&s.rs[stage][mi][grp * 4];
     }
 }
 
@@ -257,11 +298,16 @@ __device__ __forceinline__ void grouped_tiles(const typename OP::Args& a) {
             for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = zero;
+            PendingBlock pb;
             int stage = 0, ct = 0, ckb = 0;
             for (int it = 0; it < n_it; ++it) {
                 lds_barrier();
-                compute_block<OP::kPerKb>(s, stage, brow, o0, o1, acc);
+                compute_block<OP::kScale>(s, stage, brow, o0, o1, acc, pb, ckb > 0);
                 if (++ckb == KB) {
+                    if constexpr (OP::kScale == 2) {
+#pragma unroll
+                        for (int mi = 0; mi < 4; ++mi) apply_scaled(acc, pb, mi);
+                    }
                     OP::epilogue(a, s, ct, stage, brow, acc);
 #pragma unroll
                     for (int mi = 0; mi < 4; ++mi)
@@ -315,10 +361,16 @@ __device__ __forceinline__ void grouped_tiles(const typename OP::Args& a) {
 // PER_KB: per-128 activation scales or block weight scales (the fma chain per
 // K block); otherwise both scales are constant along K.  GU: compute dtype the
 // gate and up values are rounded through.
+// Hidden column (within the tile's 128) held by gate/up tile row r (and r +
+// 128 for up): the wave's column tiles t = 0, 1 (rows 32 w + 16 t + c) hold
+// the adjacent columns 32 w + 2 c + t, so each lane's two h values of a row
+// are neighbours and quantize into one 16-bit pair.
+__device__ __forceinline__ int tile_column(int r) { return (r & ~31) | ((r & 15) << 1) | ((r >> 4) & 1); }
+
 template <bool PER_KB, int GU>
 struct GateUpOp {
     using Args = GroupedGateUpArgs;
-    static constexpr bool kPerKb = PER_KB;
+    static constexpr int kScale = PER_KB ? 1 : 0;
     __device__ static int col_tiles(const Args& a) { return a.w13.N / 2 / 128; }
     __device__ static int kblocks(const Args& a) { return a.w13.K / 128; }
     __device__ static void brow(int wave, int (&b)[4]) {
@@ -335,7 +387,7 @@ struct GateUpOp {
     __device__ static void plan(const Args& a, const GemmLds& s, int t, int cw, int lane, int KB, TilePlan& p) {
         const TileMeta m = s.meta[t];
         const int I = a.w13.N / 2;
-        auto w_row = [&](int r) { return (r < 128 ? 0 : I) + m.nt * 128 + (r & 127); };
+        auto w_row = [&](int r) { return (r < 128 ? 0 : I) + m.nt * 128 + tile_column(r & 127); };
 #pragma unroll
         for (int j = 0; j < kAInst; ++j)
             p.a[j] = a.xq + (int64_t)s.rowv[t][copy_row(a_copy(cw, j), lane)] * a.xq_row_stride + copy_chunk_bytes(lane);
@@ -354,8 +406,8 @@ struct GateUpOp {
         p.rs_k = a.x_group == 128 ? 1 : 0;
     }
     // gate/up -> compute dtype, h = silu(gate) * up, FP8 per row over the
-    // tile's 128 columns, 16-byte stores of the hidden rows (multiplying
-    // waves; the copy waves pass the same two barriers).
+    // tile's 128 columns, 16-byte stores of the hidden rows and their scales
+    // (multiplying waves; the copy waves pass the same two barriers).
     static constexpr int kEpilogueBarriers = 2;
     __device__ static void epilogue(const Args& a, GemmLds& s, int t, int stage, const int (&brow)[4],
                                     const v4f (&acc)[4][4]) {
@@ -364,66 +416,62 @@ struct GateUpOp {
         const TileMeta m = s.meta[t];
         const int I = a.w13.N / 2;
         float h[4][2][4];
-        {
-            float sw[4];
+        float sw[4];
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                const int r = brow[ni] + col;
-                sw[ni] = s.ws[stage][r / 64][r % 64];
-            }
-            bool ok = true;
+        for (int ni = 0; ni < 4; ++ni) {
+            const int r = brow[ni] + col;
+            sw[ni] = s.ws[stage][r / 64][r % 64];
+        }
+        float chk = 0.0f;  // stays 0 unless some h is inf / NaN
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const v4f sxv = *(const v4f*)&s.rs[stage][mi][grp * 4];
+        for (int mi = 0; mi < 4; ++mi) {
+            const v4f sxv = *(const v4f*)&s.rs[stage][mi][grp * 4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float mx = 0.0f;
+            for (int i = 0; i < 4; ++i) {
 #pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        float g = acc[mi][tt][i], u = acc[mi][tt + 2][i];
-                        if constexpr (!PER_KB) {
-                            g = g * sxv[i] * sw[tt];
-                            u = u * sxv[i] * sw[tt + 2];
-                        }
-                        g = round_gu<GU>(g);
-                        u = round_gu<GU>(u);
-                        const float hv = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
-                        h[mi][tt][i] = hv;
-                        ok = ok && finite(hv);
-                        mx = fmaxf(mx, fabsf(hv));
+                for (int tt = 0; tt < 2; ++tt) {
+                    float g = acc[mi][tt][i], u = acc[mi][tt + 2][i];
+                    if constexpr (!PER_KB) {
+                        g = g * sxv[i] * sw[tt];
+                        u = u * sxv[i] * sw[tt + 2];
                     }
-                    mx = row_max(mx);  // over the 16 columns of the row
-                    if (col == 0) s.amax[wave][mi * 16 + grp * 4 + i] = mx;
+                    g = round_gu<GU>(g);
+                    u = round_gu<GU>(u);
+                    h[mi][tt][i] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+                    chk = fmaf(h[mi][tt][i], 0.0f, chk);
                 }
-            }
-            if (!ok) raise_status(a.status, kNonFinite);
-        }
-        lds_barrier();
-        {
-            const int groups = I / 128;
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = mi * 16 + grp * 4 + i;
-                    const float amax = fmaxf(fmaxf(s.amax[0][r], s.amax[1][r]), fmaxf(s.amax[2][r], s.amax[3][r]));
-                    const float scale = fp8_group_scale(amax);
-                    const float inv = 1.0f / scale;
-                    uint8_t* dst = s.hbuf + r * 128 + wave * 32 + col;
-                    dst[0] = (uint8_t)fp8_byte(h[mi][0][i] * inv);
-                    dst[16] = (uint8_t)fp8_byte(h[mi][1][i] * inv);
-                    if (wave == 0 && col == 0 && m.m0 + r < m.mend) a.hs[(int64_t)(m.m0 + r) * groups + m.nt] = scale;
-                }
+                // max |h| over the row's 16 lanes; every lane of the row stores the same value
+                s.amax[mi * 16 + grp * 4 + i][wave] = row_max(fmaxf(fabsf(h[mi][0][i]), fabsf(h[mi][1][i])));
             }
         }
+        if (chk != 0.0f) raise_status(a.status, kNonFinite);
         lds_barrier();
-        {
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int idx = threadIdx.x + k * kMmaWaves * kWave;
-                const int r = idx / 8, c = idx % 8;
-                const v4i v = *(const v4i*)(s.hbuf + r * 128 + c * 16);
-                if (m.m0 + r < m.mend) *(v4i*)(a.hq + (int64_t)(m.m0 + r) * I + m.nt * 128 + c * 16) = v;
+        for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = mi * 16 + grp * 4 + i;
+                const v4f am = *(const v4f*)s.amax[r];
+                const float inv = 1.0f / fp8_group_scale(fmaxf(fmaxf(am[0], am[1]), fmaxf(am[2], am[3])));
+                const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_saturate(h[mi][0][i] * inv),
+                                                               fp8_saturate(h[mi][1][i] * inv), 0, false);
+                *(uint16_t*)(s.hbuf + r * 128 + wave * 32 + 2 * col) = (uint16_t)pk;
+            }
+        }
+        lds_barrier();
+        const int groups = I / 128;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int idx = threadIdx.x + k * kMmaWaves * kWave;
+            const int r = idx / 8, c = idx % 8;
+            const v4i v = *(const v4i*)(s.hbuf + r * 128 + c * 16);
+            if (m.m0 + r < m.mend) {
+                *(v4i*)(a.hq + (int64_t)(m.m0 + r) * I + m.nt * 128 + c * 16) = v;
+                if (c == 0) {
+                    const v4f am = *(const v4f*)s.amax[r];
+                    a.hs[(int64_t)(m.m0 + r) * groups + m.nt] =
+                        fp8_group_scale(fmaxf(fmaxf(am[0], am[1]), fmaxf(am[2], am[3])));
+                }
             }
         }
     }
@@ -438,7 +486,7 @@ __global__ __launch_bounds__(kGThreads, 1) void fp8_grouped_gateup_kernel(Groupe
 
 struct DownOp {
     using Args = GroupedDownArgs;
-    static constexpr bool kPerKb = true;  // hidden scales change every 128-column block
+    static constexpr int kScale = 2;  // hidden scales change every 128-column block: deferred scaling
     __device__ static int col_tiles(const Args& a) { return (a.w2.N + kTileN - 1) / kTileN; }
     __device__ static int kblocks(const Args& a) { return a.w2.K / 128; }
     __device__ static void brow(int wave, int (&b)[4]) {
@@ -473,9 +521,9 @@ struct DownOp {
         p.kb_div = a.w2.kb_div;
         p.rs_k = 1;
     }
-    // * route weight, then 16-byte stores of each pair's fp32 partial row: each
-    // 16x16 MFMA result goes through a per-wave LDS square so that a lane holds
-    // 4 consecutive columns of one row.
+    // * route weight, then 16-byte stores of each pair's fp32 partial row: the
+    // four 16x16 MFMA results of a row tile go through per-wave LDS squares so
+    // that a lane holds 4 consecutive columns of one row.
     static constexpr int kEpilogueBarriers = 0;
     __device__ static void epilogue(const Args& a, GemmLds& s, int t, int, const int (&brow)[4],
                                     const v4f (&acc)[4][4]) {
@@ -484,16 +532,18 @@ struct DownOp {
         const int rr = grp * 4 + lane % 4, cc = (col / 4) * 4;  // the row and first column a lane stores
         const TileMeta m = s.meta[t];
         const int H = a.w2.N, n0 = m.nt * kTileN;
-        float (*xt)[16] = s.xt[wave];
+        float (*xt)[16][16] = s.xt[wave];
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
             const int pr = s.rowv[t][mi * 16 + rr];
             const float w = s.rowx[t][mi * 16 + rr];
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
+            for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xt[grp * 4 + i][col] = acc[mi][ni][i];
-                v4f o = *(const v4f*)&xt[rr][cc];
+                for (int i = 0; i < 4; ++i) xt[ni][grp * 4 + i][col] = acc[mi][ni][i];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                v4f o = *(const v4f*)&xt[ni][rr][cc];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) o[i] *= w;
                 const int n = n0 + brow[ni] + cc;
