@@ -1,6 +1,7 @@
 // Router, route grouping and FP8 activation quantization of the MoE expert
 // path, plus the stable permutation of route pairs.
 #include <algorithm>
+#include <climits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -82,20 +83,102 @@ void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stre
 
 // ------------------------------------------------------------------ router
 
-// Stand-alone router: one workgroup per chunk of tokens.
+// Stand-alone router for many tokens: one wave per token, the logits in
+// registers (expert lane + 64 j in slot j).  Softmax max / sum, the winners'
+// probabilities and the slot-order renormalisation use exactly the order of
+// block_route (lane-strided partial max / sum, then the wave reduction), so
+// both routers give the same bits.  The k winners come from k rounds of a
+// wave-wide argmax over order-preserving keys (larger logit first, the lower
+// expert index on ties; NaN ranks above every number, as in block_route).
+// Reference: backbone_graph.py:317-323.
+constexpr int kRouteWaveSlots = kMaxExperts / kWave;
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    int x = (int)v;
+    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppXor1>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppXor2>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppHalfMirror>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppMirror>(x));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane(x, 0), b = (uint32_t)__builtin_amdgcn_readlane(x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane(x, 32), d = (uint32_t)__builtin_amdgcn_readlane(x, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ int wave_min_i32(int x) {
+    x = min(x, dpp_i32<kDppXor1>(x));
+    x = min(x, dpp_i32<kDppXor2>(x));
+    x = min(x, dpp_i32<kDppHalfMirror>(x));
+    x = min(x, dpp_i32<kDppMirror>(x));
+    return min(min(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+               min(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
 __global__ __launch_bounds__(256) void route_topk_kernel(RouteArgs a) {
-    __shared__ RouteScratch rs;
-    __shared__ int16_t ids[kRouteTokens * 64];
-    const RouteSource src{nullptr, kI64, a.logits, a.row_stride, a.top_k, a.renormalize, a.ids, a.weights,
-                          a.w_dtype};
-    const int chunk = max(1, min(kRouteTokens, kRouteElems / a.experts));
-    const int t0 = blockIdx.x * chunk;
-    block_route<256>(rs, src, t0, min(chunk, a.tokens - t0), a.experts, ids, true);
+    const int lane = threadIdx.x % kWave;
+    const int t = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    if (t >= a.tokens) return;  // whole waves
+    const int E = a.experts;
+    const float* row = a.logits + (int64_t)t * a.row_stride;
+    float l[kRouteWaveSlots], ex[kRouteWaveSlots];
+    uint32_t key[kRouteWaveSlots];
+    uint32_t avail = 0;
+#pragma unroll
+    for (int j = 0; j < kRouteWaveSlots; ++j) {
+        const int e = lane + kWave * j;
+        const bool ok = e < E;
+        l[j] = ok ? row[e] : 0.0f;
+        key[j] = ordered_bits(l[j]);
+        avail |= ok ? 1u << j : 0u;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kRouteWaveSlots; ++j)
+        if (avail >> j & 1) m = fmaxf(m, l[j]);
+    m = wave_max_dpp(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRouteWaveSlots; ++j) {
+        ex[j] = expf(l[j] - m);
+        if (avail >> j & 1) sum += ex[j];
+    }
+    sum = wave_sum_dpp(sum);
+    int my_id = 0;
+    float my_x = 0.0f;
+    for (int slot = 0; slot < a.top_k; ++slot) {
+        // this lane's best remaining logit (lower slot j = lower expert on ties)
+        uint32_t bk = 0;
+        int bj = -1;
+#pragma unroll
+        for (int j = 0; j < kRouteWaveSlots; ++j)
+            if ((avail >> j & 1) && (bj < 0 || key[j] > bk)) {
+                bk = key[j];
+                bj = j;
+            }
+        const uint32_t mk = wave_max_u32(bj >= 0 ? bk : 0u);
+        const int win = wave_min_i32(bj >= 0 && bk == mk ? lane + kWave * bj : INT_MAX);
+        const int wl = win % kWave, wj = win / kWave;
+        float xw = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kRouteWaveSlots; ++j)
+            if (j == wj) xw = ex[j];
+        xw = readlane_f32(xw, wl);
+        if (lane == wl) avail &= ~(1u << wj);
+        if (lane == slot) {
+            my_id = win;
+            my_x = xw;
+        }
+    }
+    const float p = lane < a.top_k ? my_x / sum : 0.0f;
+    float wtot = 0.0f;
+    for (int j = 0; j < a.top_k; ++j) wtot += readlane_f32(p, j);
+    if (lane < a.top_k) {
+        const float w = a.renormalize ? p / wtot : p;
+        a.ids[(int64_t)t * a.top_k + lane] = my_id;
+        store_from_f32(a.weights, (int64_t)t * a.top_k + lane, a.w_dtype, w);
+    }
 }
 
 void launch_route_topk(const RouteArgs& a, hipStream_t stream) {
-    const int chunk = std::max(1, std::min(kRouteTokens, kRouteElems / a.experts));
-    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((a.tokens + chunk - 1) / chunk)), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((a.tokens + 3) / 4)), dim3(256), 0, stream, a);
 }
 
 // ------------------------------------------------------------- decode prep
@@ -217,17 +300,19 @@ __global__ __launch_bounds__(kPermuteBlock) void permute_rank_kernel(PermuteArgs
     for (int x = t; x < a.experts; x += kPermuteBlock) a.hist[(int64_t)blockIdx.x * a.experts + x] = hist[x];
 }
 
-// Shared tail of the permutation kernels (1024 threads): offsets / counts from
-// the per-expert starts `offs` [experts + 1] (LDS), -1 past the valid pairs,
-// the active-expert list and the moe_align tile map.
+// Shared tail of the permutation kernels (THREADS >= experts threads):
+// offsets / counts from the per-expert starts `offs` [experts + 1] (LDS), -1
+// past the valid pairs, the active-expert list and the moe_align tile map.
+template <int THREADS>
 __device__ void finish_permute(const PermuteArgs& a, const int* offs, int total, int* wsum) {
+    constexpr int kWaves = THREADS / kWave;
     const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
-    for (int x = t; x < a.experts; x += 1024) {
+    for (int x = t; x < a.experts; x += THREADS) {
         a.offsets[x] = offs[x];
         a.counts[x] = offs[x + 1] - offs[x];
     }
     if (t == 0) a.offsets[a.experts] = total;
-    for (int64_t x = total + t; x < a.pairs; x += 1024) a.order[x] = -1;  // invalid pairs
+    for (int64_t x = total + t; x < a.pairs; x += THREADS) a.order[x] = -1;  // invalid pairs
     if (a.active) {  // ascending experts that have pairs
         __syncthreads();  // wsum is reused
         const int on = t < a.experts && offs[t + 1] > offs[t];
@@ -235,7 +320,7 @@ __device__ void finish_permute(const PermuteArgs& a, const int* offs, int total,
         if (lane == 0) wsum[wave] = __popcll(bits);
         __syncthreads();
         int before = __popcll(bits & ((1ull << lane) - 1)), count = 0;
-        for (int w = 0; w < 16; ++w) {
+        for (int w = 0; w < kWaves; ++w) {
             if (w < wave) before += wsum[w];
             count += wsum[w];
         }
@@ -256,7 +341,7 @@ __device__ void finish_permute(const PermuteArgs& a, const int* offs, int total,
     if (lane == kWave - 1) wsum[wave] = tincl;
     __syncthreads();
     int tbase = 0, ttotal = 0;
-    for (int w = 0; w < 16; ++w) {
+    for (int w = 0; w < kWaves; ++w) {
         if (w < wave) tbase += wsum[w];
         ttotal += wsum[w];
     }
@@ -265,7 +350,7 @@ __device__ void finish_permute(const PermuteArgs& a, const int* offs, int total,
         a.tile_expert[tstart + j] = t;
         a.tile_m0[tstart + j] = offs[t] + j * a.block_m;
     }
-    for (int x = ttotal + t; x < a.max_tiles; x += 1024) a.tile_expert[x] = -1;
+    for (int x = ttotal + t; x < a.max_tiles; x += THREADS) a.tile_expert[x] = -1;
     if (t == 0 && a.tile_count) *a.tile_count = ttotal;
 }
 
@@ -307,7 +392,7 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(PermuteArgs a) {
     }
     if (t == 0) offs[a.experts] = total;
     __syncthreads();
-    finish_permute(a, offs, total, wsum);
+    finish_permute<1024>(a, offs, total, wsum);
 }
 
 // Whole permutation in one workgroup for small calls (pairs <= 1024, one per
@@ -354,7 +439,72 @@ __global__ __launch_bounds__(1024) void permute_small_kernel(PermuteArgs a) {
         a.order[offs[e] + r] = t;
     }
     __syncthreads();  // wsum is reused by the tail
-    finish_permute(a, offs, total, wsum);
+    finish_permute<1024>(a, offs, total, wsum);
+}
+
+// Scan and scatter in one launch for up to kPlaceBlocks blocks: every
+// workgroup (one per block of kPermuteBlock pairs) sums the histogram column
+// of each expert over the blocks itself (the pairs of earlier blocks and the
+// expert's total), scans the totals into the expert starts, and places its
+// own pairs; workgroup 0 also writes offsets, counts and the tile map.
+constexpr int kPlaceBlocks = 256;
+constexpr int kPlaceThreads = kMaxExperts;
+static_assert(kPlaceThreads >= kPermuteBlock, "a place workgroup covers its block's pairs");
+
+__global__ __launch_bounds__(kPlaceThreads) void permute_place_kernel(PermuteArgs a) {
+    __shared__ int wsum[kPlaceThreads / kWave];
+    __shared__ int offs[kMaxExperts + 1];
+    __shared__ int base[kMaxExperts];
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    const int blocks = (a.pairs + kPermuteBlock - 1) / kPermuteBlock, b = blockIdx.x;
+    int before = 0, count = 0;
+    if (t < a.experts) {
+        // 16 independent loads in flight per step
+        int bb = 0;
+        for (; bb + 16 <= blocks; bb += 16) {
+            int c[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) c[j] = a.hist[(int64_t)(bb + j) * a.experts + t];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                before += bb + j < b ? c[j] : 0;
+                count += c[j];
+            }
+        }
+        for (; bb < blocks; ++bb) {
+            const int c = a.hist[(int64_t)bb * a.experts + t];
+            before += bb < b ? c : 0;
+            count += c;
+        }
+    }
+    int incl = count;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += v;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int excl = incl - count, total = 0;
+    for (int w = 0; w < kPlaceThreads / kWave; ++w) {
+        if (w < wave) excl += wsum[w];
+        total += wsum[w];
+    }
+    if (t < a.experts) {
+        offs[t] = excl;
+        base[t] = excl + before;
+    }
+    if (t == 0) offs[a.experts] = total;
+    __syncthreads();
+    const int64_t i = (int64_t)b * kPermuteBlock + t;
+    if (t < kPermuteBlock && i < a.pairs) {
+        const int code = a.rank[i];
+        if (code >= 0) a.order[base[code >> 16] + (code & 0xFFFF)] = (int32_t)i;
+    }
+    if (b == 0) {
+        __syncthreads();  // wsum is reused by the tail
+        finish_permute<kPlaceThreads>(a, offs, total, wsum);
+    }
 }
 
 __global__ __launch_bounds__(kPermuteBlock) void permute_scatter_kernel(PermuteArgs a) {
@@ -378,6 +528,10 @@ void launch_permute(const PermuteArgs& a, hipStream_t stream) {
     }
     const unsigned blocks = (unsigned)((a.pairs + kPermuteBlock - 1) / kPermuteBlock);
     hipLaunchKernelGGL(permute_rank_kernel, dim3(blocks), dim3(kPermuteBlock), 0, stream, a);
+    if (blocks <= kPlaceBlocks) {
+        hipLaunchKernelGGL(permute_place_kernel, dim3(blocks), dim3(kPlaceThreads), 0, stream, a);
+        return;
+    }
     hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
     hipLaunchKernelGGL(permute_scatter_kernel, dim3(blocks), dim3(kPermuteBlock), 0, stream, a);
 }

@@ -125,6 +125,22 @@ def test_route_topk_bit_exact_ids_and_order(cuda, tokens, experts, top_k):
     assert torch.max((wb.cpu().float() - ref).abs() / ref).item() <= 2 ** -7
 
 
+@pytest.mark.parametrize("tokens,experts", [(1, 128), (4, 128), (8, 32), (2, 512)])
+def test_standalone_router_equals_decode_router(cuda, tokens, experts):
+    """The many-token router (one wave per token) and the decode kernels'
+    workgroup router give the same ids and weight bits."""
+    print_case("router agreement", tokens, experts)
+    g = torch.Generator().manual_seed(99 + tokens * experts)
+    logits = torch.randn(tokens, experts, generator=g)
+    logits[0, 3] = logits[0, 5]  # a tie
+    staged = to_device(random_fp8_bank(experts, 256, 128, generator=g), cuda)
+    x = torch.randn(tokens, 256, generator=g).bfloat16().to(cuda)
+    _, w_dec, i_dec = HipExpertBackend().forward_routed(x, logits.to(cuda), 8, staged)
+    w_wave, i_wave = router.route_topk(logits.to(cuda), 8, dtype=w_dec.dtype)
+    assert torch.equal(i_wave, i_dec)
+    assert torch.equal(w_wave, w_dec)
+
+
 def test_route_topk_ties_take_the_lower_index(cuda):
     print_case("route_topk ties")
     logits = torch.full((2, 16), -1.0)
