@@ -62,6 +62,11 @@ constexpr int kEpochSlots = 32;      // call counters, spread over memory channe
 constexpr int kEpochStride = 256;    // bytes between two call counters
 constexpr uint64_t kSpinTicks = 20000000;  // 200 ms of the 100 MHz real-time counter
 
+// Calls with at most this many (token, expert) logits rank them with every
+// thread of the workgroup (at least two threads per logit); larger ones route
+// with one wave per token.
+constexpr int kRankRouteElems = kFzThreads / 2;
+
 struct FzLds {
     int16_t sid[kFusedMaxPairs];      // expert of each pair (-1: invalid)
     float wt[kFusedMaxPairs];         // route weight of each pair
@@ -70,7 +75,7 @@ struct FzLds {
     int plist[kFusedMaxPairs];        // pairs grouped by active expert, ascending
     int prow[kFusedMaxPairs];         // activation row of each plist entry (pair / row_div)
     int ucoord[kMaxUnitDepth][3];     // (first column, pair-list start, pair count) of each batch unit
-    alignas(16) uint32_t rkey[kRouteElems];  // ordered logit bits of every (token, expert)
+    alignas(16) uint32_t rkey[kRankRouteElems];  // ordered logit bits of every (token, expert)
     float rmax[kFusedMaxPairs], rsum[kFusedMaxPairs];  // softmax max / sum per token
     float rp[kFusedMaxPairs];         // softmax probability of each routed slot
     int num_active;
@@ -97,7 +102,7 @@ __device__ __forceinline__ uint64_t load_coherent_u64(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-constexpr int kRouteJ = kMaxExperts / kWave;  // logits per lane (experts l + 64 j)
+constexpr int kRouteJ = kRouteLaneSlots;  // logits per lane (experts l + 64 j)
 
 __device__ __forceinline__ void wave_route_load(const RouteSource& src, int t, int experts, float* l) {
     const int lane = threadIdx.x % kWave;
@@ -177,13 +182,15 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     }
 
     // -------------------------------------------------------- routing
-    // The router's order statistics in parallel: per token (one wave) the
-    // softmax max and sum exactly as the router kernel forms them, every
-    // logit's ordered bits into LDS; then every (token, expert) counts the
-    // experts ranked above it in (ordered bits desc, expert asc) order --
-    // rank = router slot -- with tpe neighbouring threads sharing the count;
-    // then one wave per token renormalizes its slots in slot order.
-    if (src.logits) {
+    // Small calls (rtokens * E <= kRankRouteElems): the router's order
+    // statistics in parallel -- per token (one wave) the softmax max and sum
+    // exactly as the router kernel forms them, every logit's ordered bits into
+    // LDS; then every (token, expert) counts the experts ranked above it in
+    // (ordered bits desc, expert asc) order -- rank = router slot -- with
+    // neighbouring threads sharing the count; then one wave per token
+    // renormalizes its slots in slot order.  Larger calls: one wave per token
+    // (wave_route_token), no barrier.  Both give the router kernels' bits.
+    if (src.logits && rtokens * E <= kRankRouteElems) {
         for (int t = wave; t < rtokens; t += kFzWaves) {
             if (t != wave) wave_route_load(src, t, E, lg);
             float m = -INFINITY;
@@ -254,6 +261,21 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 s.wt[t * src.top_k + lane] = round_through(w, src.w_dtype);
                 if (B == 0) {
                     src.ids_out[(int64_t)t * src.top_k + lane] = s.sid[t * src.top_k + lane];
+                    store_from_f32(src.weights_out, (int64_t)t * src.top_k + lane, src.w_dtype, w);
+                }
+            }
+        }
+    } else if (src.logits) {
+        for (int t = wave; t < rtokens; t += kFzWaves) {
+            if (t != wave) wave_route_load(src, t, E, lg);
+            int id;
+            float w;
+            wave_route_token(lg, E, src.top_k, src.renormalize, id, w);
+            if (lane < src.top_k) {
+                s.sid[t * src.top_k + lane] = (int16_t)id;
+                s.wt[t * src.top_k + lane] = round_through(w, src.w_dtype);
+                if (B == 0) {
+                    src.ids_out[(int64_t)t * src.top_k + lane] = id;
                     store_from_f32(src.weights_out, (int64_t)t * src.top_k + lane, src.w_dtype, w);
                 }
             }
@@ -662,7 +684,6 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
 bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize, int routed_tokens) {
     const int KBd = I / 128;
     return pairs >= 1 && pairs <= kFusedMaxPairs && rows >= 1 && (int64_t)rows * H <= kFusedXBytes &&
-           (int64_t)routed_tokens * experts <= kRouteElems &&
            (int64_t)rows * H * x_esize <= kFusedRawBytes && (int64_t)pairs * I <= kFusedHBytes &&
            H <= kFusedMaxH && I <= kFusedMaxI && H % kTileRows == 0 && experts <= kMaxExperts && top_k >= 1 &&
            top_k <= 64 && KBd >= 1 && KBd <= 8;

@@ -1,6 +1,8 @@
 // Workgroup router shared by the router, decode-prep and fused decode kernels.
 #pragma once
 
+#include <climits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -29,6 +31,92 @@ struct RouteScratch {
 __device__ __forceinline__ uint32_t ordered_bits(float v) {
     const uint32_t u = __float_as_uint(v + 0.0f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Max / min over all 64 lanes (DPP inside each 16-lane row, then the rows).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    int x = (int)v;
+    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppXor1>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppXor2>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppHalfMirror>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppMirror>(x));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane(x, 0), b = (uint32_t)__builtin_amdgcn_readlane(x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane(x, 32), d = (uint32_t)__builtin_amdgcn_readlane(x, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ int wave_min_i32(int x) {
+    x = min(x, dpp_i32<kDppXor1>(x));
+    x = min(x, dpp_i32<kDppXor2>(x));
+    x = min(x, dpp_i32<kDppHalfMirror>(x));
+    x = min(x, dpp_i32<kDppMirror>(x));
+    return min(min(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+               min(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
+constexpr int kRouteLaneSlots = kMaxExperts / kWave;  // logits per lane: experts lane + 64 j
+
+// One token routed by one wave, logits in registers (l[j] = expert lane +
+// 64 j).  Softmax max / sum, the winners' probabilities and the slot-order
+// renormalisation use exactly the order of block_route (lane-strided partial
+// max / sum, then the wave reduction), so both give the same bits.  The k
+// winners come from k rounds of a wave-wide argmax over order-preserving keys
+// (larger logit first, the lower expert on ties; NaN ranks above every
+// number, as in block_route).  Lane s < top_k receives slot s: its expert and
+// its weight (renormalised unless `renormalize` is 0, not yet rounded to the
+// weights dtype).  Reference: backbone_graph.py:317-323.
+__device__ __forceinline__ void wave_route_token(const float (&l)[kRouteLaneSlots], int experts, int top_k,
+                                                 int renormalize, int& id_out, float& w_out) {
+    const int lane = threadIdx.x % kWave;
+    uint32_t key[kRouteLaneSlots];
+    uint32_t avail = 0;
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kRouteLaneSlots; ++j) {
+        const bool ok = lane + kWave * j < experts;
+        key[j] = ordered_bits(l[j]);
+        avail |= ok ? 1u << j : 0u;
+        if (ok) m = fmaxf(m, l[j]);
+    }
+    m = wave_max_dpp(m);
+    float ex[kRouteLaneSlots];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRouteLaneSlots; ++j) {
+        ex[j] = expf(l[j] - m);
+        if (avail >> j & 1) sum += ex[j];
+    }
+    sum = wave_sum_dpp(sum);
+    int my_id = 0;
+    float my_x = 0.0f;
+    for (int slot = 0; slot < top_k; ++slot) {
+        // this lane's best remaining logit (lower j = lower expert on ties)
+        uint32_t bk = 0;
+        int bj = -1;
+#pragma unroll
+        for (int j = 0; j < kRouteLaneSlots; ++j)
+            if ((avail >> j & 1) && (bj < 0 || key[j] > bk)) {
+                bk = key[j];
+                bj = j;
+            }
+        const uint32_t mk = wave_max_u32(bj >= 0 ? bk : 0u);
+        const int win = wave_min_i32(bj >= 0 && bk == mk ? lane + kWave * bj : INT_MAX);
+        const int wl = win % kWave, wj = win / kWave;
+        float xw = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kRouteLaneSlots; ++j)
+            if (j == wj) xw = ex[j];
+        xw = readlane_f32(xw, wl);
+        if (lane == wl) avail &= ~(1u << wj);
+        if (lane == slot) {
+            my_id = win;
+            my_x = xw;
+        }
+    }
+    const float p = lane < top_k ? my_x / sum : 0.0f;
+    float wtot = 0.0f;
+    for (int j = 0; j < top_k; ++j) wtot += readlane_f32(p, j);
+    id_out = my_id;
+    w_out = renormalize ? p / wtot : p;
 }
 
 template <int THREADS>

@@ -83,96 +83,23 @@ void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stre
 
 // ------------------------------------------------------------------ router
 
-// Stand-alone router for many tokens: one wave per token, the logits in
-// registers (expert lane + 64 j in slot j).  Softmax max / sum, the winners'
-// probabilities and the slot-order renormalisation use exactly the order of
-// block_route (lane-strided partial max / sum, then the wave reduction), so
-// both routers give the same bits.  The k winners come from k rounds of a
-// wave-wide argmax over order-preserving keys (larger logit first, the lower
-// expert index on ties; NaN ranks above every number, as in block_route).
-// Reference: backbone_graph.py:317-323.
-constexpr int kRouteWaveSlots = kMaxExperts / kWave;
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    int x = (int)v;
-    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppXor1>(x));
-    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppXor2>(x));
-    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppHalfMirror>(x));
-    x = (int)max((uint32_t)x, (uint32_t)dpp_i32<kDppMirror>(x));
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane(x, 0), b = (uint32_t)__builtin_amdgcn_readlane(x, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane(x, 32), d = (uint32_t)__builtin_amdgcn_readlane(x, 48);
-    return max(max(a, b), max(c, d));
-}
-__device__ __forceinline__ int wave_min_i32(int x) {
-    x = min(x, dpp_i32<kDppXor1>(x));
-    x = min(x, dpp_i32<kDppXor2>(x));
-    x = min(x, dpp_i32<kDppHalfMirror>(x));
-    x = min(x, dpp_i32<kDppMirror>(x));
-    return min(min(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
-               min(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
-}
-
+// Stand-alone router for many tokens: one wave per token (wave_route_token).
 __global__ __launch_bounds__(256) void route_topk_kernel(RouteArgs a) {
     const int lane = threadIdx.x % kWave;
     const int t = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
     if (t >= a.tokens) return;  // whole waves
-    const int E = a.experts;
     const float* row = a.logits + (int64_t)t * a.row_stride;
-    float l[kRouteWaveSlots], ex[kRouteWaveSlots];
-    uint32_t key[kRouteWaveSlots];
-    uint32_t avail = 0;
+    float l[kRouteLaneSlots];
 #pragma unroll
-    for (int j = 0; j < kRouteWaveSlots; ++j) {
+    for (int j = 0; j < kRouteLaneSlots; ++j) {
         const int e = lane + kWave * j;
-        const bool ok = e < E;
-        l[j] = ok ? row[e] : 0.0f;
-        key[j] = ordered_bits(l[j]);
-        avail |= ok ? 1u << j : 0u;
+        l[j] = e < a.experts ? row[e] : 0.0f;
     }
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kRouteWaveSlots; ++j)
-        if (avail >> j & 1) m = fmaxf(m, l[j]);
-    m = wave_max_dpp(m);
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kRouteWaveSlots; ++j) {
-        ex[j] = expf(l[j] - m);
-        if (avail >> j & 1) sum += ex[j];
-    }
-    sum = wave_sum_dpp(sum);
-    int my_id = 0;
-    float my_x = 0.0f;
-    for (int slot = 0; slot < a.top_k; ++slot) {
-        // this lane's best remaining logit (lower slot j = lower expert on ties)
-        uint32_t bk = 0;
-        int bj = -1;
-#pragma unroll
-        for (int j = 0; j < kRouteWaveSlots; ++j)
-            if ((avail >> j & 1) && (bj < 0 || key[j] > bk)) {
-                bk = key[j];
-                bj = j;
-            }
-        const uint32_t mk = wave_max_u32(bj >= 0 ? bk : 0u);
-        const int win = wave_min_i32(bj >= 0 && bk == mk ? lane + kWave * bj : INT_MAX);
-        const int wl = win % kWave, wj = win / kWave;
-        float xw = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kRouteWaveSlots; ++j)
-            if (j == wj) xw = ex[j];
-        xw = readlane_f32(xw, wl);
-        if (lane == wl) avail &= ~(1u << wj);
-        if (lane == slot) {
-            my_id = win;
-            my_x = xw;
-        }
-    }
-    const float p = lane < a.top_k ? my_x / sum : 0.0f;
-    float wtot = 0.0f;
-    for (int j = 0; j < a.top_k; ++j) wtot += readlane_f32(p, j);
+    int id;
+    float w;
+    wave_route_token(l, a.experts, a.top_k, a.renormalize, id, w);
     if (lane < a.top_k) {
-        const float w = a.renormalize ? p / wtot : p;
-        a.ids[(int64_t)t * a.top_k + lane] = my_id;
+        a.ids[(int64_t)t * a.top_k + lane] = id;
         store_from_f32(a.weights, (int64_t)t * a.top_k + lane, a.w_dtype, w);
     }
 }
