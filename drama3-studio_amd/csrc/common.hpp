@@ -161,6 +161,13 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Workgroup barrier for LDS sharing only: this wave's LDS accesses are done,
+// then s_barrier.  Unlike __syncthreads() it does not wait for the wave's
+// outstanding global loads and stores (prefetched operands, published
+// results), which matter to no other wave; the memory clobber keeps the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ void raise_status(int* status, int bits) {
     if (status) __hip_atomic_fetch_or(status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

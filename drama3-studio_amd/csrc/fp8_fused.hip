@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 s.rsum[t] = sum;
             }
         }
-        __syncthreads();
+        lds_barrier();
         const int elems = rtokens * E;
         const int tpe = elems * 4 <= kFzThreads ? 4 : elems * 2 <= kFzThreads ? 2 : 1;
         const int sub = tid % tpe;
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 s.rp[t * src.top_k + rank] = expf(l - s.rmax[t]) / s.rsum[t];
             }
         }
-        __syncthreads();
+        lds_barrier();
         for (int t = wave; t < rtokens; t += kFzWaves) {
             const float p = lane < src.top_k ? s.rp[t * src.top_k + lane] : 0.0f;
             float wtot = 0.0f;
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (a.x_group != 128) {  // per-row scale: the maximum of the row's group maxima
 #pragma unroll
         for (int q = 0; q < kQuantPerGroup; ++q) {
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             s.start[na] = valid;
         }
     }
-    __syncthreads();
+    lds_barrier();
     const int num_active = s.num_active;
 
     // ------------------------------------------------- weight loads
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s.v.red[d][wave][lane][r] = acc[r];
             }
-            __syncthreads();
+            lds_barrier();
             epoch = s.epoch;
             {
                 const int d = tid / (16 * kUnitCols), m = (tid / kUnitCols) % 16, c = tid % kUnitCols;
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
-            __syncthreads();  // partials and coordinates read before they are overwritten
+            lds_barrier();  // partials and coordinates read before they are overwritten
         }
     };
     unit_batch(0);
@@ -503,9 +503,12 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         for (int d = 0; d < kUnitDepth; ++d) load_unit(j0 + d, d);
         unit_batch(j0);
     }
-    if (my_units == 0) __syncthreads();  // no gate/up barrier ran: order the epoch's LDS write
+    if (my_units == 0) lds_barrier();  // no gate/up barrier ran: order the epoch's LDS write
     epoch = s.epoch;
-    if (B >= tiles) return;  // no down rows for this workgroup
+    if (B >= tiles) {  // no down rows for this workgroup
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load outlives the wave
+        return;
+    }
 
     // rows of this wave's first down job (pass 0), looked up before the wait
     auto a_pair = [&](int ai, int idx) -> int {
@@ -649,13 +652,13 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
 
     for (int rt = B; rt < tiles; rt += G) {
         for (int i = tid; i < P * kTileRows; i += kFzThreads) s.v.part[i / kTileRows][i % kTileRows] = 0.0f;
-        __syncthreads();  // partials zeroed (invalid pairs stay 0); FP8 hidden complete
+        lds_barrier();  // partials zeroed (invalid pairs stay 0); FP8 hidden complete
         if (rt != B) load_job(rt, wave);
         for (int jj = 0; jj < my_jobs; ++jj) {
             if (jj > 0) load_job(rt, wave + jj * kFzWaves);
             compute_job(wave + jj * kFzWaves);
         }
-        __syncthreads();
+        lds_barrier();
         const int n0 = rt * kTileRows;
         if (a.out_pairs) {  // ordered fp32 partials, one row per pair
             for (int i = tid; i < P * kTileRows; i += kFzThreads) {
@@ -677,8 +680,9 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 store_from_f32(a.out, (int64_t)t * a.out_row_stride + n0 + c, a.out_dtype, acc);
             }
         }
-        __syncthreads();  // partials reused by the next tile
+        lds_barrier();  // partials reused by the next tile
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load outlives the wave
 }
 
 bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize, int routed_tokens) {

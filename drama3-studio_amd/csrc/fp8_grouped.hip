@@ -75,14 +75,12 @@ __device__ __forceinline__ void copy4_to_lds(const void* src, void* dst) {
 // wait_copies<N>: at most N vector-memory operations of this wave remain in
 // flight.  Vector loads (direct-to-LDS copies included) complete in issue
 // order, so with the youngest N-instruction copy group allowed in flight every
-// older copy has landed.  lds_barrier: this wave's LDS accesses are done, then
-// the workgroup synchronizes.  The memory clobbers keep the compiler from
-// moving LDS accesses across them.
+// older copy has landed.  The memory clobber keeps the compiler from moving
+// LDS accesses across it.
 template <int N>
 __device__ __forceinline__ void wait_copies() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 struct TileMeta {
     int nt, e, m0, mend;   // column tile, expert, sorted rows [m0, mend) (mend clipped to m0 + 64)
