@@ -927,19 +927,36 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
         if (out_pairs == nullptr) check_output(BankGeom{{}, {}, E, H, I}, out, out_dtype, out_row_stride, pairs, top_k);
         const QuantWorkspace ws = take_quant_workspace(rows, pairs, E, H, I, workspace, workspace_bytes);
         hipStream_t st = as_stream(stream);
-        quant_group(ids, ids_dtype, pairs, E, ws, status, st);
+        // small calls: launches that group the pairs themselves and keep the
+        // activation rotation (modes 1-3) and the combine inside
+        const bool small_up = fused_enabled() && dmoe::quant_gateup_decode_fits(mode, pairs, rows, H, I, x, x_dtype,
+                                                                                 x_row_stride);
+        const bool small_dn = fused_enabled() && dmoe::quant_down_decode_fits(mode, pairs, H, I);
+        if (!small_up || !small_dn) quant_group(ids, ids_dtype, pairs, E, ws, status, st);
         const int max_active = std::min(pairs, E);
 
-        quant_operand(up, x, x_dtype, x_row_stride, rows, H, ws.xq, ws.xs, st);
-        up.row_div = row_div;
-        up.order = ws.order;
-        up.offsets = ws.offsets;
-        up.active = ws.active;
-        up.gateup = 1;
-        up.act = ws.act;
-        up.status = status;
-        dmoe::launch_quant_projection(up, max_active, st);
+        if (small_up) {
+            const dmoe::QuantGateUpArgs ga{up, x, x_dtype, x_row_stride, rows, row_div, ids, ids_dtype, E, pairs,
+                                           ws.act, status};
+            dmoe::launch_quant_gateup_decode(ga, st);
+        } else {
+            quant_operand(up, x, x_dtype, x_row_stride, rows, H, ws.xq, ws.xs, st);
+            up.row_div = row_div;
+            up.order = ws.order;
+            up.offsets = ws.offsets;
+            up.active = ws.active;
+            up.gateup = 1;
+            up.act = ws.act;
+            up.status = status;
+            dmoe::launch_quant_projection(up, max_active, st);
+        }
 
+        if (small_dn) {
+            const dmoe::QuantDownArgs da{dn, ws.act, weights, weights_dtype, ids, ids_dtype, E, pairs,
+                                         out_pairs ? 1 : top_k, out, out_dtype, out_row_stride, out_pairs, status};
+            dmoe::launch_quant_down_decode(da, st);
+            return;
+        }
         quant_operand(dn, ws.act, DMOE_BF16, I, pairs, I, ws.actq, ws.acts, st);
         dn.row_div = 1;
         dn.order = ws.order;

@@ -307,4 +307,49 @@ struct QuantProjArgs {
 void launch_rotate_quant(const RotateArgs& a, hipStream_t stream);
 void launch_quant_projection(const QuantProjArgs& a, int max_active, hipStream_t stream);
 
+// Small packed calls (at most 64 route pairs): two launches that group the
+// pairs themselves from the route ids (no permutation launch).
+constexpr int kSmallPairs = 64;
+constexpr int kQgMaxRows = 4;          // activation rows of a small gate/up call
+constexpr int kQdMaxI = 1024;          // intermediate size of a small down call
+constexpr int kQdMaxRotRows = 16;      // pairs of a small INT8-mode down call
+constexpr int kQdMaxBf16 = 24576;      // pairs * I of a small mode-0 down call
+
+// Gate/up + SiLU of a small call: hidden rows [pairs, I] bf16 (act).
+struct QuantGateUpArgs {
+    QuantProjArgs w13;      // bank and mode (grouping fields unused)
+    const void* x;          // [rows, H]; pair p reads row p / row_div
+    int x_dtype;
+    int64_t x_row_stride;
+    int rows, row_div;
+    const void* ids;        // route id of every pair
+    int ids_dtype, experts, pairs;
+    uint16_t* act;
+    int* status;
+};
+// Calls of at most 64 pairs over at most 4 rows whose activation rows are
+// 16-byte aligned (pointer and row stride).
+bool quant_gateup_decode_fits(int mode, int pairs, int rows, int H, int I, const void* x, int x_dtype,
+                              int64_t x_row_stride);
+void launch_quant_gateup_decode(const QuantGateUpArgs& a, hipStream_t stream);
+
+// Down projection * route weight + the slot-order combine of a small call,
+// from the bf16 hidden rows [pairs, I].
+struct QuantDownArgs {
+    QuantProjArgs w2;       // bank and mode (grouping fields unused)
+    const uint16_t* act;
+    const void* weights;    // route weight of each pair
+    int w_dtype;
+    const void* ids;        // route id of every pair (the combine skips ids outside [0, experts))
+    int ids_dtype, experts;
+    int pairs, top_k;
+    void* out;              // [pairs / top_k, H] in out_dtype
+    int out_dtype;
+    int64_t out_row_stride;
+    float* out_pairs;       // or ordered fp32 partials [pairs, H]
+    int* status;
+};
+bool quant_down_decode_fits(int mode, int pairs, int H, int I);
+void launch_quant_down_decode(const QuantDownArgs& a, hipStream_t stream);
+
 }  // namespace dmoe

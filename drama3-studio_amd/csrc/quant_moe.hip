@@ -25,6 +25,7 @@
 // a 128-block: lane group g owns K [32 g, 32 g + 32); bf16 MFMA t (0..3) takes
 // [32 g + 8 t, +8), i8 MFMA j (0..1) takes [32 g + 16 j, +16) -- A and B agree.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -77,6 +78,68 @@ struct QuantLds {
 // (partners fetched with ds_bpermute).  One workgroup per row.
 __device__ __forceinline__ float neg_if(float v, bool neg) { return __uint_as_float(__float_as_uint(v) ^ (neg ? 0x80000000u : 0u)); }
 
+// N 256-blocks held by a wave, lane l at positions 4l .. 4l+3 of each:
+// v = the block times H4^{x4} in the stage order above (before the 1/16 and
+// rounding).  Each stage fetches every partner of all N blocks before it
+// combines any (the lane-permute latencies overlap); digit 1 (lane bits 0-1)
+// moves by DPP quad permutes, digits 2 and 3 by ds_bpermute.
+__device__ __forceinline__ float h4_combine(const float (&p)[4], int jd) {
+    float t = neg_if(p[0], jd == 3);  // H4(jd, j) = -1 iff jd + j == 3
+    t += neg_if(p[1], jd == 2);
+    t += neg_if(p[2], jd == 1);
+    t += neg_if(p[3], jd == 0);
+    return t;
+}
+
+template <int N>
+__device__ __forceinline__ void rotate_blocks(const float (&in)[N][4], float (&v)[N][4], int lane) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[i][j] = h4_combine(in[i], j);  // digit 0: inside the lane
+    {
+        const int jd = lane & 3;
+        float p[N][4][4];
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p[i][r][0] = dpp_f32<0x00>(v[i][r]);  // quad_perm [k, k, k, k]
+                p[i][r][1] = dpp_f32<0x55>(v[i][r]);
+                p[i][r][2] = dpp_f32<0xAA>(v[i][r]);
+                p[i][r][3] = dpp_f32<0xFF>(v[i][r]);
+            }
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[i][r] = h4_combine(p[i][r], jd);
+    }
+#pragma unroll
+    for (int d = 2; d < 4; ++d) {
+        const int shift = 2 * (d - 1);
+        const int jd = (lane >> shift) & 3;
+        const int rest = lane & ~(3 << shift);
+        float p[N][4][4];
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    p[i][r][k] = __int_as_float(__builtin_amdgcn_ds_bpermute((rest | (k << shift)) * 4, __float_as_int(v[i][r])));
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[i][r] = h4_combine(p[i][r], jd);
+    }
+}
+
+// INT8 of one rotated value: clamp(rint(v / s), +-127).
+__device__ __forceinline__ uint32_t quant_byte(float v, float sc) {
+    const float t = fminf(fmaxf(__builtin_rintf(v / sc), -127.0f), 127.0f);
+    return (uint32_t)(uint8_t)(int8_t)(int)t;
+}
+
 __global__ __launch_bounds__(256) void rotate_quant_kernel(RotateArgs a) {
     __shared__ float red[4];
     constexpr int kBlocksPerWave = kMaxQuantK / 256 / 4;
@@ -92,34 +155,10 @@ __global__ __launch_bounds__(256) void rotate_quant_kernel(RotateArgs a) {
         float in[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) in[r] = load_as_f32(a.x, base + r, a.x_dtype);
-        // digit 0: inside the lane, H4(i, j) = -1 iff i + j == 3
+        float one[1][4] = {{in[0], in[1], in[2], in[3]}}, out[1][4];
+        rotate_blocks<1>(one, out, lane);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float t = neg_if(in[0], j == 3);
-            t += neg_if(in[1], j == 2);
-            t += neg_if(in[2], j == 1);
-            t += neg_if(in[3], j == 0);
-            v[b][j] = t;
-        }
-        // digits 1..3: lane bits 2(d-1) .. 2(d-1)+1
-#pragma unroll
-        for (int d = 1; d < 4; ++d) {
-            const int shift = 2 * (d - 1);
-            const int jd = (lane >> shift) & 3;
-            const int rest = lane & ~(3 << shift);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float p[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    p[i] = __int_as_float(__builtin_amdgcn_ds_bpermute((rest | (i << shift)) * 4, __float_as_int(v[b][r])));
-                float t = neg_if(p[0], jd == 3);
-                t += neg_if(p[1], jd == 2);
-                t += neg_if(p[2], jd == 1);
-                t += neg_if(p[3], jd == 0);
-                v[b][r] = t;
-            }
-        }
+        for (int r = 0; r < 4; ++r) v[b][r] = out[0][r];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             v[b][r] = round_through(v[b][r] * 0.0625f, a.x_dtype);
@@ -137,10 +176,7 @@ __global__ __launch_bounds__(256) void rotate_quant_kernel(RotateArgs a) {
         if (c >= chunks) continue;
         uint32_t packed = 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float t = fminf(fmaxf(__builtin_rintf(v[b][r] / sc), -127.0f), 127.0f);
-            packed |= (uint32_t)(uint8_t)(int8_t)(int)t << (8 * r);
-        }
+        for (int r = 0; r < 4; ++r) packed |= quant_byte(v[b][r], sc) << (8 * r);
         *(uint32_t*)(a.q + (int64_t)row * a.q_row_stride + c * 256 + 4 * lane) = packed;
     }
     if (threadIdx.x == 0) a.scales[row] = sc;
@@ -157,23 +193,54 @@ struct WRow {
     v4i r[4];  // mode 0: 4 x (8 bf16 / fp16); modes 1-3: r[0], r[1] = 2 x 16 int8
 };
 
-template <int MODE, bool F16>
-__device__ __forceinline__ void load_wrow(const QuantProjArgs& a, int e, int n, int kb, int grp, const QuantLds& s,
-                                          WRow& out) {
+// Zero-point word of banks without qzeros (zero point 8 in every nibble), so
+// the mode-0 fetch loads a word either way.
+__device__ int32_t g_zero_point8 = (int32_t)0x88888888u;
+
+// The bytes a lane loads for one weight row's 128-K block (its 32 K values),
+// kept apart from the dequantization so loads can be issued early.
+struct WRaw {
+    v4i a;       // mode 0: 4 code words; mode 1: int8 bytes 0..15; modes 2, 3: low-nibble words
+    v4i b;       // mode 1: int8 bytes 16..31; mode 2: b[0], b[1] = 2-bit high planes
+    uint32_t x;  // mode 0: fp16 scale bits; modes 2, 3: the two e4m3 rel bytes
+    uint32_t z;  // mode 0: qzeros word (0x88888888: zero point 8)
+};
+
+template <int MODE>
+__device__ __forceinline__ WRaw fetch_wrow(const QuantProjArgs& a, int e, int n, int kb, int grp) {
     const uint8_t* w = a.w + (int64_t)e * a.w_se + (int64_t)n * a.w_sn;
     const uint8_t* sc = a.s + (int64_t)e * a.s_se + (int64_t)n * a.s_sn;
+    WRaw r{};
     if constexpr (MODE == 0) {
-        const v4i words = *(const v4i*)(w + kb * 64 + grp * 16);
-        const float scale = f16_to_f32(*(const uint16_t*)(sc + kb * 2));
-        int zp = 8;
-        if (a.z) {
-            const uint32_t zw = (uint32_t)a.z[(int64_t)e * a.z_se + (int64_t)kb * (a.N / 8) + n / 8];
-            zp = (int)((zw >> (4 * (n % 8))) & 15u);
+        r.a = *(const v4i*)(w + kb * 64 + grp * 16);
+        r.x = *(const uint16_t*)(sc + kb * 2);
+        const int32_t* zw = a.z ? a.z + (int64_t)e * a.z_se + (int64_t)kb * (a.N / 8) + n / 8 : &g_zero_point8;
+        r.z = (uint32_t)*zw;
+    } else if constexpr (MODE == 1) {
+        r.a = *(const v4i*)(w + kb * 128 + grp * 32);
+        r.b = *(const v4i*)(w + kb * 128 + grp * 32 + 16);
+    } else {
+        // 32 codes: low nibbles (16 bytes), mode 2 also 2-bit high parts (8 bytes)
+        r.a = *(const v4i*)(w + kb * 64 + grp * 16);
+        if constexpr (MODE == 2) {
+            const uint2 high = *(const uint2*)(w + a.K / 2 + kb * 32 + grp * 8);
+            r.b[0] = (int)high.x;
+            r.b[1] = (int)high.y;
         }
+        r.x = *(const uint16_t*)(sc + kb * 8 + grp * 2);
+    }
+    return r;
+}
+
+template <int MODE, bool F16>
+__device__ __forceinline__ void decode_wrow(const WRaw& raw, int n, const float* book, WRow& out) {
+    if constexpr (MODE == 0) {
+        const float scale = f16_to_f32((uint16_t)raw.x);
+        const int zp = (int)((raw.z >> (4 * (n % 8))) & 15u);
         const float bias = -(float)zp * scale;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const uint32_t u = (uint32_t)words[t];
+            const uint32_t u = (uint32_t)raw.a[t];
             float v[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = fmaf((float)((u >> (4 * i)) & 15u), scale, bias);  // exact
@@ -182,15 +249,10 @@ __device__ __forceinline__ void load_wrow(const QuantProjArgs& a, int e, int n, 
                 out.r[t][i] = (int)(F16 ? pack_f16(v[2 * i], v[2 * i + 1]) : pack_bf16(v[2 * i], v[2 * i + 1]));
         }
     } else if constexpr (MODE == 1) {
-        out.r[0] = *(const v4i*)(w + kb * 128 + grp * 32);
-        out.r[1] = *(const v4i*)(w + kb * 128 + grp * 32 + 16);
+        out.r[0] = raw.a;
+        out.r[1] = raw.b;
     } else {
-        // 32 codes: low nibbles (16 bytes), mode 2 also 2-bit high parts (8 bytes)
-        const v4i low = *(const v4i*)(w + kb * 64 + grp * 16);
-        uint2 high = {0u, 0u};
-        if constexpr (MODE == 2) high = *(const uint2*)(w + a.K / 2 + kb * 32 + grp * 8);
-        const uint32_t rel2 = *(const uint16_t*)(sc + kb * 8 + grp * 2);
-        const float rel[2] = {e4m3(rel2), e4m3(rel2 >> 8)};
+        const float rel[2] = {e4m3(raw.x), e4m3(raw.x >> 8)};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {  // 16 codes = K [32 g + 16 j, +16): one rel group
 #pragma unroll
@@ -199,14 +261,14 @@ __device__ __forceinline__ void load_wrow(const QuantProjArgs& a, int e, int n, 
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
                     const int c = j * 16 + q * 4 + b;  // code index within the lane's 32
-                    const uint32_t lo = ((uint32_t)low[c / 8] >> (4 * (c % 8))) & 15u;
+                    const uint32_t lo = ((uint32_t)raw.a[c / 8] >> (4 * (c % 8))) & 15u;
                     float level;
                     if constexpr (MODE == 2) {
-                        const uint32_t hw = c < 16 ? high.x : high.y;
+                        const uint32_t hw = (uint32_t)(c < 16 ? raw.b[0] : raw.b[1]);
                         const uint32_t hi = (hw >> (2 * (c % 16))) & 3u;
                         level = (float)(int)(lo | (hi << 4)) - 32.0f;
                     } else {
-                        level = s.book[lo];
+                        level = book[lo];
                     }
                     packed |= ((uint32_t)(uint8_t)q8(level, rel[j])) << (8 * b);
                 }
@@ -214,6 +276,12 @@ __device__ __forceinline__ void load_wrow(const QuantProjArgs& a, int e, int n, 
             }
         }
     }
+}
+
+template <int MODE, bool F16>
+__device__ __forceinline__ void load_wrow(const QuantProjArgs& a, int e, int n, int kb, int grp, const float* book,
+                                          WRow& out) {
+    decode_wrow<MODE, F16>(fetch_wrow<MODE>(a, e, n, kb, grp), n, book, out);
 }
 
 template <int MODE>
@@ -249,8 +317,8 @@ __global__ __launch_bounds__(kQThreads) void quant_proj_kernel(QuantProjArgs a) 
     for (int i = 0; i < KBW; ++i) {
         const int kb = wave + i * kQWaves;
         if (kb < KB) {
-            load_wrow<MODE, F16>(a, e, ng, kb, grp, s, bg[i]);
-            if constexpr (GATEUP) load_wrow<MODE, F16>(a, e, nu, kb, grp, s, bu[i]);
+            load_wrow<MODE, F16>(a, e, ng, kb, grp, s.book, bg[i]);
+            if constexpr (GATEUP) load_wrow<MODE, F16>(a, e, nu, kb, grp, s.book, bu[i]);
         }
     }
     float sbg = 1.0f, sbu = 1.0f;
@@ -344,6 +412,645 @@ __global__ __launch_bounds__(kQThreads) void quant_proj_kernel(QuantProjArgs a) 
             }
         }
         __syncthreads();
+    }
+}
+
+// ------------------------------------------------------- small-call grouping
+
+// Calls of at most 64 route pairs group their pairs inside every workgroup
+// instead of a permutation launch: one wave holds pair p in lane p and ranks
+// by cross-lane reads -- the distinct valid experts ascending (active), each
+// with its pairs ascending (plist[start[u] .. start[u + 1])), the order of
+// the stable permutation.
+struct SmallGroups {
+    int num_active;
+    int active[kSmallPairs];
+    int start[kSmallPairs + 1];
+    int plist[kSmallPairs];
+};
+
+// Raw loads whose values are first used much later: converting right after
+// the load (inside a dtype branch) would make the wave wait for it there and
+// hold back every load issued after it.
+__device__ __forceinline__ uint2 load_id_bits(const void* ids, int i, int dtype) {
+    uint2 r = {0u, 0u};
+    if (dtype == kI64) r = ((const uint2*)ids)[i];
+    else r.x = ((const uint32_t*)ids)[i];
+    return r;
+}
+
+// The expert of a route id, -1 when outside [0, experts).
+__device__ __forceinline__ int id_expert(uint2 r, int dtype, int experts) {
+    const int64_t id = dtype == kI64 ? (int64_t)(((uint64_t)r.y << 32) | r.x) : (int64_t)(int32_t)r.x;
+    return id >= 0 && id < experts ? (int)id : -1;
+}
+
+__device__ __forceinline__ uint32_t load_bits(const void* p, int i, int dtype) {
+    return dtype == kF32 ? ((const uint32_t*)p)[i] : (uint32_t)((const uint16_t*)p)[i];
+}
+
+__device__ __forceinline__ float bits_to_f32(uint32_t b, int dtype) {
+    if (dtype == kF32) return __uint_as_float(b);
+    if (dtype == kBF16) return __uint_as_float(b << 16);
+    return f16_to_f32((uint16_t)b);
+}
+
+// Four consecutive activation values at element i of type XT, one load
+// (8-byte aligned for 16-bit types, 16-byte for fp32).
+// --------------------------------------------- block rotation, 16 per lane
+
+// A wave rotates four 256-blocks at a time, 16 lanes per block.  Phase A:
+// lane m of a block holds positions 16 m + i (i = 0..15, base-4 digits 0 and
+// 1 of the position inside the lane), so stages 0 and 1 are register adds
+// with constant signs.  A transposition through LDS (17 dwords per 16
+// values: conflict-free both ways) gives phase B: lane m holds positions
+// 16 i + m (digits 2 and 3 inside the lane) for stages 2 and 3.  Each output
+// is ((h0 p0 + h1 p1) + h2 p2) + h3 p3 in digit order with H4's signs -- the
+// stage arithmetic of rotate_quant_kernel.
+constexpr int kRotBlockDwords = 272;  // transposition buffer per block (16 x 17)
+constexpr int kRotWaveDwords = 4 * kRotBlockDwords;
+
+// 16 consecutive activation values of type XT as loaded (16-byte loads),
+// converted only when used.
+template <int XT>
+struct Raw16 {
+    uint32_t w[XT == kF32 ? 16 : 8];
+};
+
+template <int XT>
+__device__ __forceinline__ Raw16<XT> load_raw16(const void* x, int64_t i) {
+    Raw16<XT> r;
+    const uint4* p = (const uint4*)((const char*)x + i * (XT == kF32 ? 4 : 2));
+#pragma unroll
+    for (int k = 0; k < (int)(sizeof(r.w) / 16); ++k) {
+        const uint4 q = p[k];
+        r.w[4 * k] = q.x;
+        r.w[4 * k + 1] = q.y;
+        r.w[4 * k + 2] = q.z;
+        r.w[4 * k + 3] = q.w;
+    }
+    return r;
+}
+
+template <int XT>
+__device__ __forceinline__ void convert16(const Raw16<XT>& r, float (&v)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if constexpr (XT == kF32) v[i] = __uint_as_float(r.w[i]);
+        else if constexpr (XT == kBF16) v[i] = __uint_as_float(i % 2 ? r.w[i / 2] & 0xFFFF0000u : r.w[i / 2] << 16);
+        else v[i] = f16_to_f32((uint16_t)(r.w[i / 2] >> (16 * (i % 2))));
+    }
+}
+
+// Compiler fence: loads issued before it stay before it, and work on the
+// raw words stays after it (the asm reads and rewrites them), so waiting for
+// them waits only for loads issued earlier.
+template <int XT, int N>
+__device__ __forceinline__ void pin_after_loads(Raw16<XT> (&r)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+        for (int k = 0; k < (int)(sizeof(r[i].w) / 4); ++k) asm volatile("" : "+v"(r[i].w[k])::"memory");
+}
+
+// One H4 stage along the digit at register stride STRIDE (1: low digit of
+// the register index, 4: high digit).
+template <int STRIDE>
+__device__ __forceinline__ void h4_stage(float (&v)[16]) {
+    float o[16];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const int b = STRIDE == 1 ? 4 * h : h;  // register of digit value k: b + STRIDE * k
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {  // H4(j, k) = -1 iff j + k == 3
+            float t = j == 3 ? -v[b] : v[b];
+            t += j == 2 ? -v[b + STRIDE] : v[b + STRIDE];
+            t += j == 1 ? -v[b + 2 * STRIDE] : v[b + 2 * STRIDE];
+            t += j == 0 ? -v[b + 3 * STRIDE] : v[b + 3 * STRIDE];
+            o[b + STRIDE * j] = t;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = o[i];
+}
+
+// Phase A in, phase B out (before the 1/16); tb = this wave's buffer.
+__device__ __forceinline__ void rotate16(float (&v)[16], float* tb, int lane) {
+    h4_stage<1>(v);
+    h4_stage<4>(v);
+    float* blk = tb + (lane / 16) * kRotBlockDwords;
+    const int m = lane % 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) blk[17 * m + i] = v[i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = blk[17 * i + m];
+    h4_stage<1>(v);
+    h4_stage<4>(v);
+}
+
+// Whole wave; e = the expert of pair `lane`, -1 for invalid or absent pairs.
+__device__ __forceinline__ void group_pairs(int e, int P, int lane, SmallGroups& g) {
+    int rank = 0, before = 0;
+    for (int q = 0; q < P; ++q) {
+        const int eq = __builtin_amdgcn_readlane(e, q);
+        rank += (eq == e) & (q < lane);
+        before += (eq >= 0) & (eq < e);
+    }
+    const int first = e >= 0 && rank == 0;
+    int dless = 0;  // distinct experts below e
+    for (int q = 0; q < P; ++q) {
+        const int eq = __builtin_amdgcn_readlane(e, q), fq = __builtin_amdgcn_readlane(first, q);
+        dless += fq & (eq < e);
+    }
+    if (e >= 0) g.plist[before + rank] = lane;
+    if (first) {
+        g.active[dless] = e;
+        g.start[dless] = before;
+    }
+    const int na = __popcll(__ballot(first)), valid = __popcll(__ballot(e >= 0));
+    if (lane == 0) {
+        g.num_active = na;
+        g.start[na] = valid;
+    }
+}
+
+// ------------------------------------------------------ small-call gate/up
+
+// Calls of at most 64 pairs over at most 4 activation rows: workgroup =
+// (active expert, 16 gate + 16 up columns), 8 waves splitting the K blocks as
+// quant_proj_kernel does.  The workgroup groups the pairs itself, stages the
+// activation rows in LDS -- modes 1-3 rotated and INT8-quantized there with
+// rotate_quant_kernel's arithmetic -- and issues its weight loads before the
+// rotation, so the two overlap.  Output: act = bf16(bf16(silu(g)) * u).
+constexpr int kQgUnits = 4;  // rotated 256-blocks per wave, 16 lanes each: rows * H / 256 <= 32
+
+struct QGateUpLds {
+    SmallGroups g;
+    union {
+        alignas(16) int8_t q[kQgMaxRows * kMaxQuantK];        // modes 1-3: rotated INT8 rows
+        alignas(16) uint16_t h[kQgMaxRows * kMaxQuantK / 2];  // mode 0: the bf16 / fp16 rows
+    } x;
+    float sa[kQgMaxRows];
+    uint32_t rmax[kQgMaxRows];  // row maxima (non-negative float bits)
+    float book[16];
+    union {
+        float tb[kQWaves][kRotWaveDwords];  // rotation transposes
+        float red[kQWaves][kWave][8];       // cross-wave reduction
+    };
+};
+
+template <int MODE, int XT, int KBW>
+__global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGateUpArgs a) {
+    constexpr bool F16 = XT == kF16;
+    __shared__ QGateUpLds s;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int col = lane % 16, grp = lane / 16;
+    const QuantProjArgs& w = a.w13;
+    const int H = w.K, I = w.N / 2, KB = H / 128, P = a.pairs, rows = a.rows;
+    const int n0 = blockIdx.y * 16;
+
+    // loads are issued unconditionally (clamped indexes): a load merged with
+    // a constant on another path is waited for at the merge
+    const uint2 idb = load_id_bits(a.ids, min(lane, P - 1), a.ids_dtype);
+    // activation rows: every load issued now (clamped to the last unit)
+    const int nb = H / 256, units = rows * nb;
+    const int my_u = kQgUnits * wave + lane / 16;  // this lane's block (16 lanes each)
+    Raw16<XT> xin[1];
+    if constexpr (MODE != 0) {
+        const int u = min(my_u, units - 1);
+        xin[0] = load_raw16<XT>(a.x, (int64_t)(u / nb) * a.x_row_stride + (u % nb) * 256 + 16 * (lane % 16));
+        if ((int)threadIdx.x < rows) s.rmax[threadIdx.x] = 0u;
+    } else {
+        constexpr int kChunks = kQgMaxRows * kMaxQuantK / 2 / 8 / kQThreads;  // 16-byte chunks per thread
+        const int cpr = H / 8, chunks = rows * cpr;
+        v4i c16[kChunks];
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const int i = min((int)threadIdx.x + j * kQThreads, chunks - 1);
+            c16[j] = *(const v4i*)((const uint16_t*)a.x + (i / cpr) * a.x_row_stride + (i % cpr) * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const int i = threadIdx.x + j * kQThreads;
+            if (i < chunks) *(v4i*)(s.x.h + (i / cpr) * H + (i % cpr) * 8) = c16[j];
+        }
+    }
+    if (wave == 0) {
+        const int pe = lane < P ? id_expert(idb, a.ids_dtype, a.experts) : -1;
+        if (lane < P && pe < 0 && blockIdx.x == 0 && blockIdx.y == 0) raise_status(a.status, kBadExpertId);
+        group_pairs(pe, P, lane, s.g);
+    }
+    lds_barrier();
+    if ((int)blockIdx.x >= s.g.num_active) {  // uniform: fewer distinct experts than the grid assumed
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
+    const int ai = blockIdx.x;
+    const int e = s.g.active[ai], pbeg = s.g.start[ai], pend = s.g.start[ai + 1];
+    const int ng = n0 + col, nu = I + n0 + col;
+
+    // weight rows of this wave, loaded now, dequantized after the rotation
+    WRaw rg[KBW], ru[KBW];
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+        const int kb = min(wave + i * kQWaves, KB - 1);  // blocks past K: loaded, never used
+        rg[i] = fetch_wrow<MODE>(w, e, ng, kb, grp);
+        ru[i] = fetch_wrow<MODE>(w, e, nu, kb, grp);
+    }
+    float sbg = 1.0f, sbu = 1.0f, bk = 0.0f;
+    if constexpr (MODE != 0) {
+        sbg = channel_scale<MODE>(w, e, ng);
+        sbu = channel_scale<MODE>(w, e, nu);
+    }
+    if constexpr (MODE == 3)  // codebook entry lane % 16 (rows 0..15 of the aux bytes)
+        bk = *(const float*)(w.s + (int64_t)e * w.s_se + (int64_t)(lane % 16) * w.s_sn + H / 16 + 4);
+
+    if constexpr (MODE != 0) {
+        pin_after_loads(xin);  // keeps the rotation behind the weight loads
+        const bool busy = kQgUnits * wave < units;  // wave-uniform
+        float v[16];
+        if (busy) {
+            convert16(xin[0], v);
+            rotate16(v, s.tb[wave], lane);  // lanes past the last block: duplicates, never stored
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                v[i] = round_through(v[i] * 0.0625f, XT);
+                amax = fmaxf(amax, fabsf(v[i]));
+            }
+            amax = row_max(amax);
+            if (my_u < units && lane % 16 == 0) atomicMax(&s.rmax[my_u / nb], __float_as_uint(amax));
+        }
+        lds_barrier();
+        if (busy && my_u < units) {  // INT8 bytes at positions 16 i + m of the block
+            const int row = my_u / nb, c = my_u % nb, m = lane % 16;
+            const float sc = fmaxf(__uint_as_float(s.rmax[row]), 1e-12f) / 127.0f;
+            int8_t* dst = s.x.q + row * H + c * 256 + m;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dst[16 * i] = (int8_t)quant_byte(v[i], sc);
+            if (c == 0 && m == 0) s.sa[row] = sc;
+        }
+    }
+    if constexpr (MODE == 3) {
+        if (threadIdx.x < 16) s.book[threadIdx.x] = bk;
+    }
+    lds_barrier();
+
+    WRow bg[KBW], bu[KBW];
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+        const int kb = wave + i * kQWaves;
+        if (kb < KB) {
+            decode_wrow<MODE, F16>(rg[i], ng, s.book, bg[i]);
+            decode_wrow<MODE, F16>(ru[i], nu, s.book, bu[i]);
+        }
+    }
+
+    for (int m0 = pbeg; m0 < pend; m0 += 16) {
+        const int mc = min(16, pend - m0);
+        const bool live = col < mc;
+        const int xr = live ? s.g.plist[m0 + col] / a.row_div : 0;
+        v4f fg = {0, 0, 0, 0}, fu = {0, 0, 0, 0};
+        v4i ig = {0, 0, 0, 0}, iu = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < KBW; ++i) {
+            const int kb = wave + i * kQWaves;
+            if (kb >= KB) continue;
+            if constexpr (MODE == 0) {
+                const uint16_t* xp = s.x.h + xr * H + kb * 128 + grp * 32;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const v4i av = live ? *(const v4i*)(xp + 8 * t) : v4i{0, 0, 0, 0};
+                    if constexpr (F16) {
+                        fg = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, av),
+                                                                     __builtin_bit_cast(v8h, bg[i].r[t]), fg, 0, 0, 0);
+                        fu = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, av),
+                                                                     __builtin_bit_cast(v8h, bu[i].r[t]), fu, 0, 0, 0);
+                    } else {
+                        fg = mfma_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bg[i].r[t]), fg);
+                        fu = mfma_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bu[i].r[t]), fu);
+                    }
+                }
+            } else {
+                const int8_t* xp = s.x.q + xr * H + kb * 128 + grp * 32;
+                const v4i a0 = live ? *(const v4i*)xp : v4i{0, 0, 0, 0};
+                const v4i a1 = live ? *(const v4i*)(xp + 16) : v4i{0, 0, 0, 0};
+                ig = mfma_i8(a0, bg[i].r[0], ig);
+                ig = mfma_i8(a1, bg[i].r[1], ig);
+                iu = mfma_i8(a0, bu[i].r[0], iu);
+                iu = mfma_i8(a1, bu[i].r[1], iu);
+            }
+        }
+        // cross-wave reduction (exact in int32 for modes 1-3)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s.red[wave][lane][r] = MODE == 0 ? fg[r] : __int_as_float(ig[r]);
+            s.red[wave][lane][4 + r] = MODE == 0 ? fu[r] : __int_as_float(iu[r]);
+        }
+        lds_barrier();
+        if (wave == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = grp * 4 + r;
+                if (row >= mc) continue;
+                const int p = s.g.plist[m0 + row];
+                float yg, yu;
+                if constexpr (MODE == 0) {
+                    yg = s.red[0][lane][r];
+                    yu = s.red[0][lane][4 + r];
+                    for (int q = 1; q < kQWaves; ++q) {
+                        yg += s.red[q][lane][r];
+                        yu += s.red[q][lane][4 + r];
+                    }
+                } else {
+                    int sg = 0, su = 0;
+                    for (int q = 0; q < kQWaves; ++q) {
+                        sg += __float_as_int(s.red[q][lane][r]);
+                        su += __float_as_int(s.red[q][lane][4 + r]);
+                    }
+                    const float sa = s.sa[p / a.row_div];
+                    yg = (float)sg * sa * sbg;
+                    yu = (float)su * sa * sbu;
+                }
+                yg = bf16_round(yg);
+                yu = bf16_round(yu);
+                const float act = bf16_round(bf16_round(yg / (1.0f + expf(-yg))) * yu);
+                a.act[(int64_t)p * I + n0 + col] = __builtin_bit_cast(uint16_t, (__bf16)act);
+            }
+        }
+        lds_barrier();
+    }
+}
+
+bool quant_gateup_decode_fits(int mode, int pairs, int rows, int H, int I, const void* x, int x_dtype,
+                              int64_t x_row_stride) {
+    if (pairs < 1 || pairs > kSmallPairs || rows < 1 || rows > kQgMaxRows || H % 128 != 0 || H > kMaxQuantK ||
+        I % 16 != 0)
+        return false;
+    const int esize = x_dtype == kF32 ? 4 : 2;  // one 16-byte (fp32) or 8-byte load per 4 values
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || (x_row_stride * esize) % 16 != 0) return false;
+    if (mode == 0) return rows * H <= kQgMaxRows * kMaxQuantK / 2;  // 16-bit rows in LDS
+    return H % 256 == 0 && rows * (H / 256) <= kQWaves * kQgUnits;
+}
+
+void launch_quant_gateup_decode(const QuantGateUpArgs& a, hipStream_t stream) {
+    const dim3 grid((unsigned)std::min(a.pairs, a.experts), (unsigned)(a.w13.N / 2 / 16)), block(kQThreads);
+    const int kbw = (a.w13.K / 128 + kQWaves - 1) / kQWaves;
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
+    auto by_kbw = [&](auto m, auto xt) {
+        constexpr int M = decltype(m)::value, X = decltype(xt)::value;
+        if (kbw <= 1) go(quant_gateup_decode_kernel<M, X, 1>);
+        else if (kbw <= 2) go(quant_gateup_decode_kernel<M, X, 2>);
+        else go(quant_gateup_decode_kernel<M, X, 4>);
+    };
+    auto by_x = [&](auto m) {
+        constexpr int M = decltype(m)::value;
+        if (a.x_dtype == kF16) by_kbw(m, std::integral_constant<int, kF16>{});
+        else if constexpr (M == 0) by_kbw(m, std::integral_constant<int, kBF16>{});  // fp32 rows never reach mode 0
+        else if (a.x_dtype == kBF16) by_kbw(m, std::integral_constant<int, kBF16>{});
+        else by_kbw(m, std::integral_constant<int, kF32>{});
+    };
+    switch (a.w13.mode) {
+        case 0: by_x(std::integral_constant<int, 0>{}); break;
+        case 1: by_x(std::integral_constant<int, 1>{}); break;
+        case 2: by_x(std::integral_constant<int, 2>{}); break;
+        default: by_x(std::integral_constant<int, 3>{}); break;
+    }
+}
+
+// -------------------------------------------- small-call down + combine
+
+// A workgroup owns 8 output rows; each wave takes two active experts at a
+// time (MFMA columns 0-7 and 8-15), its A operand the hidden rows of their
+// pairs, staged in LDS at the start: modes 1-3 rotated + INT8-quantized
+// there (rotate_quant_kernel's arithmetic, the rotated values kept in
+// registers between the row-maximum and quantization passes), mode 0 the
+// bf16 rows as they are.  The first batch's weight loads are issued before
+// the rotation.  Each pair's output row is bf16(y) * route weight in LDS
+// (y = int32 dot * row scale * channel scale, or the fp32 dot), then the
+// workgroup sums each token's valid pairs in router slot order -- what
+// projection(weighted) + the combine of quantized_kernels.py:217-260 give.
+constexpr int kQdWaves = 4, kQdThreads = kQdWaves * kWave;
+constexpr int kQdGroups = 3;  // rotation groups (4 blocks, 16 lanes each) per wave: pairs * I / 256 <= 48
+
+struct QDownLds {
+    SmallGroups g;
+    union {
+        struct {
+            alignas(16) int8_t q[kQdMaxRotRows * kQdMaxI];  // modes 1-3: rotated INT8 hidden rows
+            float tb[kQdWaves][kRotWaveDwords];             // and the rotation transposes
+        };
+        alignas(16) uint16_t h[kQdMaxBf16];  // mode 0: bf16 hidden rows
+    } act;
+    float sa[kQdMaxRotRows];
+    uint32_t rmax[kQdMaxRotRows];
+    float wt[kSmallPairs];
+    int valid[kSmallPairs];
+    float part[kSmallPairs][8];
+    float book[kQdWaves][2][16];  // mode 3 codebooks of the wave's two experts
+};
+
+template <int MODE, int KB2>
+__global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDownArgs a) {
+    __shared__ QDownLds s;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int col = lane % 16, grp = lane / 16;
+    const QuantProjArgs& w = a.w2;
+    const int I = w.K, H = w.N, KB = I / 128, P = a.pairs;
+    const int n0 = blockIdx.x * 8;
+
+    const bool pl = wave == 0 && lane < P;  // lane p of wave 0 holds pair p
+    // loads are issued unconditionally (clamped indexes): a load merged with
+    // a constant on another path is waited for at the merge
+    const uint2 idb = load_id_bits(a.ids, min(lane, P - 1), a.ids_dtype);
+    const uint32_t wbits = load_bits(a.weights, min(lane, P - 1), a.w_dtype);  // used at the end
+    // hidden rows: every load issued now (clamped to the last unit)
+    const int nb = I / 256, units = P * nb;
+    Raw16<kBF16> hin[kQdGroups];  // group q of wave w: blocks 4 (w + 4 q) .. +3, 16 lanes each
+    if constexpr (MODE != 0) {
+#pragma unroll
+        for (int q = 0; q < kQdGroups; ++q) {
+            const int u = min(4 * (wave + kQdWaves * q) + lane / 16, units - 1);
+            hin[q] = load_raw16<kBF16>(a.act, (int64_t)(u / nb) * I + (u % nb) * 256 + 16 * (lane % 16));
+        }
+        for (int r = threadIdx.x; r < P; r += kQdThreads) s.rmax[r] = 0u;
+    } else {
+        constexpr int kChunks = kQdMaxBf16 / 8 / kQdThreads;  // 16-byte chunks per thread
+        const int chunks = P * I / 8;
+        v4i c16[kChunks];
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j)
+            c16[j] = *(const v4i*)(a.act + (int64_t)min((int)threadIdx.x + j * kQdThreads, chunks - 1) * 8);
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const int i = threadIdx.x + j * kQdThreads;
+            if (i < chunks) *(v4i*)(s.act.h + i * 8) = c16[j];
+        }
+    }
+    for (int i = threadIdx.x; i < P * 8; i += kQdThreads) s.part[i / 8][i % 8] = 0.0f;
+    const int pe = pl ? id_expert(idb, a.ids_dtype, a.experts) : -1;
+    if (wave == 0) {
+        if (pl && pe < 0 && blockIdx.x == 0) raise_status(a.status, kBadExpertId);
+        group_pairs(pe, P, lane, s.g);
+    }
+    lds_barrier();
+
+    const int num_active = s.g.num_active;
+    const int batches = (num_active + 1) / 2;
+    // batch bi = active experts 2 bi (columns 0-7) and 2 bi + 1 (8-15)
+    int e0 = 0, e1 = -1, e = 0, ec = 0;
+    WRaw raw[KB2];
+    float sch = 1.0f, bk = 0.0f;
+    const int n = n0 + (col & 7);
+    auto fetch_batch = [&](int bi) {  // loads unconditional (see above)
+        e0 = num_active > 0 ? s.g.active[2 * bi] : 0;
+        e1 = 2 * bi + 1 < num_active ? s.g.active[2 * bi + 1] : -1;
+        e = col < 8 ? e0 : e1;
+        ec = e >= 0 ? e : e0;
+#pragma unroll
+        for (int kb = 0; kb < KB2; ++kb) raw[kb] = fetch_wrow<MODE>(w, ec, n, min(kb, KB - 1), grp);
+        if constexpr (MODE != 0) sch = channel_scale<MODE>(w, ec, n);
+        if constexpr (MODE == 3) {  // lanes 0-15: codebook of e0, 16-31: of e1
+            const int eb = (lane & 16) && e1 >= 0 ? e1 : e0;
+            bk = *(const float*)(w.s + (int64_t)eb * w.s_se + (int64_t)(lane % 16) * w.s_sn + I / 16 + 4);
+        }
+    };
+    fetch_batch(min(wave, max(batches - 1, 0)));  // waves without a batch: loaded, never used
+
+    if constexpr (MODE != 0) {
+        // rotation (H4^{x4} / 16 per 256-block, rounded to bf16) and row INT8
+        pin_after_loads(hin);  // keeps the rotation behind the weight loads
+        float v[kQdGroups][16];
+#pragma unroll
+        for (int q = 0; q < kQdGroups; ++q) {
+            const int u = 4 * (wave + kQdWaves * q) + lane / 16;
+            if (4 * (wave + kQdWaves * q) >= units) break;  // wave-uniform
+            convert16(hin[q], v[q]);
+            rotate16(v[q], s.act.tb[wave], lane);  // lanes past the last block: duplicates, never stored
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                v[q][i] = bf16_round(v[q][i] * 0.0625f);
+                amax = fmaxf(amax, fabsf(v[q][i]));
+            }
+            amax = row_max(amax);
+            if (u < units && lane % 16 == 0) atomicMax(&s.rmax[u / nb], __float_as_uint(amax));
+        }
+        lds_barrier();
+#pragma unroll
+        for (int q = 0; q < kQdGroups; ++q) {  // INT8 bytes at positions 16 i + m of each block
+            const int u = 4 * (wave + kQdWaves * q) + lane / 16;
+            if (4 * (wave + kQdWaves * q) >= units) break;
+            if (u >= units) continue;
+            const int row = u / nb, c = u % nb, m = lane % 16;
+            const float sc = fmaxf(__uint_as_float(s.rmax[row]), 1e-12f) / 127.0f;
+            int8_t* dst = s.act.q + row * I + c * 256 + m;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dst[16 * i] = (int8_t)quant_byte(v[q][i], sc);
+            if (c == 0 && m == 0) s.sa[row] = sc;
+        }
+        lds_barrier();
+    }
+
+    for (int bi = wave; bi < batches; bi += kQdWaves) {
+        if (bi != wave) fetch_batch(bi);
+        if constexpr (MODE == 3) {
+            if (lane < 32) s.book[wave][lane / 16][lane % 16] = bk;  // read back by this wave only
+        }
+        WRow b[KB2];
+#pragma unroll
+        for (int kb = 0; kb < KB2; ++kb) decode_wrow<MODE, false>(raw[kb], n, s.book[wave][col < 8 ? 0 : 1], b[kb]);
+        const int s0 = s.g.start[2 * bi], M0 = s.g.start[2 * bi + 1] - s0;
+        const int s1 = e1 >= 0 ? s.g.start[2 * bi + 1] : 0, M1 = e1 >= 0 ? s.g.start[2 * bi + 2] - s1 : 0;
+        auto a_row = [&](int pass, int row) -> int {  // pair of A row `row` in a pass (-1: none)
+            const int m = pass * 8 + (row & 7);
+            if (row < 8) return m < M0 ? s.g.plist[s0 + m] : -1;
+            return m < M1 ? s.g.plist[s1 + m] : -1;
+        };
+        const int passes = (max(M0, M1) + 7) / 8;
+        for (int pass = 0; pass < passes; ++pass) {
+            const int ar = a_row(pass, col);
+            const int arc = ar >= 0 ? ar : 0;
+            v4f fa = {0, 0, 0, 0};
+            v4i ia = {0, 0, 0, 0};
+#pragma unroll
+            for (int kb = 0; kb < KB2; ++kb) {
+                if (kb >= KB) continue;
+                if constexpr (MODE == 0) {
+                    const uint16_t* xr = s.act.h + arc * I + kb * 128 + grp * 32;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const v4i av = ar >= 0 ? *(const v4i*)(xr + 8 * t) : v4i{0, 0, 0, 0};
+                        fa = mfma_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, b[kb].r[t]), fa);
+                    }
+                } else {
+                    const int8_t* xr = s.act.q + arc * I + kb * 128 + grp * 32;
+                    const v4i a0 = ar >= 0 ? *(const v4i*)xr : v4i{0, 0, 0, 0};
+                    const v4i a1 = ar >= 0 ? *(const v4i*)(xr + 16) : v4i{0, 0, 0, 0};
+                    ia = mfma_i8(a0, b[kb].r[0], ia);
+                    ia = mfma_i8(a1, b[kb].r[1], ia);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = grp * 4 + r;
+                // keep the diagonal blocks: A row half == B column half
+                const int pr = ((row < 8) == (col < 8)) ? a_row(pass, row) : -1;
+                if (pr < 0 || e < 0) continue;
+                const float y = MODE == 0 ? fa[r] : (float)ia[r] * s.sa[pr] * sch;
+                s.part[pr][col & 7] = bf16_round(y);
+            }
+        }
+    }
+    if (pl) {
+        s.wt[lane] = bits_to_f32(wbits, a.w_dtype);
+        s.valid[lane] = pe >= 0;
+    }
+    lds_barrier();
+    // pair partial = bf16(y) * route weight (fp32)
+    if (a.out_pairs) {  // ordered fp32 partials, one row per pair (invalid pairs 0)
+        for (int i = threadIdx.x; i < P * 8; i += kQdThreads) {
+            const int p = i / 8, c = i % 8;
+            a.out_pairs[(int64_t)p * H + n0 + c] = s.valid[p] ? s.part[p][c] * s.wt[p] : 0.0f;
+        }
+    } else {  // layer output: fp32 sum of each token's valid partials in router slot order
+        const int tokens = P / a.top_k;
+        for (int i = threadIdx.x; i < tokens * 8; i += kQdThreads) {
+            const int t = i / 8, c = i % 8;
+            float acc = 0.0f;
+            for (int j = 0; j < a.top_k; ++j) {
+                const int p = t * a.top_k + j;
+                if (!s.valid[p]) continue;
+                const float v = s.part[p][c] * s.wt[p];
+                acc = j == 0 ? v : acc + v;
+            }
+            store_from_f32(a.out, (int64_t)t * a.out_row_stride + n0 + c, a.out_dtype, acc);
+        }
+    }
+}
+
+bool quant_down_decode_fits(int mode, int pairs, int H, int I) {
+    if (pairs < 1 || pairs > kSmallPairs || I > kQdMaxI || I % 128 != 0 || H % 8 != 0) return false;
+    if (mode == 0) return pairs * I <= kQdMaxBf16;
+    return I % 256 == 0 && pairs <= kQdMaxRotRows && pairs * (I / 256) <= kQdWaves * kQdGroups * 4;
+}
+
+void launch_quant_down_decode(const QuantDownArgs& a, hipStream_t stream) {
+    const dim3 grid((unsigned)(a.w2.N / 8)), block(kQdThreads);
+    const int kb = a.w2.K / 128;
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
+    auto by_kb = [&](auto m) {
+        constexpr int M = decltype(m)::value;
+        if (kb <= 2) go(quant_down_decode_kernel<M, 2>);
+        else if (kb <= 4) go(quant_down_decode_kernel<M, 4>);
+        else if (kb <= 6) go(quant_down_decode_kernel<M, 6>);
+        else go(quant_down_decode_kernel<M, 8>);
+    };
+    switch (a.w2.mode) {
+        case 0: by_kb(std::integral_constant<int, 0>{}); break;
+        case 1: by_kb(std::integral_constant<int, 1>{}); break;
+        case 2: by_kb(std::integral_constant<int, 2>{}); break;
+        default: by_kb(std::integral_constant<int, 3>{}); break;
     }
 }
 

@@ -78,8 +78,12 @@ DMOE_API int dmoe_abi_version(void);
  * measurement).  Returns the previous setting.  The fused launch occupies
  * every CU and waits on its own workgroups: work on other streams of the
  * same device delays it, and a wait that exceeds 200 ms gives up with
- * DMOE_STATUS_SYNC_TIMEOUT.  No counterpart in the reference (its decode is
- * per-route-slot Triton launches, fp8_decode.py:114-147). */
+ * DMOE_STATUS_SYNC_TIMEOUT.  The same switch selects, for packed banks, the
+ * single launch that quantizes the hidden rows, projects down and combines
+ * small calls (at most 64 pairs; 16 for the INT8 modes); 0 keeps the
+ * separate rotation, projection and combine launches.  No counterpart in the
+ * reference (its decode is per-route-slot Triton launches,
+ * fp8_decode.py:114-147). */
 DMOE_API int dmoe_set_fused_decode(int enabled);
 
 /* Last error message of the calling thread.  Replaces drama_native_error

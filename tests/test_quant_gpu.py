@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from conftest import print_case
-from drama_moe import quantized
+from drama_moe import _lib, quantized
 from drama_moe.formats import QuantizedStore, random_quantized_bank
 from oracle import oracle as orc
 
@@ -123,6 +123,59 @@ def test_layer_decode_matches_oracle(cuda, mode, tokens):
     assert out.dtype == torch.bfloat16 and out.shape == x.shape
     expected = oracle_layer(store, x.float().numpy(), ids, weights.float().numpy())
     assert rel_inf(out.float().cpu().numpy(), expected) < TOL
+
+
+@pytest.fixture
+def down_launch():
+    """Selects the single-launch down + combine of small packed calls (True)
+    or the separate rotation, projection and combine launches (False)."""
+    lib = _lib.library()
+    yield lambda single: lib.dmoe_set_fused_decode(1 if single else 0)
+    lib.dmoe_set_fused_decode(1)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("tokens,top_k", [(1, 4), (1, 8), (2, 8), (3, 5), (8, 8)])
+def test_small_call_down_launch_matches_separate_launches(cuda, down_launch, mode, tokens, top_k):
+    """The small-call down launch (hidden rotation + INT8 in LDS, down,
+    slot-order combine) against the separate launches: bit-identical for
+    modes 1-3 (exact int32 dots, the same epilogue and combine order), within
+    the bar for mode 0 (fp32 dot order differs); both paths against the
+    oracle.  Invalid ids (-1, E) are skipped by the combine and give zero
+    pair rows.  Modes 1-3 at 64 pairs and every mode above 64 pairs take the
+    separate launches on both sides."""
+    print_case("quant down launch", mode, tokens, top_k)
+    g = torch.Generator().manual_seed(900 + 16 * mode + tokens)
+    store = random_quantized_bank(mode, 32, 512, 256, generator=g)
+    dev = to_device(store, cuda)
+    x = torch.randn(tokens, 512, generator=g).bfloat16()
+    ids, w = orc.route_topk(torch.randn(tokens, 32, generator=g).numpy(), top_k)
+    ids = ids.copy()
+    ids[0, 1] = -1
+    ids[-1, -1] = 32
+    weights = torch.from_numpy(w).bfloat16()
+    backend = quantized.QuantizedExpertBackend(mode)
+    args = (x.to(cuda), torch.from_numpy(ids).to(cuda), weights.to(cuda), dev)
+    results = {}
+    for single in (True, False):
+        down_launch(single)
+        results[single] = (backend.forward(*args), backend.forward_pairs(
+            x.to(cuda).repeat_interleave(top_k, 0), torch.from_numpy(ids).reshape(-1, 1).to(cuda),
+            weights.reshape(-1, 1).to(cuda), dev))
+        torch.cuda.synchronize()
+    (out1, pairs1), (out0, pairs0) = results[True], results[False]
+    if mode:
+        assert torch.equal(out1, out0) and torch.equal(pairs1, pairs0)
+    else:
+        assert rel_inf(out1.float().cpu().numpy(), out0.float().cpu().numpy()) < TOL
+        assert rel_inf(pairs1.cpu().numpy(), pairs0.cpu().numpy()) < TOL
+    flat = ids.reshape(-1)
+    bad = np.flatnonzero((flat < 0) | (flat >= 32))
+    assert torch.count_nonzero(pairs1[torch.from_numpy(bad).to(cuda)]) == 0
+    valid = np.where((ids >= 0) & (ids < 32), ids, 0)
+    wv = np.where((ids >= 0) & (ids < 32), weights.float().numpy(), 0.0).astype(np.float32)
+    expected = oracle_layer(store, x.float().numpy(), valid, wv)
+    assert rel_inf(out1.float().cpu().numpy(), expected) < TOL
 
 
 def test_w4a16_asymmetric_zero_points(cuda):
