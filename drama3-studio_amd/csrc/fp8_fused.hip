@@ -190,7 +190,22 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     // neighbouring threads sharing the count; then one wave per token
     // renormalizes its slots in slot order.  Larger calls: one wave per token
     // (wave_route_token), no barrier.  Both give the router kernels' bits.
-    if (src.logits && rtokens * E <= kRankRouteElems) {
+    if (src.logits && E <= 2 * kWave) {  // one wave per token, two logits per lane, no barrier
+        for (int t = wave; t < rtokens; t += kFzWaves) {
+            if (t != wave) wave_route_load(src, t, E, lg);
+            int id;
+            float w;
+            wave_route_small(lg, E, src.top_k, src.renormalize, id, w);
+            if (lane < src.top_k) {
+                s.sid[t * src.top_k + lane] = (int16_t)id;
+                s.wt[t * src.top_k + lane] = round_through(w, src.w_dtype);
+                if (B == 0) {
+                    src.ids_out[(int64_t)t * src.top_k + lane] = id;
+                    store_from_f32(src.weights_out, (int64_t)t * src.top_k + lane, src.w_dtype, w);
+                }
+            }
+        }
+    } else if (src.logits && rtokens * E <= kRankRouteElems) {
         for (int t = wave; t < rtokens; t += kFzWaves) {
             if (t != wave) wave_route_load(src, t, E, lg);
             float m = -INFINITY;
@@ -308,54 +323,46 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             }
         }
     }
-    lds_barrier();
-    if (a.x_group != 128) {  // per-row scale: the maximum of the row's group maxima
-#pragma unroll
-        for (int q = 0; q < kQuantPerGroup; ++q) {
-            const int u = qgroup + q * (kFzThreads / 16);
-            if (u < xunits) {
-                const int r = u / gpr;
-                float amax = 0.0f;
-                for (int g = 0; g < gpr; ++g) amax = fmaxf(amax, s.gmax[r * gpr + g]);
-                const float scale = fp8_group_scale(amax);
-                const F8 v = unpack8(xr[q][0], a.x_dtype == kF32 ? xr[q][1] : xr[q][0], a.x_dtype);
-                *(uint64_t*)&s.xq[r * H + (u % gpr) * 128 + col * 8] = encode8(v, scale);
-                if (col == 0) s.xs[u] = scale;
-            }
-        }
-    }
+    lds_barrier();  // route slots and the activation group maxima
 
     // ------------------------------------------------------- grouping
-    if (wave == 0) {  // one pair per lane (P <= 64)
-        const int e = lane < P ? s.sid[lane] : -1;
-        int rank = 0, before = 0;
-        for (int q = 0; q < P; ++q) {
-            const int eq = __builtin_amdgcn_readlane(e, q);
-            rank += (eq == e) & (q < lane);
-            before += (eq >= 0) & (eq < e);
+    // Every wave ranks the pairs in its registers (lane p: pair p), so it can
+    // issue its weight loads at once; wave 0 also writes the lists the
+    // compute phases read (after the barrier below).
+    const int pe = lane < P ? s.sid[lane] : -1;
+    int grank = 0, gbefore = 0;
+    for (int q = 0; q < P; ++q) {
+        const int eq = __builtin_amdgcn_readlane(pe, q);
+        grank += (eq == pe) & (q < lane);
+        gbefore += (eq >= 0) & (eq < pe);
+    }
+    const int gfirst = pe >= 0 && grank == 0;
+    int gdless = 0;  // distinct experts below pe
+    for (int q = 0; q < P; ++q) {
+        const int eq = __builtin_amdgcn_readlane(pe, q), fq = __builtin_amdgcn_readlane(gfirst, q);
+        gdless += fq & (eq < pe);
+    }
+    const int num_active = __popcll(__ballot(gfirst));
+    // expert of active index ai (wave-uniform; expert 0 past the last)
+    auto active_of = [&](int ai) -> int {
+        const uint64_t m = __ballot(gfirst && gdless == ai);
+        return m ? __builtin_amdgcn_readlane(pe, (int)__builtin_ctzll(m)) : 0;
+    };
+    if (wave == 0) {
+        if (pe >= 0) {
+            s.plist[gbefore + grank] = lane;
+            s.prow[gbefore + grank] = lane / a.row_div;
         }
-        const int first = e >= 0 && rank == 0;
-        int dless = 0;  // distinct experts below e
-        for (int q = 0; q < P; ++q) {
-            const int eq = __builtin_amdgcn_readlane(e, q), fq = __builtin_amdgcn_readlane(first, q);
-            dless += fq & (eq < e);
+        if (gfirst) {
+            s.active[gdless] = pe;
+            s.start[gdless] = gbefore;
         }
-        if (e >= 0) {
-            s.plist[before + rank] = lane;
-            s.prow[before + rank] = lane / a.row_div;
-        }
-        if (first) {
-            s.active[dless] = e;
-            s.start[dless] = before;
-        }
-        const int na = __popcll(__ballot(first)), valid = __popcll(__ballot(e >= 0));
+        const int valid = __popcll(__ballot(pe >= 0));
         if (lane == 0) {
-            s.num_active = na;
-            s.start[na] = valid;
+            s.num_active = num_active;
+            s.start[num_active] = valid;
         }
     }
-    lds_barrier();
-    const int num_active = s.num_active;
 
     // ------------------------------------------------- weight loads
     // Every load is issued unconditionally (clamped to valid rows: units past
@@ -374,7 +381,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         const int u = B + j * G;
         const int ai = real ? u / ucols : 0;
         const int c0 = real ? (u % ucols) * kUnitCols : 0;
-        const int e = real ? s.active[ai] : 0;
+        const int e = active_of(real ? ai : num_active);
         const int n = col < 8 ? c0 + col : I + c0 + col - 8;
         const uint8_t* wrow = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)n * a.w13.w_sn + grp * 32;
 #pragma unroll
@@ -396,8 +403,8 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     v8i db[KBJ];
     float dsw[KBJ];
     auto load_job = [&](int rt, int j) {
-        const int ai = 2 * j + (col >= 8 ? 1 : 0);
-        const int e = ai < num_active ? s.active[ai] : 0;
+        const int e0 = active_of(2 * j), e1 = active_of(2 * j + 1);  // expert 0 past the last
+        const int e = col >= 8 ? e1 : e0;
         const int n = min(rt, tiles - 1) * kTileRows + (col & 7);
         const uint8_t* wrow = a.w2.w + (int64_t)e * a.w2.w_se + (int64_t)n * a.w2.w_sn + grp * 32;
 #pragma unroll
@@ -407,7 +414,23 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             dsw[kb] = proj_scale(a.w2, e, n, kbc);
         }
     };
-    load_job(B, wave);
+    if (a.x_group != 128) {  // per-row scale: the maximum of the row's group maxima
+#pragma unroll
+        for (int q = 0; q < kQuantPerGroup; ++q) {
+            const int u = qgroup + q * (kFzThreads / 16);
+            if (u < xunits) {
+                const int r = u / gpr;
+                float amax = 0.0f;
+                for (int g = 0; g < gpr; ++g) amax = fmaxf(amax, s.gmax[r * gpr + g]);
+                const float scale = fp8_group_scale(amax);
+                const F8 v = unpack8(xr[q][0], a.x_dtype == kF32 ? xr[q][1] : xr[q][0], a.x_dtype);
+                *(uint64_t*)&s.xq[r * H + (u % gpr) * 128 + col * 8] = encode8(v, scale);
+                if (col == 0) s.xs[u] = scale;
+            }
+        }
+    }
+
+    lds_barrier();  // grouping lists and activation rows
     if (tid == kTicketThread) {
         const int n_slot = (G - eslot + kEpochSlots - 1) / kEpochSlots;  // workgroups sharing the slot
         s.epoch = (uint32_t)(ticket / (uint64_t)n_slot) + 1u;
@@ -503,6 +526,11 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         for (int d = 0; d < kUnitDepth; ++d) load_unit(j0 + d, d);
         unit_batch(j0);
     }
+    // The first down job's rows go out only now, and only from waves that
+    // have a job: the gate/up rows get the memory system to themselves, and
+    // these stream during the hidden hand-off, which they are not needed
+    // before.
+    if (B < tiles && my_jobs > 0) load_job(B, wave);
     if (my_units == 0) lds_barrier();  // no gate/up barrier ran: order the epoch's LDS write
     epoch = s.epoch;
     if (B >= tiles) {  // no down rows for this workgroup
@@ -653,7 +681,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     for (int rt = B; rt < tiles; rt += G) {
         for (int i = tid; i < P * kTileRows; i += kFzThreads) s.v.part[i / kTileRows][i % kTileRows] = 0.0f;
         lds_barrier();  // partials zeroed (invalid pairs stay 0); FP8 hidden complete
-        if (rt != B) load_job(rt, wave);
+        if (rt != B && my_jobs > 0) load_job(rt, wave);
         for (int jj = 0; jj < my_jobs; ++jj) {
             if (jj > 0) load_job(rt, wave + jj * kFzWaves);
             compute_job(wave + jj * kFzWaves);

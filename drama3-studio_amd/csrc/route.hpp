@@ -119,6 +119,54 @@ __device__ __forceinline__ void wave_route_token(const float (&l)[kRouteLaneSlot
     w_out = renormalize ? p / wtot : p;
 }
 
+// wave_route_token for at most 2 * 64 experts (l[0] = expert lane, l[1] =
+// lane + 64), with the same arithmetic and so the same bits.  A round's
+// winner is the lowest expert among the lanes holding the round's maximum key:
+// the lowest such lane in l[0] (a lane prefers l[0] on equal keys), else the
+// lowest in l[1] -- two ballots and a find-first-set instead of a second
+// wave-wide reduction.
+__device__ __forceinline__ void wave_route_small(const float (&l)[kRouteLaneSlots], int experts, int top_k,
+                                                 int renormalize, int& id_out, float& w_out) {
+    const int lane = threadIdx.x % kWave;
+    const bool ok0 = lane < experts, ok1 = lane + kWave < experts;
+    uint32_t key0 = ordered_bits(l[0]), key1 = ordered_bits(l[1]);
+    bool av0 = ok0, av1 = ok1;
+    float m = -INFINITY;
+    if (ok0) m = fmaxf(m, l[0]);
+    if (ok1) m = fmaxf(m, l[1]);
+    m = wave_max_dpp(m);
+    const float ex0 = expf(l[0] - m), ex1 = expf(l[1] - m);
+    float sum = 0.0f;
+    if (ok0) sum += ex0;
+    if (ok1) sum += ex1;
+    sum = wave_sum_dpp(sum);
+    int my_id = 0;
+    float my_x = 0.0f;
+    for (int slot = 0; slot < top_k; ++slot) {
+        const bool b1 = av1 && (!av0 || key1 > key0);  // this lane's best: l[1] only when strictly larger
+        const bool any = av0 || av1;
+        const uint32_t bk = b1 ? key1 : key0;
+        const uint32_t mk = wave_max_u32(any ? bk : 0u);
+        const uint64_t w0 = __ballot(any && !b1 && bk == mk), w1 = __ballot(any && b1 && bk == mk);
+        const int win = w0 ? __builtin_ctzll(w0) : kWave + __builtin_ctzll(w1);
+        const int wl = win % kWave;
+        const float xw = readlane_f32(win < kWave ? ex0 : ex1, wl);
+        if (lane == wl) {
+            if (win < kWave) av0 = false;
+            else av1 = false;
+        }
+        if (lane == slot) {
+            my_id = win;
+            my_x = xw;
+        }
+    }
+    const float p = lane < top_k ? my_x / sum : 0.0f;
+    float wtot = 0.0f;
+    for (int j = 0; j < top_k; ++j) wtot += readlane_f32(p, j);
+    id_out = my_id;
+    w_out = renormalize ? p / wtot : p;
+}
+
 template <int THREADS>
 __device__ void block_route(RouteScratch& rs, const RouteSource& src, int t0, int tcount, int experts,
                             int16_t* ids_lds, bool publish, float* wts_lds = nullptr) {
