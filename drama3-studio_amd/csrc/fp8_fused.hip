@@ -462,7 +462,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 s.ucoord[d][2] = um[d];
             }
         }
-        for (int pass = 0; pass < passes; ++pass) {
+        auto run_pass = [&](int pass) {
 #pragma unroll
             for (int d = 0; d < kUnitDepth; ++d) {
                 // branch-free operand reads (clamped rows, values selected after the read)
@@ -518,7 +518,12 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 }
             }
             lds_barrier();  // partials and coordinates read before they are overwritten
-        }
+        };
+        // The first pass as straight-line code: each unit's MFMAs wait for
+        // that unit's rows only (a loop makes the compiler wait for every
+        // outstanding load at its entry).
+        if (passes > 0) run_pass(0);
+        for (int pass = 1; pass < passes; ++pass) run_pass(pass);
     };
     unit_batch(0);
     for (int j0 = kUnitDepth; j0 < my_units; j0 += kUnitDepth) {

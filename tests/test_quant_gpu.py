@@ -126,9 +126,9 @@ def test_layer_decode_matches_oracle(cuda, mode, tokens):
 
 
 @pytest.fixture
-def down_launch():
-    """Selects the single-launch down + combine of small packed calls (True)
-    or the separate rotation, projection and combine launches (False)."""
+def small_launches():
+    """Selects the two small-call launches of packed calls (True) or the
+    separate permutation, rotation, projection and combine launches (False)."""
     lib = _lib.library()
     yield lambda single: lib.dmoe_set_fused_decode(1 if single else 0)
     lib.dmoe_set_fused_decode(1)
@@ -136,14 +136,17 @@ def down_launch():
 
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("tokens,top_k", [(1, 4), (1, 8), (2, 8), (3, 5), (8, 8)])
-def test_small_call_down_launch_matches_separate_launches(cuda, down_launch, mode, tokens, top_k):
-    """The small-call down launch (hidden rotation + INT8 in LDS, down,
-    slot-order combine) against the separate launches: bit-identical for
-    modes 1-3 (exact int32 dots, the same epilogue and combine order), within
-    the bar for mode 0 (fp32 dot order differs); both paths against the
-    oracle.  Invalid ids (-1, E) are skipped by the combine and give zero
-    pair rows.  Modes 1-3 at 64 pairs and every mode above 64 pairs take the
-    separate launches on both sides."""
+def test_small_call_launches_match_separate_launches(cuda, small_launches, mode, tokens, top_k):
+    """The small-call launches (pairs grouped inside each workgroup,
+    activation and hidden rotation + INT8 in LDS, slot-order combine in the
+    down launch) against the separate launches: bit-identical for modes 1-3
+    (exact int32 dots, the same epilogues and combine order), within the bar
+    for mode 0 (fp32 dot order differs); both paths against the oracle.
+    Invalid ids (-1, E) raise the status bit, are skipped by the combine and
+    give zero pair rows.  The gate/up launch takes at most 4 activation rows
+    (forward: tokens; forward_pairs: pairs), the down launch at most 16 pairs
+    in modes 1-3 (64 in mode 0 at this size); larger calls take the separate
+    launches on both sides."""
     print_case("quant down launch", mode, tokens, top_k)
     g = torch.Generator().manual_seed(900 + 16 * mode + tokens)
     store = random_quantized_bank(mode, 32, 512, 256, generator=g)
@@ -158,11 +161,12 @@ def test_small_call_down_launch_matches_separate_launches(cuda, down_launch, mod
     args = (x.to(cuda), torch.from_numpy(ids).to(cuda), weights.to(cuda), dev)
     results = {}
     for single in (True, False):
-        down_launch(single)
+        small_launches(single)
+        backend.status(cuda)
         results[single] = (backend.forward(*args), backend.forward_pairs(
             x.to(cuda).repeat_interleave(top_k, 0), torch.from_numpy(ids).reshape(-1, 1).to(cuda),
             weights.reshape(-1, 1).to(cuda), dev))
-        torch.cuda.synchronize()
+        assert backend.status(cuda) & 1, single
     (out1, pairs1), (out0, pairs0) = results[True], results[False]
     if mode:
         assert torch.equal(out1, out0) and torch.equal(pairs1, pairs0)
