@@ -329,20 +329,29 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     // Every wave ranks the pairs in its registers (lane p: pair p), so it can
     // issue its weight loads at once; wave 0 also writes the lists the
     // compute phases read (after the barrier below).
+    // The comparisons run over the expert bits, most significant first: per
+    // bit one ballot of the lanes holding it; a lane keeps the mask of lanes
+    // equal to it so far and collects those that fall below it at this bit.
     const int pe = lane < P ? s.sid[lane] : -1;
-    int grank = 0, gbefore = 0;
-    for (int q = 0; q < P; ++q) {
-        const int eq = __builtin_amdgcn_readlane(pe, q);
-        grank += (eq == pe) & (q < lane);
-        gbefore += (eq >= 0) & (eq < pe);
+    const bool pv = pe >= 0;
+    uint64_t eqm = pv ? __ballot(pv) : 0ull, ltm = 0ull;  // valid lanes: same expert / smaller expert
+#pragma unroll
+    for (int b = kExpertBits - 1; b >= 0; --b) {
+        const bool mine = (pe >> b) & 1;
+        const uint64_t set = __ballot(pv && mine);
+        if (mine) {
+            ltm |= eqm & ~set;
+            eqm &= set;
+        } else {
+            eqm &= ~set;
+        }
     }
-    const int gfirst = pe >= 0 && grank == 0;
-    int gdless = 0;  // distinct experts below pe
-    for (int q = 0; q < P; ++q) {
-        const int eq = __builtin_amdgcn_readlane(pe, q), fq = __builtin_amdgcn_readlane(gfirst, q);
-        gdless += fq & (eq < pe);
-    }
-    const int num_active = __popcll(__ballot(gfirst));
+    const int grank = __popcll(eqm & ((1ull << lane) - 1ull));  // pairs of the same expert before this one
+    const int gbefore = __popcll(ltm);                            // pairs of smaller experts
+    const bool gfirst = pv && grank == 0;
+    const uint64_t firsts = __ballot(gfirst);
+    const int gdless = __popcll(ltm & firsts);  // distinct experts below pe
+    const int num_active = __popcll(firsts);
     // expert of active index ai (wave-uniform; expert 0 past the last)
     auto active_of = [&](int ai) -> int {
         const uint64_t m = __ballot(gfirst && gdless == ai);

@@ -8,6 +8,8 @@
 namespace dmoe {
 
 constexpr int kMaxExperts = 512;      // routed experts per bank
+constexpr int kExpertBits = 9;        // bits of an expert index
+static_assert((1 << kExpertBits) >= kMaxExperts, "expert index bits");
 constexpr int kMaxDecodePairs = 256;  // tokens * top_k handled by the decode kernels
 constexpr int kMaxHidden = 8192;
 constexpr int kMaxInter = 4096;

@@ -121,16 +121,17 @@ __device__ __forceinline__ void wave_route_token(const float (&l)[kRouteLaneSlot
 
 // wave_route_token for at most 2 * 64 experts (l[0] = expert lane, l[1] =
 // lane + 64), with the same arithmetic and so the same bits.  A round's
-// winner is the lowest expert among the lanes holding the round's maximum key:
-// the lowest such lane in l[0] (a lane prefers l[0] on equal keys), else the
-// lowest in l[1] -- two ballots and a find-first-set instead of a second
-// wave-wide reduction.
+// winner is the lowest expert holding the round's maximum key among the
+// experts still available: the lowest such lane in l[0], else the lowest in
+// l[1] -- two ballots and a find-first-set instead of a second wave-wide
+// reduction.  Availability lives in two wave-uniform masks; the key of a taken
+// or absent expert is 0, so the round's maximum is the largest available key
+// (a real key of 0, the NaN pattern 0xFFFFFFFF, still competes through the
+// masks).
 __device__ __forceinline__ void wave_route_small(const float (&l)[kRouteLaneSlots], int experts, int top_k,
                                                  int renormalize, int& id_out, float& w_out) {
     const int lane = threadIdx.x % kWave;
     const bool ok0 = lane < experts, ok1 = lane + kWave < experts;
-    uint32_t key0 = ordered_bits(l[0]), key1 = ordered_bits(l[1]);
-    bool av0 = ok0, av1 = ok1;
     float m = -INFINITY;
     if (ok0) m = fmaxf(m, l[0]);
     if (ok1) m = fmaxf(m, l[1]);
@@ -140,24 +141,26 @@ __device__ __forceinline__ void wave_route_small(const float (&l)[kRouteLaneSlot
     if (ok0) sum += ex0;
     if (ok1) sum += ex1;
     sum = wave_sum_dpp(sum);
+    uint32_t k0 = ok0 ? ordered_bits(l[0]) : 0u, k1 = ok1 ? ordered_bits(l[1]) : 0u;
+    uint64_t av0 = __ballot(ok0), av1 = __ballot(ok1);
     int my_id = 0;
     float my_x = 0.0f;
     for (int slot = 0; slot < top_k; ++slot) {
-        const bool b1 = av1 && (!av0 || key1 > key0);  // this lane's best: l[1] only when strictly larger
-        const bool any = av0 || av1;
-        const uint32_t bk = b1 ? key1 : key0;
-        const uint32_t mk = wave_max_u32(any ? bk : 0u);
-        const uint64_t w0 = __ballot(any && !b1 && bk == mk), w1 = __ballot(any && b1 && bk == mk);
-        const int win = w0 ? __builtin_ctzll(w0) : kWave + __builtin_ctzll(w1);
-        const int wl = win % kWave;
-        const float xw = readlane_f32(win < kWave ? ex0 : ex1, wl);
-        if (lane == wl) {
-            if (win < kWave) av0 = false;
-            else av1 = false;
+        const uint32_t mk = wave_max_u32(max(k0, k1));
+        const uint64_t w0 = __ballot(k0 == mk) & av0, w1 = __ballot(k1 == mk) & av1;
+        const bool low = w0 != 0;  // wave-uniform
+        const int wl = (int)__builtin_ctzll(low ? w0 : w1);
+        const float x0 = readlane_f32(ex0, wl), x1 = readlane_f32(ex1, wl);
+        if (low) {
+            av0 &= ~(1ull << wl);
+            if (lane == wl) k0 = 0u;
+        } else {
+            av1 &= ~(1ull << wl);
+            if (lane == wl) k1 = 0u;
         }
         if (lane == slot) {
-            my_id = win;
-            my_x = xw;
+            my_id = low ? wl : kWave + wl;
+            my_x = low ? x0 : x1;
         }
     }
     const float p = lane < top_k ? my_x / sum : 0.0f;

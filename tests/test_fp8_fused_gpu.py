@@ -84,6 +84,27 @@ def test_fused_router_layer_equals_three_launch(cuda, decode_mode, tokens):
     np.testing.assert_array_equal(fi.cpu().numpy(), eids)
 
 
+@pytest.mark.parametrize("experts,tokens", [(128, 1), (100, 3), (8, 2)])
+def test_fused_router_ties_and_partial_lanes(cuda, decode_mode, experts, tokens):
+    """Heavily tied logits (8 distinct values) and a -inf logit, with expert
+    counts that leave the second logit of some or all lanes empty: the
+    single-launch router's ids and weights equal the router kernel's, its ids
+    the oracle's (ties to the lower expert)."""
+    print_case("fused router ties", experts, tokens)
+    g = torch.Generator().manual_seed(99 + experts + tokens)
+    staged = to_device(random_fp8_bank(experts, 1024, 256, layout="channel", generator=g), cuda)
+    x = torch.randn(tokens, 1024, generator=g).bfloat16().to(cuda)
+    logits = torch.randint(0, 8, (tokens, experts), generator=g).float() / 4.0
+    logits[0, experts // 2] = float("-inf")
+    logits = logits.to(cuda)
+    backend = HipExpertBackend()
+    (fo, fw, fi), (so, sw, si) = both(decode_mode, lambda: backend.forward_routed(x, logits, 8, staged))
+    assert torch.equal(fi, si) and torch.equal(fw, sw)
+    assert torch.equal(fo, so)
+    eids, _ = orc.route_topk(logits.cpu().numpy(), 8)
+    np.testing.assert_array_equal(fi.cpu().numpy(), eids)
+
+
 def test_fused_pairs_shared_row_and_quantized_handoff(cuda, decode_mode):
     print_case("fused pairs")
     g = torch.Generator().manual_seed(4040)
