@@ -119,6 +119,10 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
 constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16 lanes
+constexpr int kDppMirror4 = 0x1B;     // quad_perm [3,2,1,0]: lane i <-> 3-i within 4 lanes
+constexpr int kDppRor4 = 0x124;       // lane i reads lane (i - 4) mod 16 of its row
+constexpr int kDppRor12 = 0x12C;      // lane i reads lane (i + 4) mod 16 of its row
+constexpr int kDppShr1 = 0x111;       // lane i reads lane i - 1 of its row (the row's lane 0 reads 0)
 
 // Max over each 16-lane row; every lane of the row receives it.
 __device__ __forceinline__ float row_max(float v) {

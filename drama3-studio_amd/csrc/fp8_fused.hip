@@ -195,7 +195,8 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             if (t != wave) wave_route_load(src, t, E, lg);
             int id;
             float w;
-            wave_route_small(lg, E, src.top_k, src.renormalize, id, w);
+            if (src.top_k <= 8) wave_route_small(lg, E, src.top_k, src.renormalize, id, w);
+            else wave_route_rounds(lg, E, src.top_k, src.renormalize, id, w);
             if (lane < src.top_k) {
                 s.sid[t * src.top_k + lane] = (int16_t)id;
                 s.wt[t * src.top_k + lane] = round_through(w, src.w_dtype);

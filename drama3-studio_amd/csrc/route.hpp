@@ -120,15 +120,15 @@ __device__ __forceinline__ void wave_route_token(const float (&l)[kRouteLaneSlot
 }
 
 // wave_route_token for at most 2 * 64 experts (l[0] = expert lane, l[1] =
-// lane + 64), with the same arithmetic and so the same bits.  A round's
-// winner is the lowest expert holding the round's maximum key among the
-// experts still available: the lowest such lane in l[0], else the lowest in
-// l[1] -- two ballots and a find-first-set instead of a second wave-wide
+// lane + 64) and any top_k, with the same arithmetic and so the same bits.  A
+// round's winner is the lowest expert holding the round's maximum key among
+// the experts still available: the lowest such lane in l[0], else the lowest
+// in l[1] -- two ballots and a find-first-set instead of a second wave-wide
 // reduction.  Availability lives in two wave-uniform masks; the key of a taken
 // or absent expert is 0, so the round's maximum is the largest available key
 // (a real key of 0, the NaN pattern 0xFFFFFFFF, still competes through the
 // masks).
-__device__ __forceinline__ void wave_route_small(const float (&l)[kRouteLaneSlots], int experts, int top_k,
+__device__ __forceinline__ void wave_route_rounds(const float (&l)[kRouteLaneSlots], int experts, int top_k,
                                                  int renormalize, int& id_out, float& w_out) {
     const int lane = threadIdx.x % kWave;
     const bool ok0 = lane < experts, ok1 = lane + kWave < experts;
@@ -167,6 +167,87 @@ __device__ __forceinline__ void wave_route_small(const float (&l)[kRouteLaneSlot
     float wtot = 0.0f;
     for (int j = 0; j < top_k; ++j) wtot += readlane_f32(p, j);
     id_out = my_id;
+    w_out = renormalize ? p / wtot : p;
+}
+
+// Sort-network pieces for wave_route_small: 64-bit keys (order-preserving
+// logit bits, then the inverted expert index; 0 = no expert) moved between
+// lanes as two dwords.  cmpx keeps the larger or the smaller of a lane pair.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {  // every lane has a source: no old value
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src), hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t cmpx(uint64_t v, uint64_t partner, bool keep_max) {
+    return (partner > v) == keep_max ? partner : v;  // equal keys (both 0) are interchangeable
+}
+// Descending sort of each 8-lane group: merges of sorted halves whose first
+// comparator pairs position i with its mirror, then half-cleaners.
+__device__ __forceinline__ uint64_t sort8_desc(uint64_t v, int lane) {
+    v = cmpx(v, dpp_u64<kDppXor1>(v), !(lane & 1));
+    v = cmpx(v, dpp_u64<kDppMirror4>(v), (lane & 3) < 2);
+    v = cmpx(v, dpp_u64<kDppXor1>(v), !(lane & 1));
+    v = cmpx(v, dpp_u64<kDppHalfMirror>(v), (lane & 7) < 4);
+    v = cmpx(v, dpp_u64<kDppXor2>(v), !(lane & 2));
+    v = cmpx(v, dpp_u64<kDppXor1>(v), !(lane & 1));
+    return v;
+}
+// A bitonic 8-lane group sorted descending (half-cleaners at distance 4, 2, 1).
+__device__ __forceinline__ uint64_t clean8_desc(uint64_t v, int lane) {
+    const uint64_t up = dpp_u64<kDppRor12>(v), down = dpp_u64<kDppRor4>(v);
+    v = cmpx(v, (lane & 4) ? down : up, !(lane & 4));
+    v = cmpx(v, dpp_u64<kDppXor2>(v), !(lane & 2));
+    v = cmpx(v, dpp_u64<kDppXor1>(v), !(lane & 1));
+    return v;
+}
+
+// wave_route_token for at most 2 * 64 experts (l[0] = expert lane, l[1] =
+// lane + 64) and top_k <= 8, with the same arithmetic and so the same bits,
+// without serial rounds: a sorting network over the 128 unique keys (larger
+// logit first, the lower expert on ties) leaves the 8 best, in slot order, in
+// every 8-lane group -- sort each group's 8 keys of l[0] and of l[1], keep the
+// larger of each mirrored pair (a bitonic top 8) and clean it, then the same
+// merge with the mirrored group of the row, of the other row of the half and
+// of the other half.  Lane s < top_k recomputes its slot's exp(l - max) from
+// the key's logit bits and sums the probabilities in slot order with a shift
+// scan.  top_k > 8 takes the serial rounds of wave_route_rounds.
+__device__ __forceinline__ void wave_route_small(const float (&l)[kRouteLaneSlots], int experts, int top_k,
+                                                 int renormalize, int& id_out, float& w_out) {
+    const int lane = threadIdx.x % kWave;
+    const bool ok0 = lane < experts, ok1 = lane + kWave < experts;
+    float m = -INFINITY;
+    if (ok0) m = fmaxf(m, l[0]);
+    if (ok1) m = fmaxf(m, l[1]);
+    m = wave_max_dpp(m);
+    const float ex0 = expf(l[0] - m), ex1 = expf(l[1] - m);
+    float sum = 0.0f;
+    if (ok0) sum += ex0;
+    if (ok1) sum += ex1;
+    sum = wave_sum_dpp(sum);
+    uint64_t x = ok0 ? ((uint64_t)ordered_bits(l[0]) << 32) | (uint32_t)~lane : 0ull;
+    uint64_t y = ok1 ? ((uint64_t)ordered_bits(l[1]) << 32) | (uint32_t)~(kWave + lane) : 0ull;
+    x = sort8_desc(x, lane);
+    y = sort8_desc(y, lane);
+    uint64_t z = clean8_desc(umax64(x, dpp_u64<kDppHalfMirror>(y)), lane);
+    z = clean8_desc(umax64(z, dpp_u64<kDppMirror>(z)), lane);
+    z = clean8_desc(umax64(z, shfl_u64(z, lane ^ 0x17)), lane);  // the other row of the half, mirrored
+    z = clean8_desc(umax64(z, shfl_u64(z, lane ^ 0x27)), lane);  // the other half, mirrored
+    const uint32_t o = (uint32_t)(z >> 32);
+    const float lw = __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);  // the logit (-0 -> +0)
+    const float p = lane < top_k ? expf(lw - m) / sum : 0.0f;
+    float acc = p;  // lane s: p_0 + ... + p_s, added in slot order
+    for (int j = 1; j < top_k; ++j) {
+        const float prev = dpp_f32<kDppShr1>(acc);
+        acc = lane >= 1 ? prev + p : p;
+    }
+    const float wtot = readlane_f32(acc, top_k - 1);
+    id_out = (int)~(uint32_t)z;
     w_out = renormalize ? p / wtot : p;
 }
 

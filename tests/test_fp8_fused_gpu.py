@@ -84,13 +84,14 @@ def test_fused_router_layer_equals_three_launch(cuda, decode_mode, tokens):
     np.testing.assert_array_equal(fi.cpu().numpy(), eids)
 
 
-@pytest.mark.parametrize("experts,tokens", [(128, 1), (100, 3), (8, 2)])
-def test_fused_router_ties_and_partial_lanes(cuda, decode_mode, experts, tokens):
+@pytest.mark.parametrize("experts,tokens,top_k", [(128, 1, 8), (100, 3, 8), (8, 2, 8), (128, 1, 5), (64, 2, 12)])
+def test_fused_router_ties_and_partial_lanes(cuda, decode_mode, experts, tokens, top_k):
     """Heavily tied logits (8 distinct values) and a -inf logit, with expert
-    counts that leave the second logit of some or all lanes empty: the
-    single-launch router's ids and weights equal the router kernel's, its ids
-    the oracle's (ties to the lower expert)."""
-    print_case("fused router ties", experts, tokens)
+    counts that leave the second logit of some or all lanes empty, top_k up to
+    8 (the sorting network) and above (serial rounds): the single-launch
+    router's ids and weights equal the router kernel's, its ids the oracle's
+    (ties to the lower expert)."""
+    print_case("fused router ties", experts, tokens, top_k)
     g = torch.Generator().manual_seed(99 + experts + tokens)
     staged = to_device(random_fp8_bank(experts, 1024, 256, layout="channel", generator=g), cuda)
     x = torch.randn(tokens, 1024, generator=g).bfloat16().to(cuda)
@@ -98,10 +99,10 @@ def test_fused_router_ties_and_partial_lanes(cuda, decode_mode, experts, tokens)
     logits[0, experts // 2] = float("-inf")
     logits = logits.to(cuda)
     backend = HipExpertBackend()
-    (fo, fw, fi), (so, sw, si) = both(decode_mode, lambda: backend.forward_routed(x, logits, 8, staged))
+    (fo, fw, fi), (so, sw, si) = both(decode_mode, lambda: backend.forward_routed(x, logits, top_k, staged))
     assert torch.equal(fi, si) and torch.equal(fw, sw)
     assert torch.equal(fo, so)
-    eids, _ = orc.route_topk(logits.cpu().numpy(), 8)
+    eids, _ = orc.route_topk(logits.cpu().numpy(), top_k)
     np.testing.assert_array_equal(fi.cpu().numpy(), eids)
 
 
