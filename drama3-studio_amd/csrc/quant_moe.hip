@@ -549,25 +549,34 @@ __device__ __forceinline__ void rotate16(float (&v)[16], float* tb, int lane) {
 }
 
 // Whole wave; e = the expert of pair `lane`, -1 for invalid or absent pairs.
-__device__ __forceinline__ void group_pairs(int e, int P, int lane, SmallGroups& g) {
-    int rank = 0, before = 0;
-    for (int q = 0; q < P; ++q) {
-        const int eq = __builtin_amdgcn_readlane(e, q);
-        rank += (eq == e) & (q < lane);
-        before += (eq >= 0) & (eq < e);
+// The comparisons run over the expert bits, most significant first: per bit
+// one ballot of the lanes holding it; a lane keeps the mask of lanes equal to
+// it so far and collects those that fall below it at this bit.
+__device__ __forceinline__ void group_pairs(int e, int lane, SmallGroups& g) {
+    const bool v = e >= 0;
+    uint64_t eqm = v ? __ballot(v) : 0ull, ltm = 0ull;  // valid lanes: same expert / smaller expert
+#pragma unroll
+    for (int b = kExpertBits - 1; b >= 0; --b) {
+        const bool mine = (e >> b) & 1;
+        const uint64_t set = __ballot(v && mine);
+        if (mine) {
+            ltm |= eqm & ~set;
+            eqm &= set;
+        } else {
+            eqm &= ~set;
+        }
     }
-    const int first = e >= 0 && rank == 0;
-    int dless = 0;  // distinct experts below e
-    for (int q = 0; q < P; ++q) {
-        const int eq = __builtin_amdgcn_readlane(e, q), fq = __builtin_amdgcn_readlane(first, q);
-        dless += fq & (eq < e);
-    }
-    if (e >= 0) g.plist[before + rank] = lane;
+    const int rank = __popcll(eqm & ((1ull << lane) - 1ull));  // pairs of the same expert before this one
+    const int before = __popcll(ltm);                           // pairs of smaller experts
+    const bool first = v && rank == 0;
+    const uint64_t firsts = __ballot(first);
+    const int dless = __popcll(ltm & firsts);  // distinct experts below e
+    if (v) g.plist[before + rank] = lane;
     if (first) {
         g.active[dless] = e;
         g.start[dless] = before;
     }
-    const int na = __popcll(__ballot(first)), valid = __popcll(__ballot(e >= 0));
+    const int na = __popcll(firsts), valid = __popcll(__ballot(v));
     if (lane == 0) {
         g.num_active = na;
         g.start[na] = valid;
@@ -638,7 +647,7 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
     if (wave == 0) {
         const int pe = lane < P ? id_expert(idb, a.ids_dtype, a.experts) : -1;
         if (lane < P && pe < 0 && blockIdx.x == 0 && blockIdx.y == 0) raise_status(a.status, kBadExpertId);
-        group_pairs(pe, P, lane, s.g);
+        group_pairs(pe, lane, s.g);
     }
     lds_barrier();
     if ((int)blockIdx.x >= s.g.num_active) {  // uniform: fewer distinct experts than the grid assumed
@@ -874,24 +883,21 @@ __global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDown
             hin[q] = load_raw16<kBF16>(a.act, (int64_t)(u / nb) * I + (u % nb) * 256 + 16 * (lane % 16));
         }
         for (int r = threadIdx.x; r < P; r += kQdThreads) s.rmax[r] = 0u;
-    } else {
-        constexpr int kChunks = kQdMaxBf16 / 8 / kQdThreads;  // 16-byte chunks per thread
-        const int chunks = P * I / 8;
-        v4i c16[kChunks];
+    }
+    // mode 0: the bf16 hidden rows, stored to LDS once the weight loads are out
+    constexpr int kChunks = MODE == 0 ? kQdMaxBf16 / 8 / kQdThreads : 1;  // 16-byte chunks per thread
+    const int chunks = P * I / 8;
+    v4i c16[kChunks];
+    if constexpr (MODE == 0) {
 #pragma unroll
         for (int j = 0; j < kChunks; ++j)
             c16[j] = *(const v4i*)(a.act + (int64_t)min((int)threadIdx.x + j * kQdThreads, chunks - 1) * 8);
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            const int i = threadIdx.x + j * kQdThreads;
-            if (i < chunks) *(v4i*)(s.act.h + i * 8) = c16[j];
-        }
     }
     for (int i = threadIdx.x; i < P * 8; i += kQdThreads) s.part[i / 8][i % 8] = 0.0f;
     const int pe = pl ? id_expert(idb, a.ids_dtype, a.experts) : -1;
     if (wave == 0) {
         if (pl && pe < 0 && blockIdx.x == 0) raise_status(a.status, kBadExpertId);
-        group_pairs(pe, P, lane, s.g);
+        group_pairs(pe, lane, s.g);
     }
     lds_barrier();
 
@@ -917,7 +923,14 @@ __global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDown
     };
     fetch_batch(min(wave, max(batches - 1, 0)));  // waves without a batch: loaded, never used
 
-    if constexpr (MODE != 0) {
+    if constexpr (MODE == 0) {
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const int i = threadIdx.x + j * kQdThreads;
+            if (i < chunks) *(v4i*)(s.act.h + i * 8) = c16[j];
+        }
+        lds_barrier();
+    } else {
         // rotation (H4^{x4} / 16 per 256-block, rounded to bf16) and row INT8
         pin_after_loads(hin);  // keeps the rotation behind the weight loads
         float v[kQdGroups][16];
