@@ -604,19 +604,24 @@ struct QGateUpLds {
     float book[16];
     union {
         float tb[kQWaves][kRotWaveDwords];  // rotation transposes
-        float red[kQWaves][kWave][8];       // cross-wave reduction
+        float red[kQWaves][kWave][12];      // cross-wave reduction (gate, up, third tile)
     };
 };
 
-template <int MODE, int XT, int KBW>
+// NT: B operand tiles of 16 rows -- 2: 16 gate + 16 up columns per
+// workgroup; 3: 24 + 24, the third tile holding gate columns 16-23 (MFMA
+// columns 0-7) and up columns 16-23 (8-15), so that 8 active experts of a
+// 768-column expert make one workgroup per CU instead of 1.5.
+template <int MODE, int XT, int KBW, int NT>
 __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGateUpArgs a) {
     constexpr bool F16 = XT == kF16;
+    constexpr int NX = NT == 3 ? KBW : 1;  // third-tile registers
     __shared__ QGateUpLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int col = lane % 16, grp = lane / 16;
     const QuantProjArgs& w = a.w13;
     const int H = w.K, I = w.N / 2, KB = H / 128, P = a.pairs, rows = a.rows;
-    const int n0 = blockIdx.y * 16;
+    const int n0 = blockIdx.y * (NT == 3 ? 24 : 16);
 
     // loads are issued unconditionally (clamped indexes): a load merged with
     // a constant on another path is waited for at the merge
@@ -657,19 +662,25 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
     const int ai = blockIdx.x;
     const int e = s.g.active[ai], pbeg = s.g.start[ai], pend = s.g.start[ai + 1];
     const int ng = n0 + col, nu = I + n0 + col;
+    const int nxg = n0 + 16 + (col & 7), nxu = I + nxg, nx = col < 8 ? nxg : nxu;  // third tile (NT 3)
 
     // weight rows of this wave, loaded now, dequantized after the rotation
-    WRaw rg[KBW], ru[KBW];
+    WRaw rg[KBW], ru[KBW], rx[NX];
 #pragma unroll
     for (int i = 0; i < KBW; ++i) {
         const int kb = min(wave + i * kQWaves, KB - 1);  // blocks past K: loaded, never used
         rg[i] = fetch_wrow<MODE>(w, e, ng, kb, grp);
         ru[i] = fetch_wrow<MODE>(w, e, nu, kb, grp);
+        if constexpr (NT == 3) rx[i] = fetch_wrow<MODE>(w, e, nx, kb, grp);
     }
-    float sbg = 1.0f, sbu = 1.0f, bk = 0.0f;
+    float sbg = 1.0f, sbu = 1.0f, sxg = 1.0f, sxu = 1.0f, bk = 0.0f;
     if constexpr (MODE != 0) {
         sbg = channel_scale<MODE>(w, e, ng);
         sbu = channel_scale<MODE>(w, e, nu);
+        if constexpr (NT == 3) {  // both scales of the lane's third-tile column (col & 7)
+            sxg = channel_scale<MODE>(w, e, nxg);
+            sxu = channel_scale<MODE>(w, e, nxu);
+        }
     }
     if constexpr (MODE == 3)  // codebook entry lane % 16 (rows 0..15 of the aux bytes)
         bk = *(const float*)(w.s + (int64_t)e * w.s_se + (int64_t)(lane % 16) * w.s_sn + H / 16 + 4);
@@ -705,13 +716,14 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
     }
     lds_barrier();
 
-    WRow bg[KBW], bu[KBW];
+    WRow bg[KBW], bu[KBW], bx[NX];
 #pragma unroll
     for (int i = 0; i < KBW; ++i) {
         const int kb = wave + i * kQWaves;
         if (kb < KB) {
             decode_wrow<MODE, F16>(rg[i], ng, s.book, bg[i]);
             decode_wrow<MODE, F16>(ru[i], nu, s.book, bu[i]);
+            if constexpr (NT == 3) decode_wrow<MODE, F16>(rx[i], nx, s.book, bx[i]);
         }
     }
 
@@ -719,8 +731,8 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
         const int mc = min(16, pend - m0);
         const bool live = col < mc;
         const int xr = live ? s.g.plist[m0 + col] / a.row_div : 0;
-        v4f fg = {0, 0, 0, 0}, fu = {0, 0, 0, 0};
-        v4i ig = {0, 0, 0, 0}, iu = {0, 0, 0, 0};
+        v4f fg = {0, 0, 0, 0}, fu = {0, 0, 0, 0}, fx = {0, 0, 0, 0};
+        v4i ig = {0, 0, 0, 0}, iu = {0, 0, 0, 0}, ix = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < KBW; ++i) {
             const int kb = wave + i * kQWaves;
@@ -735,9 +747,14 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
                                                                      __builtin_bit_cast(v8h, bg[i].r[t]), fg, 0, 0, 0);
                         fu = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, av),
                                                                      __builtin_bit_cast(v8h, bu[i].r[t]), fu, 0, 0, 0);
+                        if constexpr (NT == 3)
+                            fx = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, av),
+                                                                         __builtin_bit_cast(v8h, bx[i].r[t]), fx, 0, 0, 0);
                     } else {
                         fg = mfma_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bg[i].r[t]), fg);
                         fu = mfma_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bu[i].r[t]), fu);
+                        if constexpr (NT == 3)
+                            fx = mfma_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bx[i].r[t]), fx);
                     }
                 }
             } else {
@@ -748,6 +765,10 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
                 ig = mfma_i8(a1, bg[i].r[1], ig);
                 iu = mfma_i8(a0, bu[i].r[0], iu);
                 iu = mfma_i8(a1, bu[i].r[1], iu);
+                if constexpr (NT == 3) {
+                    ix = mfma_i8(a0, bx[i].r[0], ix);
+                    ix = mfma_i8(a1, bx[i].r[1], ix);
+                }
             }
         }
         // cross-wave reduction (exact in int32 for modes 1-3)
@@ -755,6 +776,7 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
         for (int r = 0; r < 4; ++r) {
             s.red[wave][lane][r] = MODE == 0 ? fg[r] : __int_as_float(ig[r]);
             s.red[wave][lane][4 + r] = MODE == 0 ? fu[r] : __int_as_float(iu[r]);
+            if constexpr (NT == 3) s.red[wave][lane][8 + r] = MODE == 0 ? fx[r] : __int_as_float(ix[r]);
         }
         lds_barrier();
         if (wave == 0) {
@@ -785,6 +807,32 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
                 yu = bf16_round(yu);
                 const float act = bf16_round(bf16_round(yg / (1.0f + expf(-yg))) * yu);
                 a.act[(int64_t)p * I + n0 + col] = __builtin_bit_cast(uint16_t, (__bf16)act);
+                if constexpr (NT == 3) {
+                    if (col < 8) {  // gate column n0 + 16 + col here, its up column in lane + 8
+                        float xg, xu;
+                        if constexpr (MODE == 0) {
+                            xg = s.red[0][lane][8 + r];
+                            xu = s.red[0][lane + 8][8 + r];
+                            for (int q = 1; q < kQWaves; ++q) {
+                                xg += s.red[q][lane][8 + r];
+                                xu += s.red[q][lane + 8][8 + r];
+                            }
+                        } else {
+                            int sg = 0, su = 0;
+                            for (int q = 0; q < kQWaves; ++q) {
+                                sg += __float_as_int(s.red[q][lane][8 + r]);
+                                su += __float_as_int(s.red[q][lane + 8][8 + r]);
+                            }
+                            const float sa = s.sa[p / a.row_div];
+                            xg = (float)sg * sa * sxg;
+                            xu = (float)su * sa * sxu;
+                        }
+                        xg = bf16_round(xg);
+                        xu = bf16_round(xu);
+                        const float xact = bf16_round(bf16_round(xg / (1.0f + expf(-xg))) * xu);
+                        a.act[(int64_t)p * I + nxg] = __builtin_bit_cast(uint16_t, (__bf16)xact);
+                    }
+                }
             }
         }
         lds_barrier();
@@ -802,15 +850,36 @@ bool quant_gateup_decode_fits(int mode, int pairs, int rows, int H, int I, const
     return H % 256 == 0 && rows * (H / 256) <= kQWaves * kQgUnits;
 }
 
+namespace {
+int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+}  // namespace
+
 void launch_quant_gateup_decode(const QuantGateUpArgs& a, hipStream_t stream) {
-    const dim3 grid((unsigned)std::min(a.pairs, a.experts), (unsigned)(a.w13.N / 2 / 16)), block(kQThreads);
+    // 24-column workgroups when 16-column ones would not all fit one per CU
+    const int I = a.w13.N / 2, max_active = std::min(a.pairs, a.experts);
+    const bool wide = I % 24 == 0 && max_active * (I / 16) > device_cus();
+    const dim3 grid((unsigned)max_active, (unsigned)(I / (wide ? 24 : 16))), block(kQThreads);
     const int kbw = (a.w13.K / 128 + kQWaves - 1) / kQWaves;
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
+    auto by_nt = [&](auto m, auto xt, auto kb) {
+        constexpr int M = decltype(m)::value, X = decltype(xt)::value, K = decltype(kb)::value;
+        if (wide) go(quant_gateup_decode_kernel<M, X, K, 3>);
+        else go(quant_gateup_decode_kernel<M, X, K, 2>);
+    };
     auto by_kbw = [&](auto m, auto xt) {
-        constexpr int M = decltype(m)::value, X = decltype(xt)::value;
-        if (kbw <= 1) go(quant_gateup_decode_kernel<M, X, 1>);
-        else if (kbw <= 2) go(quant_gateup_decode_kernel<M, X, 2>);
-        else go(quant_gateup_decode_kernel<M, X, 4>);
+        if (kbw <= 1) by_nt(m, xt, std::integral_constant<int, 1>{});
+        else if (kbw <= 2) by_nt(m, xt, std::integral_constant<int, 2>{});
+        else by_nt(m, xt, std::integral_constant<int, 4>{});
     };
     auto by_x = [&](auto m) {
         constexpr int M = decltype(m)::value;

@@ -182,6 +182,34 @@ def test_small_call_launches_match_separate_launches(cuda, small_launches, mode,
     assert rel_inf(out1.float().cpu().numpy(), expected) < TOL
 
 
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("inter,tokens,top_k", [(768, 1, 8), (768, 2, 8)])
+def test_small_call_wide_gateup_workgroups(cuda, small_launches, mode, inter, tokens, top_k):
+    """Expert widths divisible by 24 whose 16-column gate/up workgroups would
+    outnumber the CUs take 24-column workgroups (a third MFMA tile holding
+    gate and up columns 16-23): bit-identical to the separate launches for
+    modes 1-3, within the bar for mode 0, and against the oracle."""
+    print_case("quant wide gate/up", mode, inter, tokens, top_k)
+    g = torch.Generator().manual_seed(1700 + 16 * mode + tokens)
+    store = random_quantized_bank(mode, 32, 512, inter, generator=g)
+    dev = to_device(store, cuda)
+    x = torch.randn(tokens, 512, generator=g).bfloat16()
+    ids, w = orc.route_topk(torch.randn(tokens, 32, generator=g).numpy(), top_k)
+    weights = torch.from_numpy(w).bfloat16()
+    backend = quantized.QuantizedExpertBackend(mode)
+    args = (x.to(cuda), torch.from_numpy(ids).to(cuda), weights.to(cuda), dev)
+    outs = {}
+    for single in (True, False):
+        small_launches(single)
+        outs[single] = backend.forward(*args)
+    if mode:
+        assert torch.equal(outs[True], outs[False])
+    else:
+        assert rel_inf(outs[True].float().cpu().numpy(), outs[False].float().cpu().numpy()) < TOL
+    expected = oracle_layer(store, x.float().numpy(), ids, weights.float().numpy())
+    assert rel_inf(outs[True].float().cpu().numpy(), expected) < TOL
+
+
 def test_w4a16_asymmetric_zero_points(cuda):
     print_case("w4a16 asym")
     g = torch.Generator().manual_seed(404)
