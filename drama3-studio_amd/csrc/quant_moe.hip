@@ -53,6 +53,8 @@ __device__ __forceinline__ float bf16_round(float v) { return (float)(__bf16)v; 
 // E4M3 byte -> fp32 (hardware decode of one byte).
 __device__ __forceinline__ float e4m3(uint32_t byte) { return fp8x2_to_f32(byte & 0xFFu, false)[0]; }
 
+using h2v = _Float16 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ int8_t q8(float level, float rel) {
     const float v = fminf(fmaxf(__builtin_rintf(level * rel), -127.0f), 127.0f);
     return (int8_t)(int)v;
@@ -251,6 +253,38 @@ __device__ __forceinline__ void decode_wrow(const WRaw& raw, int n, const float*
     } else if constexpr (MODE == 1) {
         out.r[0] = raw.a;
         out.r[1] = raw.b;
+    } else if constexpr (MODE == 2) {
+        // Two codes per packed fp16 pair: code c as the fp16 1024 + c (exponent
+        // 2^10, ulp 1); level = that - 1056; level * rel is exact (6 + 4
+        // significant bits, |.| <= 32 * 448); clamping to [-127, 127] before
+        // the rounding equals clamping after it (integer bounds); + 1536 then
+        // rounds to the nearest even integer r and leaves r's two's-complement
+        // byte as the low byte of the half -- q8(level, rel) for every code and
+        // E4M3 byte.  Pair k of a group holds codes k (low half) and k + 8.
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {  // 16 codes = K [32 g + 16 j, +16): one rel group
+            const _Float16 rh = (_Float16)e4m3(raw.x >> (8 * j));  // exact
+            const h2v rel2 = {rh, rh};
+            const uint32_t a0 = (uint32_t)raw.a[2 * j], a1 = (uint32_t)raw.a[2 * j + 1], hw = (uint32_t)raw.b[j];
+            uint32_t pr[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t lo = ((a0 >> (4 * k)) & 15u) | (((a1 >> (4 * k)) & 15u) << 16);
+                const uint32_t hi = (hw >> (2 * k)) & 0x00030003u;
+                h2v v = (__builtin_bit_cast(h2v, lo | (hi << 4) | 0x64006400u) - h2v{1056, 1056}) * rel2;
+                v = __builtin_elementwise_min(__builtin_elementwise_max(v, h2v{-127, -127}), h2v{127, 127});
+                pr[k] = __builtin_bit_cast(uint32_t, v + h2v{1536, 1536});
+            }
+            // int q of the group: codes 4q .. 4q + 3 (low bytes of the halves)
+            const uint32_t t01 = __builtin_amdgcn_perm(pr[1], pr[0], 0x06020400u);
+            const uint32_t t23 = __builtin_amdgcn_perm(pr[3], pr[2], 0x06020400u);
+            const uint32_t t45 = __builtin_amdgcn_perm(pr[5], pr[4], 0x06020400u);
+            const uint32_t t67 = __builtin_amdgcn_perm(pr[7], pr[6], 0x06020400u);
+            out.r[j][0] = (int)__builtin_amdgcn_perm(t23, t01, 0x05040100u);
+            out.r[j][1] = (int)__builtin_amdgcn_perm(t67, t45, 0x05040100u);
+            out.r[j][2] = (int)__builtin_amdgcn_perm(t23, t01, 0x07060302u);
+            out.r[j][3] = (int)__builtin_amdgcn_perm(t67, t45, 0x07060302u);
+        }
     } else {
         const float rel[2] = {e4m3(raw.x), e4m3(raw.x >> 8)};
 #pragma unroll
@@ -262,15 +296,7 @@ __device__ __forceinline__ void decode_wrow(const WRaw& raw, int n, const float*
                 for (int b = 0; b < 4; ++b) {
                     const int c = j * 16 + q * 4 + b;  // code index within the lane's 32
                     const uint32_t lo = ((uint32_t)raw.a[c / 8] >> (4 * (c % 8))) & 15u;
-                    float level;
-                    if constexpr (MODE == 2) {
-                        const uint32_t hw = (uint32_t)(c < 16 ? raw.b[0] : raw.b[1]);
-                        const uint32_t hi = (hw >> (2 * (c % 16))) & 3u;
-                        level = (float)(int)(lo | (hi << 4)) - 32.0f;
-                    } else {
-                        level = book[lo];
-                    }
-                    packed |= ((uint32_t)(uint8_t)q8(level, rel[j])) << (8 * b);
+                    packed |= ((uint32_t)(uint8_t)q8(book[lo], rel[j])) << (8 * b);
                 }
                 out.r[j][q] = (int)packed;
             }
