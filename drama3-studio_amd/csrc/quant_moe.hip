@@ -310,6 +310,27 @@ __device__ __forceinline__ void load_wrow(const QuantProjArgs& a, int e, int n, 
     decode_wrow<MODE, F16>(fetch_wrow<MODE>(a, e, n, kb, grp), n, book, out);
 }
 
+// W4A8 INT8 weights by table: tab[rel byte * 16 + code] = q8(book[code],
+// e4m3(rel byte)), so the result equals decode_wrow<3>'s.  A lane's four codes
+// of an output int index the 16-byte row of its group's scale byte through
+// two byte permutes (codes 0-7 and 8-15) and a byte select.
+__device__ __forceinline__ void decode_w4a8_tab(const WRaw& raw, const int8_t* tab, WRow& out) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {  // 16 codes = K [32 g + 16 j, +16): one rel group
+        const v4i row = *(const v4i*)(tab + (((uint32_t)raw.x >> (8 * j)) & 0xFFu) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // codes 16 j + 4 q .. +3: nibbles 4 (q % 2) .. +3 of word 2 j + q / 2
+            uint32_t t = ((uint32_t)raw.a[2 * j + q / 2] >> (16 * (q % 2))) & 0xFFFFu;
+            t = (t | (t << 8)) & 0x00FF00FFu;
+            t = (t | (t << 4)) & 0x0F0F0F0Fu;  // byte b: code 4 q + b
+            const uint32_t sel = t & 0x07070707u, high = ((t >> 3) & 0x01010101u) * 0xFFu;
+            const uint32_t lo8 = __builtin_amdgcn_perm((uint32_t)row[1], (uint32_t)row[0], sel);
+            const uint32_t hi8 = __builtin_amdgcn_perm((uint32_t)row[3], (uint32_t)row[2], sel);
+            out.r[j][q] = (int)((hi8 & high) | (lo8 & ~high));
+        }
+    }
+}
+
 template <int MODE>
 __device__ __forceinline__ float channel_scale(const QuantProjArgs& a, int e, int n) {
     const uint8_t* sc = a.s + (int64_t)e * a.s_se + (int64_t)n * a.s_sn;
@@ -628,6 +649,7 @@ struct QGateUpLds {
     float sa[kQgMaxRows];
     uint32_t rmax[kQgMaxRows];  // row maxima (non-negative float bits)
     float book[16];
+    alignas(16) int8_t qtab[256 * 16];  // mode 3: INT8 weight of (scale byte, code)
     union {
         float tb[kQWaves][kRotWaveDwords];  // rotation transposes
         float red[kQWaves][kWave][12];      // cross-wave reduction (gate, up, third tile)
@@ -739,6 +761,8 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
     }
     if constexpr (MODE == 3) {
         if (threadIdx.x < 16) s.book[threadIdx.x] = bk;
+        lds_barrier();
+        for (int i = threadIdx.x; i < 256 * 16; i += kQThreads) s.qtab[i] = q8(s.book[i % 16], e4m3((uint32_t)i / 16));
     }
     lds_barrier();
 
@@ -747,9 +771,15 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
     for (int i = 0; i < KBW; ++i) {
         const int kb = wave + i * kQWaves;
         if (kb < KB) {
-            decode_wrow<MODE, F16>(rg[i], ng, s.book, bg[i]);
-            decode_wrow<MODE, F16>(ru[i], nu, s.book, bu[i]);
-            if constexpr (NT == 3) decode_wrow<MODE, F16>(rx[i], nx, s.book, bx[i]);
+            if constexpr (MODE == 3) {  // one table for the workgroup's expert
+                decode_w4a8_tab(rg[i], s.qtab, bg[i]);
+                decode_w4a8_tab(ru[i], s.qtab, bu[i]);
+                if constexpr (NT == 3) decode_w4a8_tab(rx[i], s.qtab, bx[i]);
+            } else {
+                decode_wrow<MODE, F16>(rg[i], ng, s.book, bg[i]);
+                decode_wrow<MODE, F16>(ru[i], nu, s.book, bu[i]);
+                if constexpr (NT == 3) decode_wrow<MODE, F16>(rx[i], nx, s.book, bx[i]);
+            }
         }
     }
 
