@@ -58,6 +58,7 @@ constexpr int kAInst = kGroupM / 8 / kCopyWaves;    // A copy instructions per c
 constexpr int kBInst = kTileN / 8 / kCopyWaves;     // B copy instructions per copy wave per block (16)
 constexpr int kScaleInst = 4 / kCopyWaves;          // weight-scale (and row-scale) copies per copy wave (2)
 constexpr int kCopies = kAInst + kBInst + 2 * kScaleInst;  // vector-memory instructions per copy wave per block
+constexpr int kLeanCopies = kAInst + kBInst;                // the same without scale copies
 constexpr int kChunk = 16;                          // tiles whose metadata a workgroup holds at once
 static_assert(2 * kCopies <= 63, "two blocks of copies must fit the wave's vmcnt range");
 
@@ -123,17 +124,20 @@ __device__ __forceinline__ int a_copy(int cw, int j) { return cw * kAInst + j; }
 __device__ __forceinline__ int b_copy(int cw, int j) { return cw * kBInst + j; }
 __device__ __forceinline__ int s_copy(int cw, int j) { return cw * kScaleInst + j; }
 
-__device__ __forceinline__ void issue_stage(GemmLds& s, const TilePlan& p, int kb, int stage, int cw) {
+// Scale copies go to scale slot `slot` (the stage, or with scales constant
+// along K the tile's parity at its first block only); slot < 0: none.
+__device__ __forceinline__ void issue_stage(GemmLds& s, const TilePlan& p, int kb, int stage, int cw, int slot) {
     const int64_t koff = (int64_t)kb * 128;
 #pragma unroll
     for (int j = 0; j < kAInst; ++j) copy16_to_lds(p.a[j] + koff, &s.a[stage][a_copy(cw, j) * 1024]);
 #pragma unroll
     for (int j = 0; j < kBInst; ++j) copy16_to_lds(p.bbase + p.b[j] + koff, &s.b[stage][b_copy(cw, j) * 1024]);
+    if (slot < 0) return;
     const int64_t wk = (int64_t)(kb / p.kb_div) * p.ws_k, rk = (int64_t)kb * p.rs_k;
 #pragma unroll
     for (int j = 0; j < kScaleInst; ++j) {
-        copy4_to_lds(p.wsrc[j] + wk, &s.ws[stage][s_copy(cw, j)][0]);
-        copy4_to_lds(p.rsrc[j] + rk, &s.rs[stage][s_copy(cw, j)][0]);
+        copy4_to_lds(p.wsrc[j] + wk, &s.ws[slot][s_copy(cw, j)][0]);
+        copy4_to_lds(p.rsrc[j] + rk, &s.rs[slot][s_copy(cw, j)][0]);
     }
 }
 
@@ -286,6 +290,11 @@ __device__ __forceinline__ void grouped_tiles(const typename OP::Args& a) {
         __syncthreads();
 
         const int n_it = ntc * KB;
+        // Scales constant along K (OP::kTileScales): copied once per tile, at
+        // its first block, into scale slot (tile index & 1) -- the next write
+        // of a slot (two tiles later) is issued after the barrier that ends
+        // the epilogue reading it when KB >= 2 -- instead of with every block.
+        const bool lean = OP::kTileScales && KB >= 2;
         // Both roles pass the same barriers: one per block (copies of block it
         // visible; nobody reads the stage block it + 2 overwrites) and the
         // epilogue's OP::kEpilogueBarriers after each tile's last block.
@@ -306,7 +315,7 @@ __device__ __forceinline__ void grouped_tiles(const typename OP::Args& a) {
 #pragma unroll
                         for (int mi = 0; mi < 4; ++mi) apply_scaled(acc, pb, mi);
                     }
-                    OP::epilogue(a, s, ct, stage, brow, acc);
+                    OP::epilogue(a, s, ct, lean ? ct & 1 : stage, brow, acc);
 #pragma unroll
                     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -321,7 +330,7 @@ __device__ __forceinline__ void grouped_tiles(const typename OP::Args& a) {
             int iss_t = 0, iss_kb = 0;
             auto issue_next = [&](int stage) {
                 if (iss_kb == 0) OP::plan(a, s, iss_t, cw, lane, KB, p);
-                issue_stage(s, p, iss_kb, stage, cw);
+                issue_stage(s, p, iss_kb, stage, cw, lean ? (iss_kb == 0 ? iss_t & 1 : -1) : stage);
                 if (++iss_kb == KB) {
                     iss_kb = 0;
                     ++iss_t;
@@ -338,7 +347,10 @@ __device__ __forceinline__ void grouped_tiles(const typename OP::Args& a) {
             for (int it = 0; it < n_it; ++it) {
                 // this wave's copies of block it have landed (block it + 1 may
                 // still be in flight)
-                if (it + 1 < n_it) wait_copies<kCopies>();
+                if (it + 1 < n_it) {
+                    if (lean && (it + 1) % KB != 0) wait_copies<kLeanCopies>();
+                    else wait_copies<kCopies>();
+                }
                 else wait_copies<0>();
                 lds_barrier();
                 if (it + 2 < n_it) issue_next(stage == 0 ? 2 : stage - 1);
@@ -369,6 +381,7 @@ template <bool PER_KB, int GU>
 struct GateUpOp {
     using Args = GroupedGateUpArgs;
     static constexpr int kScale = PER_KB ? 1 : 0;
+    static constexpr bool kTileScales = !PER_KB;  // per-row activation and per-channel weight scales
     __device__ static int col_tiles(const Args& a) { return a.w13.N / 2 / 128; }
     __device__ static int kblocks(const Args& a) { return a.w13.K / 128; }
     __device__ static void brow(int wave, int (&b)[4]) {
@@ -485,6 +498,7 @@ __global__ __launch_bounds__(kGThreads, 1) void fp8_grouped_gateup_kernel(Groupe
 struct DownOp {
     using Args = GroupedDownArgs;
     static constexpr int kScale = 2;  // hidden scales change every 128-column block: deferred scaling
+    static constexpr bool kTileScales = false;
     __device__ static int col_tiles(const Args& a) { return (a.w2.N + kTileN - 1) / kTileN; }
     __device__ static int kblocks(const Args& a) { return a.w2.K / 128; }
     __device__ static void brow(int wave, int (&b)[4]) {
