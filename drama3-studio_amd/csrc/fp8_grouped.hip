@@ -97,7 +97,10 @@ struct alignas(16) GemmLds {
     float rowx[kChunk][kGroupM];         // down: route weight of the row
     float amax[kGroupM][kMmaWaves];      // gate/up epilogue: per-wave row maxima of |h|
     union {
-        uint8_t hbuf[kGroupM * 128];     // gate/up epilogue: the FP8 hidden tile
+        struct {
+            uint8_t hbuf[kGroupM * 128];      // gate/up epilogue: the FP8 hidden tile
+            float rinv[kMmaWaves][kGroupM];   // gate/up epilogue: each wave's copy of 1 / row scale
+        };
         float xt[kMmaWaves][4][16][16];  // down epilogue: per-wave transposes of four 16x16 MFMA results
     };
 };
@@ -235,6 +238,25 @@ __device__ __forceinline__ void compute_block(const GemmLds& s, int stage, const
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) pb.rs[mi] = *(const v4f*)&s.rs[stage][mi][grp * 4];
     }
+}
+
+// Maxima over each 16-lane row of 16 values per lane (v[k]), scattered: lane
+// c of the row ends with the row-wide maximum of index c.  Four exchange steps
+// (partners differing in lane bit 3, 2, 1, 0), each halving the values a lane
+// keeps: it keeps the half its bit selects and sends the partner the other.
+__device__ __forceinline__ float row_max16_scatter(const float (&v)[16], int col) {
+    float a[8], b[4], c[2];
+    const bool h3 = col & 8, h2 = col & 4, h1 = col & 2, h0 = col & 1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        a[k] = fmaxf(h3 ? v[8 + k] : v[k], dpp_f32<kDppMirror>(h3 ? v[k] : v[8 + k]));
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        b[k] = fmaxf(h2 ? a[4 + k] : a[k], dpp_f32<kDppHalfMirror>(h2 ? a[k] : a[4 + k]));
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        c[k] = fmaxf(h1 ? b[2 + k] : b[k], dpp_f32<kDppXor2>(h1 ? b[k] : b[2 + k]));
+    return fmaxf(h0 ? c[1] : c[0], dpp_f32<kDppXor1>(h0 ? c[0] : c[1]));
 }
 
 template <int GU>
@@ -434,6 +456,7 @@ struct GateUpOp {
             sw[ni] = s.ws[stage][r / 64][r % 64];
         }
         float chk = 0.0f;  // stays 0 unless some h is inf / NaN
+        float rm[16];      // |h| maximum of the lane's two columns, row index 4 mi + i
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
             const v4f sxv = *(const v4f*)&s.rs[stage][mi][grp * 4];
@@ -451,21 +474,25 @@ struct GateUpOp {
                     h[mi][tt][i] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
                     chk = fmaf(h[mi][tt][i], 0.0f, chk);
                 }
-                // max |h| over the row's 16 lanes; every lane of the row stores the same value
-                s.amax[mi * 16 + grp * 4 + i][wave] = row_max(fmaxf(fabsf(h[mi][0][i]), fabsf(h[mi][1][i])));
+                rm[mi * 4 + i] = fmaxf(fabsf(h[mi][0][i]), fabsf(h[mi][1][i]));
             }
         }
+        // the wave's maximum of row index `col` over the 16 lanes of the row group
+        s.amax[(col / 4) * 16 + grp * 4 + col % 4][wave] = row_max16_scatter(rm, col);
         if (chk != 0.0f) raise_status(a.status, kNonFinite);
         lds_barrier();
+        {  // lane r: 1 / scale of tile row r, in this wave's own slots (read back by this wave only)
+            const v4f am = *(const v4f*)s.amax[lane];
+            s.rinv[wave][lane] = 1.0f / fp8_group_scale(fmaxf(fmaxf(am[0], am[1]), fmaxf(am[2], am[3])));
+        }
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
+            const v4f inv = *(const v4f*)&s.rinv[wave][mi * 16 + grp * 4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = mi * 16 + grp * 4 + i;
-                const v4f am = *(const v4f*)s.amax[r];
-                const float inv = 1.0f / fp8_group_scale(fmaxf(fmaxf(am[0], am[1]), fmaxf(am[2], am[3])));
-                const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_saturate(h[mi][0][i] * inv),
-                                                               fp8_saturate(h[mi][1][i] * inv), 0, false);
+                const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_saturate(h[mi][0][i] * inv[i]),
+                                                               fp8_saturate(h[mi][1][i] * inv[i]), 0, false);
                 *(uint16_t*)(s.hbuf + r * 128 + wave * 32 + 2 * col) = (uint16_t)pk;
             }
         }
