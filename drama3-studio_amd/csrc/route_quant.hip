@@ -83,7 +83,7 @@ void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stre
 
 // ------------------------------------------------------------------ router
 
-// Stand-alone router for many tokens: one wave per token (wave_route_token).
+// Stand-alone router for many tokens: one wave per token.
 __global__ __launch_bounds__(256) void route_topk_kernel(RouteArgs a) {
     const int lane = threadIdx.x % kWave;
     const int t = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
@@ -97,7 +97,10 @@ __global__ __launch_bounds__(256) void route_topk_kernel(RouteArgs a) {
     }
     int id;
     float w;
-    wave_route_token(l, a.experts, a.top_k, a.renormalize, id, w);
+    // the same bits either way: the in-register sorting network for up to
+    // 2 * 64 experts and top-8, else k argmax rounds
+    if (a.experts <= 2 * kWave && a.top_k <= 8) wave_route_small(l, a.experts, a.top_k, a.renormalize, id, w);
+    else wave_route_token(l, a.experts, a.top_k, a.renormalize, id, w);
     if (lane < a.top_k) {
         a.ids[(int64_t)t * a.top_k + lane] = id;
         store_from_f32(a.weights, (int64_t)t * a.top_k + lane, a.w_dtype, w);
