@@ -1,7 +1,7 @@
 """CPU oracle for the quantized MoE expert path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker.  The product
+``bench.py`` may import this package, and only to check results.  The product
 (``drama3-studio_amd/drama_moe``) never imports it.
 
 Contents

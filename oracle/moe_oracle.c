@@ -1,5 +1,5 @@
 /*
- * moe_oracle.c -- TEST INFRASTRUCTURE ONLY (the checker, never the product).
+ * moe_oracle.c -- TEST INFRASTRUCTURE ONLY (it checks results; never the product).
  *
  * A scalar CPU restatement of the reference's quantized MoE expert arithmetic.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load

@@ -402,7 +402,7 @@ def test_hipgraph_replays_match_eager(cuda):
 
 @pytest.mark.parametrize("tokens", [1, 16])
 def test_full_size_layer_against_oracle(cuda, tokens):
-    """BASELINE decode shape: E=128, H=2048, I=768, top-8, per-channel FP8."""
+    """The benchmark decode layer: E=128, H=2048, I=768, top-8, per-channel FP8."""
     print_case("full-size layer", tokens)
     staged, x, ids, weights, expected = _layer_case(cuda, 128, 2048, 768, tokens, 8, "channel",
                                                     torch.bfloat16, 20261201 + 2, bank_on_device=True)
