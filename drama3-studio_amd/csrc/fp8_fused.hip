@@ -452,7 +452,9 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     // barrier, then one thread per (unit, row, column) sums the eight waves in
     // order, rounds gate / up, applies SiLU and publishes h with the epoch.
     uint32_t epoch = 0;  // read from LDS after the first gate/up barrier
-    auto unit_batch = [&](int j0) {
+    // prefetch: the batch's last pass issues the next batch's loads as soon
+    // as its MFMAs have read the operands, ahead of the reduction and publish.
+    auto unit_batch = [&](int j0, bool prefetch) {
         // unit coordinates once per wave (uniform), and for the reducing threads in LDS
         int uc0[kUnitDepth], ust[kUnitDepth], um[kUnitDepth];
         int passes = 0;
@@ -504,6 +506,10 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s.v.red[d][wave][lane][r] = acc[r];
             }
+            if (prefetch && pass == passes - 1) {
+#pragma unroll
+                for (int d = 0; d < kUnitDepth; ++d) load_unit(j0 + kUnitDepth + d, d);
+            }
             lds_barrier();
             epoch = s.epoch;
             {
@@ -535,12 +541,8 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         if (passes > 0) run_pass(0);
         for (int pass = 1; pass < passes; ++pass) run_pass(pass);
     };
-    unit_batch(0);
-    for (int j0 = kUnitDepth; j0 < my_units; j0 += kUnitDepth) {
-#pragma unroll
-        for (int d = 0; d < kUnitDepth; ++d) load_unit(j0 + d, d);
-        unit_batch(j0);
-    }
+    unit_batch(0, kUnitDepth < my_units);
+    for (int j0 = kUnitDepth; j0 < my_units; j0 += kUnitDepth) unit_batch(j0, j0 + kUnitDepth < my_units);
     // The first down job's rows go out only now, and only from waves that
     // have a job: the gate/up rows get the memory system to themselves, and
     // these stream during the hidden hand-off, which they are not needed
