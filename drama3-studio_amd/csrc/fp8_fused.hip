@@ -577,8 +577,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     // Column 8 a + b of a group is stored at word 16 b + a, so word j of
     // lane `col` (column 8 col + j) sits at 16 j + col: every load of the 16
     // lanes reads 128 contiguous bytes, and each lane ends with its 8
-    // consecutive columns (one producer unit).  Poll the first word, then read
-    // the rest, re-reading any word that still carries an older epoch.
+    // consecutive columns (one producer unit).
     constexpr int kHUnits = kFzThreads / 16;
     for (int u0 = 0; u0 < P * KBd; u0 += 2 * kHUnits) {
         uint64_t w[2][8];
@@ -593,31 +592,24 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         auto ok = [&](uint64_t word) { return (uint32_t)(word >> 32) == epoch; };
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         bool timed_out = false;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) w[q][0] = want[q] ? load_coherent_u64(hsrc[q]) : ((uint64_t)epoch << 32);
-        while (!(ok(w[0][0]) && ok(w[1][0])) && !timed_out) {
-            __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-                if (!ok(w[q][0])) w[q][0] = load_coherent_u64(hsrc[q]);
-            timed_out = __builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks;
-        }
+        // all 16 words at once (one round trip when the producers are done),
+        // then re-read only the words that still carry an older epoch
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int j = 1; j < 8; ++j) w[q][j] = want[q] ? load_coherent_u64(hsrc[q] + 16 * j) : ((uint64_t)epoch << 32);
+            for (int j = 0; j < 8; ++j) w[q][j] = want[q] ? load_coherent_u64(hsrc[q] + 16 * j) : ((uint64_t)epoch << 32);
         bool ready = true;
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int j = 1; j < 8; ++j) ready = ready && ok(w[q][j]);
+            for (int j = 0; j < 8; ++j) ready = ready && ok(w[q][j]);
         while (!ready && !timed_out) {
             __builtin_amdgcn_s_sleep(1);
             ready = true;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
 #pragma unroll
-                for (int j = 1; j < 8; ++j) {
+                for (int j = 0; j < 8; ++j) {
                     if (!ok(w[q][j])) w[q][j] = load_coherent_u64(hsrc[q] + 16 * j);
                     ready = ready && ok(w[q][j]);
                 }
