@@ -183,17 +183,19 @@ def test_small_call_launches_match_separate_launches(cuda, small_launches, mode,
 
 
 @pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("inter,tokens,top_k", [(768, 1, 8), (768, 2, 8)])
-def test_small_call_wide_gateup_workgroups(cuda, small_launches, mode, inter, tokens, top_k):
+@pytest.mark.parametrize("inter,tokens,top_k,x_dtype", [(768, 1, 8, torch.bfloat16), (768, 2, 8, torch.bfloat16),
+                                                        (768, 1, 8, torch.float16)])
+def test_small_call_wide_gateup_workgroups(cuda, small_launches, mode, inter, tokens, top_k, x_dtype):
     """Expert widths divisible by 24 whose 16-column gate/up workgroups would
     outnumber the CUs take 24-column workgroups (a third MFMA tile holding
     gate and up columns 16-23): bit-identical to the separate launches for
-    modes 1-3, within the bar for mode 0, and against the oracle."""
-    print_case("quant wide gate/up", mode, inter, tokens, top_k)
+    modes 1-3, within the bar for mode 0, and against the oracle; bf16 and
+    fp16 activations."""
+    print_case("quant wide gate/up", mode, inter, tokens, top_k, x_dtype)
     g = torch.Generator().manual_seed(1700 + 16 * mode + tokens)
     store = random_quantized_bank(mode, 32, 512, inter, generator=g)
     dev = to_device(store, cuda)
-    x = torch.randn(tokens, 512, generator=g).bfloat16()
+    x = torch.randn(tokens, 512, generator=g).to(x_dtype)
     ids, w = orc.route_topk(torch.randn(tokens, 32, generator=g).numpy(), top_k)
     weights = torch.from_numpy(w).bfloat16()
     backend = quantized.QuantizedExpertBackend(mode)
@@ -206,7 +208,8 @@ def test_small_call_wide_gateup_workgroups(cuda, small_launches, mode, inter, to
         assert torch.equal(outs[True], outs[False])
     else:
         assert rel_inf(outs[True].float().cpu().numpy(), outs[False].float().cpu().numpy()) < TOL
-    expected = oracle_layer(store, x.float().numpy(), ids, weights.float().numpy())
+    expected = oracle_layer(store, x.float().numpy(), ids, weights.float().numpy(),
+                            "fp16" if x_dtype == torch.float16 else "bf16")
     assert rel_inf(outs[True].float().cpu().numpy(), expected) < TOL
 
 
