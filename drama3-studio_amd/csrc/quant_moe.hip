@@ -466,7 +466,7 @@ __global__ __launch_bounds__(kQThreads) void quant_proj_kernel(QuantProjArgs a) 
 
 // Calls of at most 64 route pairs group their pairs inside every workgroup
 // instead of a permutation launch: one wave holds pair p in lane p and ranks
-// by cross-lane reads -- the distinct valid experts ascending (active), each
+// with ballots -- the distinct valid experts ascending (active), each
 // with its pairs ascending (plist[start[u] .. start[u + 1])), the order of
 // the stable permutation.
 struct SmallGroups {
