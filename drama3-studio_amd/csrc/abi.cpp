@@ -836,13 +836,26 @@ int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
         check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
         const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
                                       ids_out, weights_out, weights_dtype};
-        if (pairs > dmoe::kMaxDecodePairs) {  // the prefill path routes in its own launch first
+        Activations call_a = a;
+        if (pairs > dmoe::kMaxDecodePairs) {
+            // the prefill path routes first, in one launch with the activation
+            // quantization into the call's workspace (the two are independent)
+            const size_t need = prefill_workspace_layout(pairs, g.experts, g.H, g.I, nullptr, nullptr);
+            require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+            require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+            PrefillWorkspace pw{};
+            prefill_workspace_layout(pairs, g.experts, g.H, g.I, static_cast<char*>(workspace), &pw);
             const dmoe::RouteArgs ra{logits, logits_row_stride, tokens, g.experts, top_k, renormalize != 0,
                                      ids_out, weights_out, weights_dtype};
-            dmoe::launch_route_topk(ra, as_stream(stream));
+            const dmoe::QuantArgs qa{x, x_dtype, x_row_stride, tokens, g.H, a.x_group, 0, pw.xq, pw.xs, status};
+            dmoe::launch_route_quantize(ra, qa, as_stream(stream));
+            call_a.xq = pw.xq;
+            call_a.xs = pw.xs;
+            call_a.xq_row_stride = g.H;
+            call_a.xs_row_stride = g.H / a.x_group;
         }
-        fp8_call(g, a, route, ids_out, DMOE_I64, weights_out, weights_dtype, pairs, top_k, gu_dtype, out, out_dtype,
-                 out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
+        fp8_call(g, call_a, route, ids_out, DMOE_I64, weights_out, weights_dtype, pairs, top_k, gu_dtype, out,
+                 out_dtype, out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
     });
 }
 

@@ -256,6 +256,7 @@ void launch_fp8_down_decode(const DownArgs& a, hipStream_t stream);
 void launch_fp8_quantize(const QuantArgs& a, hipStream_t stream);
 void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stream);
 void launch_route_topk(const RouteArgs& a, hipStream_t stream);
+void launch_route_quantize(const RouteArgs& r, const QuantArgs& q, hipStream_t stream);
 void launch_permute(const PermuteArgs& a, hipStream_t stream);
 size_t permute_scratch_bytes(int64_t pairs, int experts);
 void launch_fp8_grouped_gateup(const GroupedGateUpArgs& a, hipStream_t stream);

@@ -83,10 +83,10 @@ void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stre
 
 // ------------------------------------------------------------------ router
 
-// Stand-alone router for many tokens: one wave per token.
-__global__ __launch_bounds__(256) void route_topk_kernel(RouteArgs a) {
+// Stand-alone router for many tokens: one wave per token, four per block.
+__device__ __forceinline__ void route_tokens(const RouteArgs& a, int block) {
     const int lane = threadIdx.x % kWave;
-    const int t = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    const int t = block * (256 / kWave) + threadIdx.x / kWave;
     if (t >= a.tokens) return;  // whole waves
     const float* row = a.logits + (int64_t)t * a.row_stride;
     float l[kRouteLaneSlots];
@@ -107,8 +107,29 @@ __global__ __launch_bounds__(256) void route_topk_kernel(RouteArgs a) {
     }
 }
 
+__global__ __launch_bounds__(256) void route_topk_kernel(RouteArgs a) { route_tokens(a, blockIdx.x); }
+
 void launch_route_topk(const RouteArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((a.tokens + 3) / 4)), dim3(256), 0, stream, a);
+}
+
+// The router and the activation quantization of one prefill call, independent
+// of each other, in one launch: blocks [0, route_blocks) route, the rest
+// quantize (the work of fp8_quantize_kernel's block b = blockIdx - route_blocks).
+__global__ __launch_bounds__(256) void route_quantize_kernel(RouteArgs r, QuantArgs q, int route_blocks) {
+    if ((int)blockIdx.x < route_blocks) {
+        route_tokens(r, blockIdx.x);
+        return;
+    }
+    const int b = blockIdx.x - route_blocks;  // block-uniform: the quantizer's barriers see whole blocks
+    if (q.group == 128) quantize_unit128(q, (int64_t)b * 16 + threadIdx.x / 16);
+    else quantize_row(q, b);
+}
+
+void launch_route_quantize(const RouteArgs& r, const QuantArgs& q, hipStream_t stream) {
+    const int route_blocks = (r.tokens + 3) / 4;
+    hipLaunchKernelGGL(route_quantize_kernel, dim3((unsigned)(route_blocks + quantize_blocks(q))), dim3(256), 0,
+                       stream, r, q, route_blocks);
 }
 
 // ------------------------------------------------------------- decode prep
