@@ -156,6 +156,11 @@ def run_gpu(steps: int, warmup: int):
     # The graph holds one fp8_fused_decode_kernel launch per step and nothing
     # else, so the per-step time is that kernel's average launch duration.
     us_per_step, total_ms = decode_graph_us(backend, xs, logits, banks, outs, stream, steps, warmup)
+    # the status word of every timed step: a bounded wait that gave up
+    # (SYNC_TIMEOUT) or a bad route would make the timing meaningless
+    status = backend.status(device)
+    if status:
+        raise RuntimeError(f"decode steps raised device status bits {status:#x}")
     alg_bytes, uniq = step_bytes(logits, 1)
     fused_out = outs.clone()
     lib.dmoe_set_fused_decode(0)
@@ -165,12 +170,15 @@ def run_gpu(steps: int, warmup: int):
         lib.dmoe_set_fused_decode(1)
     same = bool(torch.equal(outs, fused_out))
     multi = {}
-    for tokens in (4, 8):
+    for tokens in (4, 8, 16):
         mx, ml, mo = decode_inputs(tokens, device, SEED + tokens)
         t_us, _ = decode_graph_us(backend, mx, ml, banks, mo, stream, min(steps, 1024), warmup)
         mbytes, muniq = step_bytes(ml, tokens)
         multi[f"tokens_{tokens}"] = {"us": round(t_us, 2), "unique_experts_mean": round(muniq, 2),
                                      "hbm_frac": round(mbytes / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    status = backend.status(device)
+    if status:
+        raise RuntimeError(f"decode steps raised device status bits {status:#x}")
     return {
         "us_per_step": us_per_step, "total_ms": total_ms, "alg_bytes_step": alg_bytes,
         "step_gbs": alg_bytes / (us_per_step * 1e-6) / 1e9, "unique_experts_mean": uniq,

@@ -12,6 +12,7 @@
 #include <string>
 
 #include "kernels.hpp"
+#include "layout.hpp"
 
 namespace {
 
@@ -47,10 +48,22 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 std::atomic<int> g_fused_decode{1};
 bool fused_enabled() { return g_fused_decode.load(std::memory_order_relaxed) != 0; }
 
+// Bound of the single-launch decode's hand-off wait, in ticks of the 100 MHz
+// real-time counter (dmoe_set_sync_spin_limit); 200 ms by default.
+constexpr uint64_t kDefaultSpinTicks = 20000000;
+std::atomic<uint64_t> g_spin_ticks{kDefaultSpinTicks};
+
+// tokens * top_k in 64 bits, checked against the per-call pair limit before
+// it is narrowed (a wrapped product could look like a small valid count).
+int checked_pairs(int tokens, int top_k) {
+    const int64_t pairs = (int64_t)tokens * top_k;
+    require(pairs >= 1, "at least one route pair is required");
+    require(pairs <= dmoe::kMaxPermutePairs, "more than 1048576 route pairs (tokens * top_k) per call: split the rows");
+    return (int)pairs;
+}
+
 bool is_float_dtype(int d) { return d == DMOE_F32 || d == DMOE_BF16 || d == DMOE_F16; }
 bool is_id_dtype(int d) { return d == DMOE_I32 || d == DMOE_I64; }
-
-size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 dmoe::Fp8Proj to_kernel(const DmoeFp8Proj& p) {
     require(p.weight && p.scale, "FP8 projection weight and scale pointers are required");
@@ -97,52 +110,13 @@ BankGeom check_bank(const DmoeFp8Bank* bank) {
     return g;
 }
 
-struct Fp8Workspace {
-    int* counters;
-    int* sync;
-    dmoe::Grouping* grouping;
-    uint8_t* xq;
-    float* xs;
-    float* h32;
-    uint64_t* ht;
-    uint8_t* hq;
-    float* hs;
-};
+using Fp8Workspace = dmoe::DecodeWorkspace;
 
-// Workspace: the arrival counters come first at a fixed size, so one
-// zero-filled workspace serves calls of any pair count and bank geometry;
-// the grouping and the per-call buffers follow.  The counter region ends with
-// the two grid counters of the fused decode.
-constexpr size_t kArrivalBytes = (size_t)dmoe::kMaxDecodePairs * (dmoe::kMaxInter / 128) * 4;
-constexpr size_t kCounterBytes = kArrivalBytes + 32 * 256;
-
-size_t fp8_workspace_layout(int pairs, int H, int I, char* base, Fp8Workspace* ws) {
-    size_t off = 0;
-    auto take = [&](size_t n) {
-        const size_t o = off;
-        off = align256(off + n);
-        return base ? base + o : nullptr;
-    };
-    char* counters = take(kCounterBytes);
-    char* grouping = take(sizeof(dmoe::Grouping));
-    char* xq = take((size_t)pairs * H);
-    char* xs = take((size_t)pairs * (H / 128) * 4);
-    char* h32 = take((size_t)pairs * I * 4);
-    char* ht = take(pairs <= dmoe::kFusedMaxPairs ? (size_t)pairs * I * 8 : 0);
-    char* hq = take((size_t)pairs * I);
-    char* hs = take((size_t)pairs * (I / 128) * 4);
-    if (ws) {
-        ws->counters = reinterpret_cast<int*>(counters);
-        ws->sync = reinterpret_cast<int*>(counters + kArrivalBytes);
-        ws->grouping = reinterpret_cast<dmoe::Grouping*>(grouping);
-        ws->xq = reinterpret_cast<uint8_t*>(xq);
-        ws->xs = reinterpret_cast<float*>(xs);
-        ws->h32 = reinterpret_cast<float*>(h32);
-        ws->ht = reinterpret_cast<uint64_t*>(ht);
-        ws->hq = reinterpret_cast<uint8_t*>(hq);
-        ws->hs = reinterpret_cast<float*>(hs);
-    }
-    return off;
+size_t fp8_workspace_layout(int pairs, int H, int I, void* base, Fp8Workspace* ws) {
+    dmoe::Carver c(base);
+    const Fp8Workspace w = dmoe::decode_layout(c, pairs, H, I);
+    if (ws) *ws = w;
+    return c.size();
 }
 
 struct Activations {
@@ -225,7 +199,7 @@ void launch_gate_up(const BankGeom& g, const Activations& a, int pairs, int gu_d
     ga.quantize_hidden = quantize_hidden;
     ga.hq = hq;
     ga.hs = hs;
-    ga.counters = ws.counters;
+    ga.counters = ws.head.arrival;
     ga.status = status;
     dmoe::launch_fp8_gateup_decode(ga, std::min(pairs, g.experts), stream);
 }
@@ -260,7 +234,7 @@ Fp8Workspace take_workspace(const BankGeom& g, int pairs, void* workspace, size_
     require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
     require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
     Fp8Workspace ws{};
-    fp8_workspace_layout(pairs, g.H, g.I, static_cast<char*>(workspace), &ws);
+    fp8_workspace_layout(pairs, g.H, g.I, workspace, &ws);
     return ws;
 }
 
@@ -311,13 +285,14 @@ bool fp8_fused_call(const BankGeom& g, const Activations& a, const dmoe::RouteSo
     fa.rows = rows;
     fa.x_group = a.x_group;
     fa.gu_dtype = gu_dtype;
-    fa.ht = ws.ht;
-    fa.sync = ws.sync;
+    fa.ht = ws.head.handoff;
+    fa.sync = ws.head.epochs;
     fa.out = out;
     fa.out_dtype = out_dtype;
     fa.out_row_stride = out_row_stride;
     fa.out_pairs = out_pairs;
     fa.status = status;
+    fa.spin_ticks = g_spin_ticks.load(std::memory_order_relaxed);
     return dmoe::launch_fp8_fused_decode(fa, stream);
 }
 
@@ -338,62 +313,16 @@ void fp8_decode_call(const BankGeom& g, Activations a, const dmoe::RouteSource& 
                 out_pairs, status, stream, in_down ? ws.h32 : nullptr);
 }
 
-// Workspace of the grouped (prefill) path: the moe_align map, FP8 activations
-// (one row per pair at most), the FP8 hidden in sorted order and the fp32
-// partials of every pair.  It starts with the same reserved counter region as
-// the decode layout and never writes it, so one workspace serves both paths
-// and the decode arrival counters stay zero.
-struct PrefillWorkspace {
-    int32_t* permute_scratch;
-    int32_t* order;
-    int32_t* counts;
-    int32_t* offsets;
-    int32_t* tile_expert;
-    int32_t* tile_m0;
-    int32_t* tile_count;
-    uint8_t* xq;
-    float* xs;
-    uint8_t* hq;
-    float* hs;
-    float* partial;
-};
+// Workspace of the grouped (prefill) path (dmoe::prefill_layout): it starts
+// with the same head as the decode layout and never writes it, so one
+// workspace serves both paths.
+using dmoe::PrefillWorkspace;
 
-size_t prefill_workspace_layout(int pairs, int experts, int H, int I, char* base, PrefillWorkspace* ws) {
-    size_t off = 0;
-    auto take = [&](size_t n) {
-        const size_t o = off;
-        off = align256(off + n);
-        return base ? base + o : nullptr;
-    };
-    const int tiles = dmoe::max_block_tiles(pairs, experts, dmoe::kGroupM);
-    take(kCounterBytes);  // decode arrival counters: reserved, untouched here
-    char* scratch = take(dmoe::permute_scratch_bytes(pairs, experts));
-    char* order = take((size_t)pairs * 4);
-    char* counts = take((size_t)experts * 4);
-    char* offsets = take((size_t)(experts + 1) * 4);
-    char* tile_expert = take((size_t)tiles * 4);
-    char* tile_m0 = take((size_t)tiles * 4);
-    char* tile_count = take(4);
-    char* xq = take((size_t)pairs * H);
-    char* xs = take((size_t)pairs * (H / 128) * 4);
-    char* hq = take((size_t)pairs * I);
-    char* hs = take((size_t)pairs * (I / 128) * 4);
-    char* partial = take((size_t)pairs * H * 4);
-    if (ws) {
-        ws->permute_scratch = reinterpret_cast<int32_t*>(scratch);
-        ws->order = reinterpret_cast<int32_t*>(order);
-        ws->counts = reinterpret_cast<int32_t*>(counts);
-        ws->offsets = reinterpret_cast<int32_t*>(offsets);
-        ws->tile_expert = reinterpret_cast<int32_t*>(tile_expert);
-        ws->tile_m0 = reinterpret_cast<int32_t*>(tile_m0);
-        ws->tile_count = reinterpret_cast<int32_t*>(tile_count);
-        ws->xq = reinterpret_cast<uint8_t*>(xq);
-        ws->xs = reinterpret_cast<float*>(xs);
-        ws->hq = reinterpret_cast<uint8_t*>(hq);
-        ws->hs = reinterpret_cast<float*>(hs);
-        ws->partial = reinterpret_cast<float*>(partial);
-    }
-    return off;
+size_t prefill_workspace_layout(int pairs, int experts, int H, int I, void* base, PrefillWorkspace* ws) {
+    dmoe::Carver c(base);
+    const PrefillWorkspace w = dmoe::prefill_layout(c, pairs, experts, H, I);
+    if (ws) *ws = w;
+    return c.size();
 }
 
 size_t workspace_bytes_for(const BankGeom& g, int pairs) {
@@ -415,7 +344,7 @@ void fp8_prefill_call(const BankGeom& g, Activations a, const void* ids, int ids
     require((int64_t)g.w13.N * g.w13.w_sn < (int64_t(1) << 32) && (int64_t)g.w2.N * g.w2.w_sn < (int64_t(1) << 32),
             "grouped path: rows x row stride of one expert must stay below 4 GiB");
     PrefillWorkspace ws{};
-    prefill_workspace_layout(pairs, g.experts, g.H, g.I, static_cast<char*>(workspace), &ws);
+    prefill_workspace_layout(pairs, g.experts, g.H, g.I, workspace, &ws);
     const int tiles = dmoe::max_block_tiles(pairs, g.experts, dmoe::kGroupM);
 
     dmoe::PermuteArgs pa{ids, ids_dtype, pairs, g.experts, ws.order, ws.counts, ws.offsets, status,
@@ -529,53 +458,13 @@ dmoe::QuantProjArgs check_quant_proj(const DmoeQuantProj& p, int mode, int exper
     return q;
 }
 
-struct QuantWorkspace {
-    int32_t* permute_scratch;
-    int32_t* order;
-    int32_t* counts;
-    int32_t* offsets;
-    int32_t* active;
-    int8_t* xq;
-    float* xs;
-    uint16_t* act;
-    int8_t* actq;
-    float* acts;
-    float* partial;
-};
+using dmoe::QuantWorkspace;
 
-size_t quant_workspace_layout(int rows, int pairs, int experts, int H, int I, char* base, QuantWorkspace* ws) {
-    size_t off = 0;
-    auto take = [&](size_t n) {
-        const size_t o = off;
-        off = align256(off + n);
-        return base ? base + o : nullptr;
-    };
-    take(kCounterBytes);  // decode arrival counters: reserved, untouched here
-    char* scratch = take(dmoe::permute_scratch_bytes(pairs, experts));
-    char* order = take((size_t)pairs * 4);
-    char* counts = take((size_t)experts * 4);
-    char* offsets = take((size_t)(experts + 1) * 4);
-    char* active = take((size_t)(experts + 1) * 4);
-    char* xq = take((size_t)rows * H);
-    char* xs = take((size_t)rows * 4);
-    char* act = take((size_t)pairs * I * 2);
-    char* actq = take((size_t)pairs * I);
-    char* acts = take((size_t)pairs * 4);
-    char* partial = take((size_t)pairs * H * 4);
-    if (ws) {
-        ws->permute_scratch = reinterpret_cast<int32_t*>(scratch);
-        ws->order = reinterpret_cast<int32_t*>(order);
-        ws->counts = reinterpret_cast<int32_t*>(counts);
-        ws->offsets = reinterpret_cast<int32_t*>(offsets);
-        ws->active = reinterpret_cast<int32_t*>(active);
-        ws->xq = reinterpret_cast<int8_t*>(xq);
-        ws->xs = reinterpret_cast<float*>(xs);
-        ws->act = reinterpret_cast<uint16_t*>(act);
-        ws->actq = reinterpret_cast<int8_t*>(actq);
-        ws->acts = reinterpret_cast<float*>(acts);
-        ws->partial = reinterpret_cast<float*>(partial);
-    }
-    return off;
+size_t quant_workspace_layout(int rows, int pairs, int experts, int H, int I, void* base, QuantWorkspace* ws) {
+    dmoe::Carver c(base);
+    const QuantWorkspace w = dmoe::quant_layout(c, rows, pairs, experts, H, I);
+    if (ws) *ws = w;
+    return c.size();
 }
 
 QuantWorkspace take_quant_workspace(int rows, int pairs, int experts, int H, int I, void* workspace,
@@ -584,7 +473,7 @@ QuantWorkspace take_quant_workspace(int rows, int pairs, int experts, int H, int
     require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
     require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
     QuantWorkspace ws{};
-    quant_workspace_layout(rows, pairs, experts, H, I, static_cast<char*>(workspace), &ws);
+    quant_workspace_layout(rows, pairs, experts, H, I, workspace, &ws);
     return ws;
 }
 
@@ -634,6 +523,8 @@ extern "C" {
 int dmoe_abi_version(void) { return DMOE_ABI_VERSION; }
 
 int dmoe_set_fused_decode(int enabled) { return g_fused_decode.exchange(enabled != 0 ? 1 : 0); }
+
+uint64_t dmoe_set_sync_spin_limit(uint64_t ticks) { return g_spin_ticks.exchange(ticks); }
 
 const char* dmoe_last_error(void) { return g_last_error.c_str(); }
 
@@ -725,7 +616,7 @@ int dmoe_fp8_moe_forward(const DmoeFp8Bank* bank, const void* x, int x_dtype, in
     return checked([&] {
         const BankGeom g = check_bank(bank);
         require(tokens >= 1 && top_k >= 1 && top_k <= g.experts, "bad token count or top_k");
-        const int pairs = tokens * top_k;
+        const int pairs = checked_pairs(tokens, top_k);
         const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, x_group};
         check_activations(g, a, pairs);
         check_routes(ids, ids_dtype, weights, weights_dtype);
@@ -829,7 +720,7 @@ int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
         require(tokens >= 1 && top_k >= 1 && top_k <= g.experts && top_k <= 64, "bad token count or top_k");
         require(logits != nullptr && logits_row_stride >= g.experts, "router logits [tokens, experts] required");
         require(ids_out && weights_out && is_float_dtype(weights_dtype), "routing outputs are required");
-        const int pairs = tokens * top_k;
+        const int pairs = checked_pairs(tokens, top_k);
         const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, x_group};
         check_activations(g, a, pairs);
         check_gu_dtype(gu_dtype);
@@ -844,7 +735,7 @@ int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
             require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
             require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
             PrefillWorkspace pw{};
-            prefill_workspace_layout(pairs, g.experts, g.H, g.I, static_cast<char*>(workspace), &pw);
+            prefill_workspace_layout(pairs, g.experts, g.H, g.I, workspace, &pw);
             const dmoe::RouteArgs ra{logits, logits_row_stride, tokens, g.experts, top_k, renormalize != 0,
                                      ids_out, weights_out, weights_dtype};
             const dmoe::QuantArgs qa{x, x_dtype, x_row_stride, tokens, g.H, a.x_group, 0, pw.xq, pw.xs, status};

@@ -39,7 +39,8 @@
 // exchange (calls on one workspace never overlap).  The host launches at most
 // as many workgroups as the device holds at once, so a waiting lane never
 // keeps a producer from a CU; every wait is bounded anyway (kSyncTimeout
-// status bit) so every wave exits.
+// status bit, after a.spin_ticks of the 100 MHz real-time counter) so every
+// wave exits.
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -47,6 +48,7 @@
 #include "common.hpp"
 #include "fp8_util.hpp"
 #include "kernels.hpp"
+#include "layout.hpp"
 #include "route.hpp"
 
 namespace dmoe {
@@ -58,9 +60,6 @@ constexpr int kUnitCols = 8;    // output columns of one gate/up unit
 constexpr int kTileRows = 8;    // hidden rows of one down tile
 constexpr int kMaxUnitDepth = 4;
 constexpr int kQuantPerGroup = kFusedXBytes / 128 / (kFzThreads / 16);  // (row, group) units per 16 lanes
-constexpr int kEpochSlots = 32;      // call counters, spread over memory channels
-constexpr int kEpochStride = 256;    // bytes between two call counters
-constexpr uint64_t kSpinTicks = 20000000;  // 200 ms of the 100 MHz real-time counter
 
 // Calls with at most this many (token, expert) logits rank them with every
 // thread of the workgroup (at least two threads per logit); larger ones route
@@ -614,7 +613,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                     ready = ready && ok(w[q][j]);
                 }
             }
-            timed_out = __builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks;
+            timed_out = __builtin_amdgcn_s_memrealtime() - t0 > a.spin_ticks;
         }
         if (timed_out) raise_status(a.status, kSyncTimeout);
 #pragma unroll

@@ -5,14 +5,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "limits.hpp"
+
 namespace dmoe {
 
-constexpr int kMaxExperts = 512;      // routed experts per bank
-constexpr int kExpertBits = 9;        // bits of an expert index
-static_assert((1 << kExpertBits) >= kMaxExperts, "expert index bits");
-constexpr int kMaxDecodePairs = 256;  // tokens * top_k handled by the decode kernels
-constexpr int kMaxHidden = 8192;
-constexpr int kMaxInter = 4096;
 // Hidden-activation bytes (pairs * I) the down kernel quantizes itself in LDS
 // for small decode calls; larger calls quantize in the gate/up kernel.
 constexpr int kDownQuantBytes = 8192;  // 64 (pair, 128-group) units: 4 passes of 16
@@ -45,15 +41,6 @@ struct RouteSource {
     int w_dtype;
 };
 
-// Expert grouping of the route pairs of one decode call, written once by the
-// prep kernel and read by both decode kernels: the ascending active experts
-// and, per active expert, a bitmask of its pairs (pair p <-> bit p).
-struct Grouping {
-    int num_active;
-    int pad[3];
-    int expert[kMaxExperts];
-    uint32_t mask[kMaxExperts][kMaxDecodePairs / 32];
-};
 
 struct GateUpArgs {
     Fp8Proj w13;
@@ -94,8 +81,6 @@ struct DownArgs {
     int* status;
 };
 
-constexpr int kMaxPermutePairs = 1 << 20;  // route pairs of one permutation / grouped call
-constexpr int kPermuteBlock = 256;         // pairs per block of the permutation kernels
 constexpr int kSmallPermute = 1024;        // pairs permuted by a single workgroup
 constexpr int kRouteElems = 1024;   // logits one workgroup ranks at a time (tokens * experts)
 constexpr int kRouteTokens = 8;     // tokens one workgroup routes at a time
@@ -146,13 +131,10 @@ struct PermuteArgs {
     int32_t* tile_count;    // optional: number of valid tiles
 };
 
-// Tile-map capacity for `pairs` route pairs over `experts` experts.
-inline int max_block_tiles(int pairs, int experts, int block_m) { return (pairs + block_m - 1) / block_m + experts; }
 
 // Grouped (prefill) FP8 GEMMs over the moe_align tile map: 64 sorted pairs
 // per tile.  Gate/up writes the FP8 hidden of every sorted position; down
 // writes route-weighted fp32 partials by original pair index.
-constexpr int kGroupM = 64;
 
 struct GroupedGateUpArgs {
     Fp8Proj w13;
@@ -213,12 +195,10 @@ struct PrepArgs {
 // Single-launch decode (fp8_fused.hip): routing, activation quantization,
 // gate/up + SiLU, hidden quantization, down * route weight and the slot-order
 // combine in one persistent launch of at most one workgroup per CU.
-constexpr int kFusedMaxPairs = 64;     // route pairs of one fused call
 constexpr int kFusedXBytes = 16384;    // FP8 activation rows (rows * H) a workgroup stages
 constexpr int kFusedRawBytes = 32768;  // the same rows as given (bf16 / fp16 / fp32)
 constexpr int kFusedHBytes = 49152;    // FP8 hidden (pairs * I) a workgroup stages
 constexpr int kFusedMaxH = 2048;
-constexpr int kFusedMaxI = 1024;
 
 struct FusedDecodeArgs {
     Fp8Proj w13, w2;
@@ -242,6 +222,7 @@ struct FusedDecodeArgs {
     int64_t out_row_stride;
     float* out_pairs;           // ... or [pairs, H] ordered fp32 partials when non-null
     int* status;
+    uint64_t spin_ticks;        // bound of the hand-off wait (100 MHz ticks) before kSyncTimeout
 };
 
 bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize, int routed_tokens);
@@ -258,7 +239,6 @@ void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stre
 void launch_route_topk(const RouteArgs& a, hipStream_t stream);
 void launch_route_quantize(const RouteArgs& r, const QuantArgs& q, hipStream_t stream);
 void launch_permute(const PermuteArgs& a, hipStream_t stream);
-size_t permute_scratch_bytes(int64_t pairs, int experts);
 void launch_fp8_grouped_gateup(const GroupedGateUpArgs& a, hipStream_t stream);
 void launch_fp8_grouped_down(const GroupedDownArgs& a, hipStream_t stream);
 void launch_combine(const CombineArgs& a, hipStream_t stream);

@@ -467,11 +467,6 @@ __global__ __launch_bounds__(kPermuteBlock) void permute_scatter_kernel(PermuteA
     a.order[a.hist[(int64_t)blockIdx.x * a.experts + e] + r] = (int32_t)i;
 }
 
-size_t permute_scratch_bytes(int64_t pairs, int experts) {
-    const int64_t blocks = (pairs + kPermuteBlock - 1) / kPermuteBlock;
-    return (size_t)(pairs + blocks * experts) * 4;
-}
-
 void launch_permute(const PermuteArgs& a, hipStream_t stream) {
     if (a.pairs <= kSmallPermute) {
         hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(1024), 0, stream, a);

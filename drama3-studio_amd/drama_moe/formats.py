@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
+from typing import Callable
 
 import torch
 
@@ -27,6 +28,57 @@ EXPERT_BUFFER_NAMES = ("w13_weight", "w13_scale_inv", "w2_weight", "w2_scale_inv
 def select_fp8(weight: torch.Tensor, index) -> torch.Tensor:
     """Select FP8 entries through their bytes (offload.py:39-41)."""
     return weight.view(torch.uint8)[index].view(weight.dtype)
+
+
+# ------------------------------------------------------------- bank geometry
+
+@dataclass(frozen=True)
+class ProjectionFormat:
+    """How one projection [E, N, K] of a bank format is stored: the weight
+    element type and its packed column count (a function of K), the scale
+    element type and the trailing scale shapes allowed for (N, K)."""
+
+    weight_dtype: torch.dtype
+    weight_columns: Callable[[int], int]
+    scale_dtype: torch.dtype
+    scale_shapes: Callable[[int, int], tuple]
+
+
+# FP8 (the reference's StagedExperts, offload.py:175-184) and the packed
+# modes 0-3 of QuantizedStore (quantized_model.py:26-68): 128x128 block or
+# per-channel scales; GPTQ int32 words with fp16 group scales; INT8 rows with
+# a channel scale; 6-bit (nibble + 2-bit planes) and 4-bit codebook codes
+# with E4M3 group-16 scale bytes followed by the fp32 channel scale (and, in
+# mode 3, the codebook).
+BANK_FORMATS: dict = {
+    "fp8": ProjectionFormat(FP8_DTYPE, lambda k: k, torch.float32,
+                            lambda n, k: ((n // FP8_BLOCK_SIZE, k // FP8_BLOCK_SIZE), (n, 1))),
+    0: ProjectionFormat(torch.int32, lambda k: k // 8, torch.float16, lambda n, k: ((n, k // 128),)),
+    1: ProjectionFormat(torch.int8, lambda k: k, torch.float32, lambda n, k: ((n, 1),)),
+    2: ProjectionFormat(torch.int8, lambda k: 3 * k // 4, torch.uint8, lambda n, k: ((n, k // 16 + 4),)),
+    3: ProjectionFormat(torch.int8, lambda k: k // 2, torch.uint8, lambda n, k: ((n, k // 16 + 8),)),
+}
+
+
+def check_bank_buffers(fmt, buffers: dict, experts: int, hidden: int, inter: int) -> None:
+    """Check the four buffers of a bank of format ``fmt`` against the
+    geometry (E, H, I): w13 holds [E, 2I, H] and w2 [E, H, I] in that
+    format's storage.  Raises ValueError naming the first buffer whose element
+    type or shape differs, or when the buffers span several devices."""
+    spec = BANK_FORMATS[fmt]
+    for prefix, n, k in (("w13", 2 * inter, hidden), ("w2", hidden, inter)):
+        wanted = ((f"{prefix}_weight", spec.weight_dtype, ((experts, n, spec.weight_columns(k)),)),
+                  (f"{prefix}_scale_inv", spec.scale_dtype,
+                   tuple((experts, *shape) for shape in spec.scale_shapes(n, k))))
+        for name, dtype, shapes in wanted:
+            tensor = buffers[name]
+            if tensor.dtype != dtype:
+                raise ValueError(f"{name} must be {dtype}; got {tensor.dtype}")
+            if tuple(tensor.shape) not in shapes:
+                raise ValueError(f"{name} has shape {tuple(tensor.shape)}; expected "
+                                 + " or ".join(str(s) for s in shapes))
+    if len({t.device for t in buffers.values()}) != 1:
+        raise ValueError("Expert bank tensors must share one device")
 
 
 @dataclass(frozen=True)
@@ -62,31 +114,18 @@ class StagedExperts:
         return sum(getattr(self, n).numel() * getattr(self, n).element_size()
                    for n in EXPERT_BUFFER_NAMES)
 
+    def buffers(self) -> dict:
+        return {name: getattr(self, name) for name in EXPERT_BUFFER_NAMES}
+
     def validate(self) -> None:
-        for name in EXPERT_BUFFER_NAMES:
-            tensor = getattr(self, name)
-            expected = FP8_DTYPE if name.endswith("_weight") else torch.float32
-            if tensor.dtype != expected:
-                raise ValueError(f"{name} must be {expected}; got {tensor.dtype}")
-            if tensor.ndim != 3:
-                raise ValueError(f"{name} must be a stacked three-dimensional tensor")
-        experts, gate_up, hidden = self.w13_weight.shape
-        if experts < 1 or gate_up % 2:
-            raise ValueError("Expert bank needs at least one expert and even gate/up rows")
-        inter = gate_up // 2
-        if hidden % FP8_BLOCK_SIZE or inter % FP8_BLOCK_SIZE:
-            raise ValueError("Expert dimensions must be divisible by the FP8 block size")
-        if tuple(self.w2_weight.shape) != (experts, hidden, inter):
-            raise ValueError(f"w2_weight has shape {tuple(self.w2_weight.shape)}, "
-                             f"expected {(experts, hidden, inter)}")
-        for name, rows, cols in (("w13_scale_inv", gate_up, hidden), ("w2_scale_inv", hidden, inter)):
-            shape = tuple(getattr(self, name).shape)
-            if shape not in ((experts, rows // 128, cols // 128), (experts, rows, 1)):
-                raise ValueError(f"{name} has shape {shape}; expected 128x128 blocks "
-                                 f"{(experts, rows // 128, cols // 128)} or per-channel {(experts, rows, 1)}")
-        devices = {getattr(self, n).device for n in EXPERT_BUFFER_NAMES}
-        if len(devices) != 1:
-            raise ValueError("Expert bank tensors must share one device")
+        w13 = self.w13_weight
+        if w13.ndim != 3:
+            raise ValueError("w13_weight must be a stacked [experts, 2 * intermediate, hidden] tensor")
+        experts, gate_up, hidden = w13.shape
+        if experts < 1 or gate_up % 2 or hidden % FP8_BLOCK_SIZE or (gate_up // 2) % FP8_BLOCK_SIZE:
+            raise ValueError("FP8 banks need at least one expert, and hidden and intermediate sizes "
+                             "that are multiples of the FP8 block size")
+        check_bank_buffers("fp8", self.buffers(), experts, hidden, gate_up // 2)
 
     @property
     def device(self) -> torch.device:
@@ -227,33 +266,24 @@ class QuantizedStore:
                 total += z.numel() * z.element_size()
         return total
 
+    def buffers(self) -> dict:
+        return {name: getattr(self, name) for name in EXPERT_BUFFER_NAMES}
+
     def validate(self) -> None:
         if self.mode not in (0, 1, 2, 3):
             raise ValueError("Unknown quantized bank format")
-        for name in EXPERT_BUFFER_NAMES:
-            value = getattr(self, name)
-            if value.ndim != 3 or value.shape[0] != self.num_experts:
-                raise ValueError(f"Quantized bank must be three-dimensional per expert: {name}")
-        for bank, scales, n, k in ((self.w13_weight, self.w13_scale_inv, 2 * self.intermediate, self.hidden),
-                                   (self.w2_weight, self.w2_scale_inv, self.hidden, self.intermediate)):
-            columns = (k // 8 if self.mode == 0 else k if self.mode == 1 else
-                       k * 3 // 4 if self.mode == 2 else k // 2)
-            scale_columns = (k // 128 if self.mode == 0 else 1 if self.mode == 1 else
-                             k // 16 + (8 if self.mode == 3 else 4))
-            if tuple(bank.shape[1:]) != (n, columns) or tuple(scales.shape[1:]) != (n, scale_columns):
-                raise ValueError("Quantized weight/scale geometry mismatch")
-            if bank.dtype != (torch.int32 if self.mode == 0 else torch.int8):
-                raise ValueError("Quantized weight dtype mismatch")
-            if scales.dtype != (torch.float16 if self.mode == 0 else
-                                torch.float32 if self.mode == 1 else torch.uint8):
-                raise ValueError("Quantized scale dtype mismatch")
-        if self.mode != 0 and (self.w13_zeros is not None or self.w2_zeros is not None):
-            raise ValueError("Zero points apply to W4A16 banks only")
-        for zeros, n, k in ((self.w13_zeros, 2 * self.intermediate, self.hidden),
-                            (self.w2_zeros, self.hidden, self.intermediate)):
-            if zeros is not None and (zeros.dtype != torch.int32 or
-                                      tuple(zeros.shape) != (self.num_experts, k // 128, n // 8)):
-                raise ValueError("W4A16 zero points must be GPTQ qzeros [E, K/128, N/8] int32")
+        if self.w13_weight.ndim != 3:
+            raise ValueError("Quantized banks are stacked [experts, rows, columns] tensors")
+        check_bank_buffers(self.mode, self.buffers(), self.num_experts, self.hidden, self.intermediate)
+        zero_points = {"w13_zeros": (self.w13_zeros, 2 * self.intermediate, self.hidden),
+                       "w2_zeros": (self.w2_zeros, self.hidden, self.intermediate)}
+        for name, (zeros, n, k) in zero_points.items():
+            if zeros is None:
+                continue
+            if self.mode != 0:
+                raise ValueError("Zero points apply to W4A16 banks only")
+            if zeros.dtype != torch.int32 or tuple(zeros.shape) != (self.num_experts, k // 128, n // 8):
+                raise ValueError(f"{name} must be GPTQ qzeros [E, K/128, N/8] int32")
 
 
 def random_quantized_bank(mode: int, experts: int, hidden: int, inter: int, *,

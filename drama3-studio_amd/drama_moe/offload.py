@@ -17,8 +17,6 @@ the host; bad expert ids are reported through a device status word
 """
 from __future__ import annotations
 
-import types
-
 import torch
 from torch import Tensor, nn
 
@@ -30,17 +28,49 @@ MAX_PAIRS = 65536   # route pairs of one call (above DECODE_PAIRS: grouped GEMMs
 
 
 class _DeviceState:
-    """Per-device zero-initialised workspace and status word."""
+    """Per-device workspace and status word of the HIP backends.
+
+    The workspace is zero-filled once when allocated and reused by every call
+    on the device (the C ABI keeps what must stay zero at zero).  Growth
+    allocates a larger zeroed buffer and RETIRES the old one instead of
+    freeing it: a hipGraph captured earlier keeps the old pointer, and its
+    replays must still find live memory there.  Growth while a stream is
+    being captured is refused (the allocation would belong to the graph's
+    private pool): run the call once eagerly, or ``reserve`` first.
+
+    Calls on the device share the buffer, so they are ordered: a call on a
+    stream other than the previous call's first waits for that stream (outside
+    capture; replays of captured graphs must be ordered by the caller).
+    """
 
     def __init__(self, device: torch.device):
         self.device = device
         self.workspace = torch.zeros(0, dtype=torch.uint8, device=device)
+        self.retired: list[Tensor] = []
         self.status = torch.zeros(1, dtype=torch.int32, device=device)
+        self._last_stream = None
+
+    def reserve(self, nbytes: int) -> Tensor:
+        if self.workspace.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    f"the expert workspace must grow to {nbytes} bytes inside a graph capture; run this "
+                    "call once eagerly (or reserve the workspace) before capturing")
+            size = max(nbytes, 2 * self.workspace.numel(), 1 << 20)
+            grown = torch.zeros(size, dtype=torch.uint8, device=self.device)
+            if self.workspace.numel():
+                self.retired.append(self.workspace)
+            self.workspace = grown
+        return self.workspace
 
     def workspace_for(self, nbytes: int) -> Tensor:
-        if self.workspace.numel() < nbytes:
-            self.workspace = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
-        return self.workspace
+        ws = self.reserve(nbytes)
+        stream = torch.cuda.current_stream(self.device)
+        last = self._last_stream
+        if last is not None and last != stream and not torch.cuda.is_current_stream_capturing():
+            stream.wait_stream(last)
+        self._last_stream = stream
+        return ws
 
 
 _STATES: dict[torch.device, _DeviceState] = {}
@@ -227,23 +257,85 @@ class HipExpertBackend:
         return out
 
 
-def store_from_module(module: nn.Module) -> StagedExperts:
-    """The four FP8 buffers of an expert module (offload.py:107-118)."""
+def store_from_module(module: nn.Module):
+    """The resident bank of an expert module: the packed store a quantized
+    loader bound to it (``_drama_quant_store``, quantized_model.py:106-111),
+    else a StagedExperts over its four FP8 buffers (offload.py:107-118)."""
+    packed = getattr(module, "_drama_quant_store", None)
+    if packed is not None:
+        packed.validate()
+        return packed
     if not getattr(module, "fp8", False):
         raise ValueError("Expert offload requires FP8 buffers, not dense BF16 weights")
-    store = StagedExperts(**{name: getattr(module, name) for name in EXPERT_BUFFER_NAMES})
-    store.validate()
-    return store
+    bank = StagedExperts(**{name: getattr(module, name) for name in EXPERT_BUFFER_NAMES})
+    bank.validate()
+    return bank
+
+
+_COMPUTE_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def check_route_call(x: Tensor, ids: Tensor, weights: Tensor, hidden: int) -> None:
+    """The caller contract of one expert call, checked before any work:
+    x [tokens, hidden] in a compute dtype, ids [tokens, top_k >= 1] int32 or
+    int64, floating-point weights of the same shape, one device for all."""
+    rules = (
+        (x.ndim == 2 and x.shape[-1] == hidden,
+         lambda: f"Expected hidden rows [N, {hidden}], got {tuple(x.shape)}"),
+        (ids.ndim == 2 and ids.shape[0] == x.shape[0] and ids.shape[1] >= 1,
+         lambda: "Expert IDs must be [tokens, top_k] with top_k >= 1"),
+        (tuple(weights.shape) == tuple(ids.shape), lambda: "Routing weights must have the shape of the expert IDs"),
+        (ids.dtype in (torch.int32, torch.int64), lambda: "Expert IDs must be int32 or int64"),
+        (weights.is_floating_point(), lambda: "Routing weights must be floating point"),
+        (x.dtype in _COMPUTE_DTYPES, lambda: "Expert compute dtype must be float16, bfloat16 or float32"),
+        (ids.device == x.device and weights.device == x.device,
+         lambda: "Hidden states, expert IDs and routing weights must share a device"),
+    )
+    for ok, message in rules:
+        if not ok:
+            raise ValueError(message())
+
+
+def check_id_range(ids: Tensor, experts: int) -> None:
+    """Eager range check of route ids (one host sync)."""
+    low, high = (int(v) for v in torch.aminmax(ids))
+    if low < 0 or high >= experts:
+        raise ValueError(f"Expert IDs must be in [0, {experts})")
+
+
+class _RoutedForward:
+    """Forward of an attached expert module: hands ``(x, topk_ids,
+    topk_weights)`` to the manager.  ``shadowed`` is the instance-level forward
+    it replaced (None when the module used its class's forward), so detaching
+    restores exactly what was there."""
+
+    def __init__(self, manager: "ResidentExpertManager", module: nn.Module):
+        self.manager = manager
+        self.module = module
+        self.shadowed = module.__dict__.get("forward")
+
+    def __call__(self, x: Tensor, topk_ids: Tensor, topk_weights: Tensor) -> Tensor:
+        return self.manager.forward(self.module, x, topk_ids, topk_weights)
+
+
+def _attached(module: nn.Module) -> bool:
+    # ours (a _RoutedForward instance) or the reference manager's marker
+    return isinstance(module.__dict__.get("forward"), _RoutedForward) or hasattr(
+        module, "_drama_offload_original_forward")
 
 
 class ResidentExpertManager:
     """Routes ``experts(x, topk_ids, topk_weights)`` of attached modules to a
-    backend with the whole bank resident (the caller contract of
-    ExpertOffloadManager.forward, offload.py:1016-1063).
+    backend with the whole bank resident in HBM -- the caller contract of
+    ExpertOffloadManager.attach / forward (offload.py:996-1063) without its
+    staging tiers.
 
-    ``validate_ids=True`` keeps the reference's eager check that ids lie in
-    [0, E) before any expert runs (one host sync per call); ``False`` leaves it
-    to the device status word so a call can be captured in a hipGraph.
+    Banks are resolved once per module and reused while the module keeps the
+    same buffers.  FP8 banks run on ``backend`` (default HipExpertBackend);
+    packed banks bound by a quantized loader on a QuantizedExpertBackend of
+    their mode.  ``validate_ids=True`` keeps the reference's eager range check
+    of the ids (one host sync per call); ``False`` leaves bad ids to the
+    device status word so calls can be captured in hipGraphs.
     """
 
     def __init__(self, *, backend=None, validate_ids: bool = True) -> None:
@@ -251,73 +343,99 @@ class ResidentExpertManager:
         self.validate_ids = validate_ids
         self.modules: dict[str, nn.Module] = {}
         self.forward_calls = 0
+        self._banks: dict[int, tuple] = {}
+        self._packed_backends: dict[int, object] = {}
         self._closed = False
 
-    def attach(self, name: str, module: nn.Module) -> None:
+    def _require_open(self) -> None:
         if self._closed:
             raise RuntimeError("This expert manager has been closed")
-        if hasattr(module, "_drama_offload_original_forward") or name in self.modules:
+
+    def _bank_of(self, module: nn.Module):
+        key = tuple(id(getattr(module, name, None)) for name in EXPERT_BUFFER_NAMES) + (
+            id(getattr(module, "_drama_quant_store", None)),)
+        cached = self._banks.get(id(module))
+        if cached is None or cached[0] != key:
+            cached = (key, store_from_module(module))
+            self._banks[id(module)] = cached
+        return cached[1]
+
+    def _backend_for(self, bank):
+        if isinstance(bank, StagedExperts):
+            return self.backend
+        backend = self._packed_backends.get(bank.mode)
+        if backend is None:
+            from .quantized import QuantizedExpertBackend
+
+            backend = self._packed_backends[bank.mode] = QuantizedExpertBackend(bank.mode)
+        return backend
+
+    def attach(self, name: str, module: nn.Module) -> None:
+        self._require_open()
+        if name in self.modules or _attached(module):
             raise ValueError(f"Expert module {name!r} already has an offload manager")
-        store_from_module(module)
-        module._drama_offload_original_forward = module.forward
-        manager = self
-
-        def forward(experts: nn.Module, x: Tensor, topk_ids: Tensor, topk_weights: Tensor) -> Tensor:
-            return manager.forward(experts, x, topk_ids, topk_weights)
-
-        module.forward = types.MethodType(forward, module)
+        self._bank_of(module)
+        module.forward = _RoutedForward(self, module)
         self.modules[name] = module
 
     @torch.no_grad()
     def forward(self, module: nn.Module, x: Tensor, topk_ids: Tensor, topk_weights: Tensor) -> Tensor:
-        if self._closed:
-            raise RuntimeError("This expert manager has been closed")
-        store = store_from_module(module)
-        if x.ndim != 2 or x.shape[-1] != store.hidden:
-            raise ValueError(f"Expected hidden rows [N, {store.hidden}], got {tuple(x.shape)}")
-        if topk_ids.ndim != 2 or topk_ids.shape[0] != x.shape[0]:
-            raise ValueError("Expert IDs must have shape [tokens, top_k]")
-        if topk_weights.shape != topk_ids.shape or topk_ids.shape[1] < 1:
-            raise ValueError("Routing weights must match IDs and top_k must be positive")
-        if topk_ids.dtype not in (torch.int32, torch.int64):
-            raise ValueError("Expert IDs must have an integer dtype")
-        if topk_ids.device != x.device or topk_weights.device != x.device:
-            raise ValueError("Hidden states, expert IDs and routing weights must share a device")
-        if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            raise ValueError("Expert compute dtype must be float16, bfloat16 or float32")
-        if not topk_weights.is_floating_point():
-            raise ValueError("Routing weights must be floating point")
+        self._require_open()
+        bank = self._bank_of(module)
+        check_route_call(x, topk_ids, topk_weights, bank.hidden)
         self.forward_calls += 1
         if x.shape[0] == 0:
             return torch.zeros_like(x)
         if self.validate_ids:
-            low, high = int(topk_ids.min()), int(topk_ids.max())
-            if low < 0 or high >= store.count:
-                raise ValueError(f"Expert IDs must be in [0, {store.count})")
-        return self.backend.forward(x, topk_ids, topk_weights, store)
+            check_id_range(topk_ids, bank.count)
+        return self._backend_for(bank).forward(x, topk_ids, topk_weights, bank)
 
     def close(self) -> None:
         for module in self.modules.values():
-            original = module.__dict__.pop("_drama_offload_original_forward", None)
-            if original is not None:
-                module.forward = original
+            routed = module.__dict__.get("forward")
+            if isinstance(routed, _RoutedForward):
+                if routed.shadowed is None:
+                    del module.forward  # the class's forward shows through again
+                else:
+                    module.forward = routed.shadowed
         self.modules.clear()
+        self._banks.clear()
         self._closed = True
 
 
+# Keywords of the reference's install_expert_offload (offload.py:1534-1546)
+# that configure its host staging tiers; with every expert resident they have
+# nothing to configure and are accepted for call-site compatibility.
+STAGING_KEYWORDS = frozenset({"max_staged_experts", "max_pair_rows", "cache_experts", "hot_cache_experts",
+                              "pin_memory", "profile_transfers", "combined_decode_bank", "packed_staging"})
+
+
 def install_expert_offload(backbone: nn.Module, *, backend=None, validate_ids: bool = True,
-                           **_ignored) -> ResidentExpertManager:
-    """Attach a resident manager to every FP8 expert module (offload.py:1534).
-    Staging / cache keywords of the reference are accepted and ignored: every
-    expert is HBM-resident."""
+                           **staging) -> ResidentExpertManager:
+    """Attach a resident manager to every routed expert module of a backbone
+    (modules holding w13_weight and w2_weight, offload.py:1479-1484, 1534).
+    ``backend`` is a backend object, or "hip" / "triton" (both mean the gfx950
+    FP8 backend).  Every bank is checked before any forward is replaced."""
+    unknown = set(staging) - STAGING_KEYWORDS
+    if unknown:
+        raise TypeError(f"install_expert_offload() got unexpected keywords {sorted(unknown)}")
+    if isinstance(backend, str):
+        if backend not in ("hip", "triton"):
+            raise ValueError(f"Unknown expert backend {backend!r}: this build provides 'hip'")
+        backend = HipExpertBackend()
+    targets = [(name, module) for name, module in backbone.named_modules()
+               if hasattr(module, "w13_weight") and hasattr(module, "w2_weight")]
+    if not targets:
+        raise ValueError("Backbone contains no routed expert modules")
+    for name, module in targets:
+        store_from_module(module)
+        if _attached(module):
+            raise ValueError("Backbone already has an expert offload manager")
     manager = ResidentExpertManager(backend=backend, validate_ids=validate_ids)
-    for name, module in backbone.named_modules():
-        if getattr(module, "fp8", False) and all(hasattr(module, n) for n in EXPERT_BUFFER_NAMES):
-            manager.attach(name, module)
-    if not manager.modules:
-        raise ValueError("No FP8 expert modules found")
+    for name, module in targets:
+        manager.attach(name, module)
     return manager
 
 
-__all__ = ["HipExpertBackend", "ResidentExpertManager", "install_expert_offload",
+__all__ = ["HipExpertBackend", "ResidentExpertManager", "install_expert_offload", "check_route_call",
            "store_from_module", "StagedExperts", "FP8_DTYPE", "DECODE_PAIRS"]

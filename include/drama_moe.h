@@ -13,9 +13,13 @@
  *     library never synchronizes the host, so every entry point may be
  *     captured in a hipGraph;
  *   - no entry point allocates device memory; scratch comes from the caller's
- *     `workspace` (size from the matching *_workspace_bytes query), which must
- *     be zero-filled once when first allocated -- the library leaves its
- *     counter region zeroed after every call;
+ *     `workspace` (size from the matching *_workspace_bytes query).  A
+ *     workspace is zero-filled AS A WHOLE once, when it is allocated, and
+ *     never partially afterwards: its head holds arrival counters the decode
+ *     kernels return to zero, call counters that only grow and hand-off words
+ *     tagged with the call's epoch.  Re-zeroing only the counters would restart
+ *     the epochs while old tagged words remain, and a later call could take
+ *     such a word for its own;
  *   - `status` (optional, may be NULL) is a device int the kernels OR their
  *     DMOE_STATUS_* bits into, so a caller can check data errors (bad expert
  *     ids, non-finite activations) without a per-call host sync.
@@ -77,7 +81,8 @@ DMOE_API int dmoe_abi_version(void);
  * hand-off inside; 0 selects the three-launch decode for every call (A/B
  * measurement).  Returns the previous setting.  The fused launch occupies
  * every CU and waits on its own workgroups: work on other streams of the
- * same device delays it, and a wait that exceeds 200 ms gives up with
+ * same device delays it, and a wait that exceeds the bound of
+ * dmoe_set_sync_spin_limit (200 ms by default) gives up with
  * DMOE_STATUS_SYNC_TIMEOUT.  The same switch selects, for packed banks, the
  * single launch that quantizes the hidden rows, projects down and combines
  * small calls (at most 64 pairs; 16 for the INT8 modes); 0 keeps the
@@ -85,6 +90,15 @@ DMOE_API int dmoe_abi_version(void);
  * reference (its decode is per-route-slot Triton launches,
  * fp8_decode.py:114-147). */
 DMOE_API int dmoe_set_fused_decode(int enabled);
+
+/* Process-wide bound of the single-launch decode's hand-off wait, in ticks
+ * of the GPU's 100 MHz real-time counter (default 20,000,000 = 200 ms).  A
+ * wait that exceeds it gives up: the call sets DMOE_STATUS_SYNC_TIMEOUT in
+ * the status word, its outputs are invalid, and every workgroup still exits.
+ * 0 gives up at the first re-read of a word that is not ready (lets a test
+ * drive the timeout path from the host).  Returns the previous bound.  No
+ * counterpart in the reference. */
+DMOE_API uint64_t dmoe_set_sync_spin_limit(uint64_t ticks);
 
 /* Last error message of the calling thread.  Replaces drama_native_error
  * (native/include/drama_native.h:19; runtime.cpp:290). */
@@ -133,10 +147,10 @@ DMOE_API int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts
                           int* status, void* stream);
 
 /* Workspace bytes of an FP8 call over `pairs` route pairs (0 outside
- * [1, 2^20]).  A workspace is zero-filled once when allocated (256-byte
- * aligned) and reused by later calls of any size it covers: its leading
- * region holds arrival counters that the decode kernels return to zero.
- * Calls sharing one workspace must not overlap. */
+ * [1, 2^20]).  A workspace is 256-byte aligned, zero-filled as a whole once
+ * when allocated, and reused by later calls of any kind and size it covers
+ * (every layout begins with the same fixed head, which only the decode
+ * kernels write).  Calls sharing one workspace must not overlap. */
 DMOE_API size_t dmoe_fp8_workspace_bytes(const DmoeFp8Bank* bank, int pairs);
 
 /* Whole routed-expert call: x [tokens, H] (bf16/fp16/fp32, row stride in

@@ -79,6 +79,11 @@ def test_forward_rejects_small_workspace_and_oversized_calls():
     assert "workspace too small" in _lib.library().dmoe_last_error().decode()
     assert _forward(_bank(), tokens=600000, top_k=2) == -1
     assert "1048576 route pairs" in _lib.library().dmoe_last_error().decode()
+    # tokens * top_k = 2^32 + 64 would wrap to 64 pairs in 32-bit arithmetic
+    wide = _bank()
+    wide.experts = 64
+    assert _forward(wide, tokens=(1 << 26) + 1, top_k=64) == -1
+    assert "1048576 route pairs" in _lib.library().dmoe_last_error().decode()
 
 
 def test_workspace_query_grows_with_pairs():

@@ -141,8 +141,8 @@ def test_fused_invalid_ids_contribute_zero_and_raise_status(cuda, decode_mode):
 
 def test_fused_repeated_calls_rearm_the_grid_counters(cuda):
     """Hundreds of back-to-back single-launch calls (eager and graph-replayed)
-    stay identical: the grid counters return to zero after every call and no
-    wait times out."""
+    stay identical: each call derives its own epoch from the call counters,
+    never accepts an older call's hand-off words, and no wait times out."""
     print_case("fused repeated calls")
     g = torch.Generator().manual_seed(99)
     staged = to_device(random_fp8_bank(128, 2048, 768, layout="channel", generator=g), cuda)
@@ -167,4 +167,57 @@ def test_fused_repeated_calls_rearm_the_grid_counters(cuda):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, first)
+    assert backend.status(cuda) == 0
+
+
+def test_sync_timeout_is_reported_and_every_kernel_exits(cuda):
+    """With the hand-off wait bounded at zero ticks the single-launch decode
+    gives up at the first word that is not ready: the status word carries
+    DMOE_STATUS_SYNC_TIMEOUT and every launch still completes.  With the
+    default bound restored the next call is exact again."""
+    print_case("forced sync timeout")
+    lib = _lib.library()
+    g = torch.Generator().manual_seed(123)
+    staged = to_device(random_fp8_bank(128, 2048, 768, layout="channel", generator=g), cuda)
+    backend = HipExpertBackend()
+    x = torch.randn(1, 2048, generator=g).bfloat16().to(cuda)
+    logits = torch.randn(1, 128, generator=g).to(cuda)
+    expected, _, _ = backend.forward_routed(x, logits, 8, staged)
+    torch.cuda.synchronize()
+    assert backend.status(cuda) == 0
+    previous = lib.dmoe_set_sync_spin_limit(0)
+    try:
+        for _ in range(8):
+            backend.forward_routed(x, logits, 8, staged)
+        torch.cuda.synchronize()
+    finally:
+        lib.dmoe_set_sync_spin_limit(previous)
+    assert backend.status(cuda) & _lib.STATUS_SYNC_TIMEOUT
+    again, _, _ = backend.forward_routed(x, logits, 8, staged)
+    torch.cuda.synchronize()
+    assert backend.status(cuda) == 0
+    assert torch.equal(again, expected)
+
+
+def test_decode_after_prefill_on_one_workspace(cuda, decode_mode):
+    """A 2048-token grouped call and then a 1-token single-launch call on the
+    same per-device workspace: the grouped call's permutation and tile map
+    never reach the decode's hand-off words, so the decode equals the
+    three-launch decode bit for bit."""
+    print_case("decode after prefill, shared workspace")
+    g = torch.Generator().manual_seed(321)
+    staged = to_device(random_fp8_bank(128, 2048, 768, layout="channel", generator=g), cuda)
+    backend = HipExpertBackend()
+    xs = torch.randn(2048, 2048, generator=g).bfloat16().to(cuda)
+    big_logits = torch.randn(2048, 128, generator=g).to(cuda)
+    x = torch.randn(1, 2048, generator=g).bfloat16().to(cuda)
+    logits = torch.randn(1, 128, generator=g).to(cuda)
+
+    def run():
+        backend.forward_routed(xs, big_logits, 8, staged)
+        out, _, _ = backend.forward_routed(x, logits, 8, staged)
+        return out
+
+    fused, staged_out = both(decode_mode, run)
+    assert torch.equal(fused, staged_out)
     assert backend.status(cuda) == 0
