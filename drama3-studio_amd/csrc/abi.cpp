@@ -52,6 +52,9 @@ bool fused_enabled() { return g_fused_decode.load(std::memory_order_relaxed) != 
 // real-time counter (dmoe_set_sync_spin_limit); 200 ms by default.
 constexpr uint64_t kDefaultSpinTicks = 20000000;
 std::atomic<uint64_t> g_spin_ticks{kDefaultSpinTicks};
+// Diagnostic switch (dmoe_debug_force_sync_timeout): hand-off readers wait for
+// a tag no producer writes, so every wait runs to the bound.
+std::atomic<int> g_force_timeout{0};
 
 // tokens * top_k in 64 bits, checked against the per-call pair limit before
 // it is narrowed (a wrapped product could look like a small valid count).
@@ -293,6 +296,7 @@ bool fp8_fused_call(const BankGeom& g, const Activations& a, const dmoe::RouteSo
     fa.out_pairs = out_pairs;
     fa.status = status;
     fa.spin_ticks = g_spin_ticks.load(std::memory_order_relaxed);
+    fa.tag_skew = g_force_timeout.load(std::memory_order_relaxed) ? 1u : 0u;
     return dmoe::launch_fp8_fused_decode(fa, stream);
 }
 
@@ -516,6 +520,33 @@ void quant_operand(dmoe::QuantProjArgs& q, const void* x, int x_dtype, int64_t x
     }
 }
 
+// Router + routed experts of one layer (dmoe_fp8_moe_layer): the validated
+// call.
+struct LayerCall {
+    BankGeom g;
+    Activations a;
+    dmoe::RouteSource route;
+    int pairs;
+};
+
+LayerCall check_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride, int tokens,
+                      const float* logits, int64_t logits_row_stride, int top_k, int renormalize, int64_t* ids_out,
+                      void* weights_out, int weights_dtype, int x_group, int gu_dtype, void* out, int out_dtype,
+                      int64_t out_row_stride) {
+    const BankGeom g = check_bank(bank);
+    require(tokens >= 1 && top_k >= 1 && top_k <= g.experts && top_k <= 64, "bad token count or top_k");
+    require(logits != nullptr && logits_row_stride >= g.experts, "router logits [tokens, experts] required");
+    require(ids_out && weights_out && is_float_dtype(weights_dtype), "routing outputs are required");
+    const int pairs = checked_pairs(tokens, top_k);
+    const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, x_group};
+    check_activations(g, a, pairs);
+    check_gu_dtype(gu_dtype);
+    check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
+    const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
+                                  ids_out, weights_out, weights_dtype};
+    return LayerCall{g, a, route, pairs};
+}
+
 }  // namespace
 
 extern "C" {
@@ -525,6 +556,8 @@ int dmoe_abi_version(void) { return DMOE_ABI_VERSION; }
 int dmoe_set_fused_decode(int enabled) { return g_fused_decode.exchange(enabled != 0 ? 1 : 0); }
 
 uint64_t dmoe_set_sync_spin_limit(uint64_t ticks) { return g_spin_ticks.exchange(ticks); }
+
+int dmoe_debug_force_sync_timeout(int force) { return g_force_timeout.exchange(force != 0 ? 1 : 0); }
 
 const char* dmoe_last_error(void) { return g_last_error.c_str(); }
 
@@ -716,36 +749,29 @@ int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
                        int x_group, int gu_dtype, void* out, int out_dtype, int64_t out_row_stride,
                        void* workspace, size_t workspace_bytes, int* status, void* stream) {
     return checked([&] {
-        const BankGeom g = check_bank(bank);
-        require(tokens >= 1 && top_k >= 1 && top_k <= g.experts && top_k <= 64, "bad token count or top_k");
-        require(logits != nullptr && logits_row_stride >= g.experts, "router logits [tokens, experts] required");
-        require(ids_out && weights_out && is_float_dtype(weights_dtype), "routing outputs are required");
-        const int pairs = checked_pairs(tokens, top_k);
-        const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, x_group};
-        check_activations(g, a, pairs);
-        check_gu_dtype(gu_dtype);
-        check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
-        const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
-                                      ids_out, weights_out, weights_dtype};
-        Activations call_a = a;
-        if (pairs > dmoe::kMaxDecodePairs) {
+        const LayerCall c = check_layer(bank, x, x_dtype, x_row_stride, tokens, logits, logits_row_stride, top_k,
+                                        renormalize, ids_out, weights_out, weights_dtype, x_group, gu_dtype, out,
+                                        out_dtype, out_row_stride);
+        const BankGeom& g = c.g;
+        Activations call_a = c.a;
+        if (c.pairs > dmoe::kMaxDecodePairs) {
             // the prefill path routes first, in one launch with the activation
             // quantization into the call's workspace (the two are independent)
-            const size_t need = prefill_workspace_layout(pairs, g.experts, g.H, g.I, nullptr, nullptr);
+            const size_t need = prefill_workspace_layout(c.pairs, g.experts, g.H, g.I, nullptr, nullptr);
             require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
             require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
             PrefillWorkspace pw{};
-            prefill_workspace_layout(pairs, g.experts, g.H, g.I, workspace, &pw);
+            prefill_workspace_layout(c.pairs, g.experts, g.H, g.I, workspace, &pw);
             const dmoe::RouteArgs ra{logits, logits_row_stride, tokens, g.experts, top_k, renormalize != 0,
                                      ids_out, weights_out, weights_dtype};
-            const dmoe::QuantArgs qa{x, x_dtype, x_row_stride, tokens, g.H, a.x_group, 0, pw.xq, pw.xs, status};
+            const dmoe::QuantArgs qa{x, x_dtype, x_row_stride, tokens, g.H, c.a.x_group, 0, pw.xq, pw.xs, status};
             dmoe::launch_route_quantize(ra, qa, as_stream(stream));
             call_a.xq = pw.xq;
             call_a.xs = pw.xs;
             call_a.xq_row_stride = g.H;
-            call_a.xs_row_stride = g.H / a.x_group;
+            call_a.xs_row_stride = g.H / c.a.x_group;
         }
-        fp8_call(g, call_a, route, ids_out, DMOE_I64, weights_out, weights_dtype, pairs, top_k, gu_dtype, out,
+        fp8_call(g, call_a, c.route, ids_out, DMOE_I64, weights_out, weights_dtype, c.pairs, top_k, gu_dtype, out,
                  out_dtype, out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
     });
 }

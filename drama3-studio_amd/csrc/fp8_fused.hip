@@ -588,7 +588,10 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             want[q] = u < P * KBd && s.sid[min(u, P * KBd - 1) / KBd] >= 0;
             hsrc[q] = a.ht + (int64_t)(want[q] ? u / KBd : 0) * I + (want[q] ? u % KBd : 0) * 128 + col;
         }
-        auto ok = [&](uint64_t word) { return (uint32_t)(word >> 32) == epoch; };
+        // the tag a ready word carries: this call's epoch (tag_skew = 1 only in
+        // the diagnostic mode that forces every wait to run to its bound)
+        const uint32_t tag = epoch + a.tag_skew;
+        auto ok = [&](uint64_t word) { return (uint32_t)(word >> 32) == tag; };
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         bool timed_out = false;
         // all 16 words at once (one round trip when the producers are done),
@@ -596,7 +599,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) w[q][j] = want[q] ? load_coherent_u64(hsrc[q] + 16 * j) : ((uint64_t)epoch << 32);
+            for (int j = 0; j < 8; ++j) w[q][j] = want[q] ? load_coherent_u64(hsrc[q] + 16 * j) : ((uint64_t)tag << 32);
         bool ready = true;
 #pragma unroll
         for (int q = 0; q < 2; ++q)

@@ -223,6 +223,7 @@ struct FusedDecodeArgs {
     float* out_pairs;           // ... or [pairs, H] ordered fp32 partials when non-null
     int* status;
     uint64_t spin_ticks;        // bound of the hand-off wait (100 MHz ticks) before kSyncTimeout
+    uint32_t tag_skew;          // 0; 1 makes readers wait for a tag no producer writes (diagnostic)
 };
 
 bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize, int routed_tokens);

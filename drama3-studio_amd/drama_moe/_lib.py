@@ -53,6 +53,7 @@ _SIGNATURES = {
     "dmoe_abi_version": ([], _I),
     "dmoe_set_fused_decode": ([_I], _I),
     "dmoe_set_sync_spin_limit": ([ctypes.c_uint64], ctypes.c_uint64),
+    "dmoe_debug_force_sync_timeout": ([_I], _I),
     "dmoe_last_error": ([], ctypes.c_char_p),
     "dmoe_decode_fp8": ([_P, _P, _L, _P], _I),
     "dmoe_fp8_quantize": ([_P, _I, _L, _I, _I, _I, _P, _P, _P, _P], _I),

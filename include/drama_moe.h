@@ -95,10 +95,16 @@ DMOE_API int dmoe_set_fused_decode(int enabled);
  * of the GPU's 100 MHz real-time counter (default 20,000,000 = 200 ms).  A
  * wait that exceeds it gives up: the call sets DMOE_STATUS_SYNC_TIMEOUT in
  * the status word, its outputs are invalid, and every workgroup still exits.
- * 0 gives up at the first re-read of a word that is not ready (lets a test
- * drive the timeout path from the host).  Returns the previous bound.  No
- * counterpart in the reference. */
+ * Returns the previous bound.  No counterpart in the reference. */
 DMOE_API uint64_t dmoe_set_sync_spin_limit(uint64_t ticks);
+
+/* Diagnostic switch (default 0) for testing the timeout path from the host:
+ * while set, the single-launch decode's hand-off readers wait for a tag that
+ * no producer ever writes, so every wait runs to the spin bound and each call
+ * ends with DMOE_STATUS_SYNC_TIMEOUT and invalid outputs; every workgroup
+ * still exits.  Returns the previous setting.  No counterpart in the
+ * reference. */
+DMOE_API int dmoe_debug_force_sync_timeout(int force);
 
 /* Last error message of the calling thread.  Replaces drama_native_error
  * (native/include/drama_native.h:19; runtime.cpp:290). */

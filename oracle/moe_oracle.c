@@ -300,6 +300,40 @@ ORC_API int orc_permute(const int64_t* ids, int64_t pairs, int64_t experts, int3
     return 0;
 }
 
+/* Expert-sorted pair indices padded per expert to whole blocks of block_m
+ * rows: the layout moe_align(ids, E, block_m) hands to fused_moe_gemm
+ * (call sites offload.py:299-306 and hybrid_layer.py:39; the fish-speech
+ * fp8_moe module that computes it is not part of the reference, so this
+ * follows the published moe_align_block_size layout).  For each expert in
+ * ascending order: its pairs in ascending pair index, then the sentinel value
+ * `pairs` up to the next multiple of block_m; expert_ids[b] is the expert of
+ * block b and *padded the total padded row count.  Pairs whose id lies outside
+ * [0, experts) are left out.  Blocks past the last (up to cap_blocks) hold
+ * expert -1 and sentinel rows.  Brute force: one pass over the pairs per
+ * expert. */
+ORC_API int orc_moe_align(const int64_t* ids, int64_t pairs, int64_t experts, int64_t block_m,
+                          int64_t cap_blocks, int32_t* sorted_ids, int32_t* expert_ids, int32_t* padded) {
+    if (block_m < 1 || experts < 1) return -1;
+    for (int64_t i = 0; i < cap_blocks * block_m; ++i) sorted_ids[i] = (int32_t)pairs;
+    for (int64_t b = 0; b < cap_blocks; ++b) expert_ids[b] = -1;
+    int64_t block = 0;
+    for (int64_t e = 0; e < experts; ++e) {
+        int64_t rows = 0;
+        for (int64_t i = 0; i < pairs; ++i) {
+            if (ids[i] != e) continue;
+            if (block * block_m + rows >= cap_blocks * block_m) return -2;
+            sorted_ids[block * block_m + rows] = (int32_t)i;
+            ++rows;
+        }
+        const int64_t nb = (rows + block_m - 1) / block_m;
+        if (block + nb > cap_blocks) return -2;
+        for (int64_t b = 0; b < nb; ++b) expert_ids[block + b] = (int32_t)e;
+        block += nb;
+    }
+    *padded = (int32_t)(block * block_m);
+    return 0;
+}
+
 /* ------------------------------------------- packed quantized projections */
 
 /* Published H4 basis [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] and the

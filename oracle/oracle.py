@@ -47,7 +47,7 @@ def lib():
         _lib.orc_f32_from_f16.restype = ctypes.c_float
         _lib.orc_f32_from_f16.argtypes = [ctypes.c_uint16]
         for name in ("orc_quantize_fp8", "orc_fp8_expert_pairs", "orc_fp8_moe_forward",
-                     "orc_route_topk", "orc_permute", "orc_rotate_quantize",
+                     "orc_route_topk", "orc_permute", "orc_moe_align", "orc_rotate_quantize",
                      "orc_quant_projection", "orc_quant_dequantize"):
             getattr(_lib, name).restype = ctypes.c_int
     return _lib
@@ -182,6 +182,22 @@ def permute(ids, experts):
     _check(lib().orc_permute(_ptr(flat), ctypes.c_int64(flat.size), ctypes.c_int64(experts),
                              _ptr(order), _ptr(counts), _ptr(offsets)), "permute")
     return order, counts, offsets
+
+
+def moe_align(ids, experts, block_m):
+    """Block-padded expert-sorted pair indices (the moe_align layout of
+    offload.py:299-306): (sorted_ids int32 [cap * block_m], expert_ids int32
+    [cap], padded) with cap = ceil(pairs / block_m) + experts blocks; sentinel
+    = pairs, expert -1 past the last block; invalid ids left out."""
+    flat = np.ascontiguousarray(ids, np.int64).reshape(-1)
+    cap = (flat.size + block_m - 1) // block_m + experts
+    sorted_ids = np.empty(cap * block_m, np.int32)
+    expert_ids = np.empty(cap, np.int32)
+    padded = np.zeros(1, np.int32)
+    _check(lib().orc_moe_align(_ptr(flat), ctypes.c_int64(flat.size), ctypes.c_int64(experts),
+                               ctypes.c_int64(block_m), ctypes.c_int64(cap), _ptr(sorted_ids),
+                               _ptr(expert_ids), _ptr(padded)), "moe_align")
+    return sorted_ids, expert_ids, int(padded[0])
 
 
 # -------------------------------------------------- packed quantized modes

@@ -171,10 +171,11 @@ def test_fused_repeated_calls_rearm_the_grid_counters(cuda):
 
 
 def test_sync_timeout_is_reported_and_every_kernel_exits(cuda):
-    """With the hand-off wait bounded at zero ticks the single-launch decode
-    gives up at the first word that is not ready: the status word carries
-    DMOE_STATUS_SYNC_TIMEOUT and every launch still completes.  With the
-    default bound restored the next call is exact again."""
+    """The host forces the single-launch decode's bounded hand-off wait to
+    give up: with the diagnostic switch on, readers wait for a tag no producer
+    writes, so each wait runs to a 100 us bound.  The status word then carries
+    DMOE_STATUS_SYNC_TIMEOUT and every launch still completes; with the switch
+    off and the default bound restored the next call is exact again."""
     print_case("forced sync timeout")
     lib = _lib.library()
     g = torch.Generator().manual_seed(123)
@@ -185,12 +186,14 @@ def test_sync_timeout_is_reported_and_every_kernel_exits(cuda):
     expected, _, _ = backend.forward_routed(x, logits, 8, staged)
     torch.cuda.synchronize()
     assert backend.status(cuda) == 0
-    previous = lib.dmoe_set_sync_spin_limit(0)
+    previous = lib.dmoe_set_sync_spin_limit(10_000)  # 100 us of the 100 MHz counter
+    forced = lib.dmoe_debug_force_sync_timeout(1)
     try:
-        for _ in range(8):
+        for _ in range(2):
             backend.forward_routed(x, logits, 8, staged)
         torch.cuda.synchronize()
     finally:
+        lib.dmoe_debug_force_sync_timeout(forced)
         lib.dmoe_set_sync_spin_limit(previous)
     assert backend.status(cuda) & _lib.STATUS_SYNC_TIMEOUT
     again, _, _ = backend.forward_routed(x, logits, 8, staged)

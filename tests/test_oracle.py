@@ -421,3 +421,51 @@ def test_asymmetric_w4a16_zero_points():
     zp = zeros.permute(0, 2, 1).repeat_interleave(128, -1).float()  # [1, n, k]
     explicit = ((codes.float() - zp) * scales.float().repeat_interleave(128, -1)).bfloat16().float()
     np.testing.assert_array_equal(orc.quant_dequantize(bank, 0), explicit[0].numpy())
+
+
+# --------------------------------------------------------------- moe_align
+
+def test_moe_align_known_answer():
+    # ids flattened [2, 0, 2, 1, 0, 5] over 4 experts (5 is invalid), blocks of 2:
+    # expert 0 -> pairs 1, 4; expert 1 -> pair 3 + sentinel; expert 2 -> pairs 0, 2
+    sorted_ids, expert_ids, padded = orc.moe_align(np.array([[2, 0], [2, 1], [0, 5]]), 4, 2)
+    assert padded == 6
+    assert sorted_ids[:6].tolist() == [1, 4, 3, 6, 0, 2]
+    assert expert_ids.tolist()[:4] == [0, 1, 2, -1]
+    assert np.all(sorted_ids[6:] == 6)
+
+
+@pytest.mark.parametrize("pairs,experts,block_m", [(1, 1, 16), (37, 8, 4), (1000, 128, 16),
+                                                   (4096, 128, 64), (513, 7, 1), (300, 512, 32)])
+def test_moe_align_properties(pairs, experts, block_m):
+    from moe_align_props import check_moe_align
+
+    rng = np.random.default_rng(pairs + experts)
+    ids = rng.integers(0, experts, pairs)
+    if pairs > 10:
+        ids[rng.integers(0, pairs, 3)] = [-1, experts, experts + 9]
+    sorted_ids, expert_ids, padded = orc.moe_align(ids, experts, block_m)
+    check_moe_align(sorted_ids, expert_ids, padded, ids, experts, block_m)
+    # agrees with the stable permutation of the valid pairs
+    valid = ids[(ids >= 0) & (ids < experts)]
+    order, counts, _ = orc.permute(valid, experts)
+    index = np.flatnonzero((ids >= 0) & (ids < experts))
+    assert np.array_equal(sorted_ids[sorted_ids != pairs], index[order])
+
+
+def test_moe_align_checker_catches_planted_mistakes():
+    from moe_align_props import check_moe_align
+
+    rng = np.random.default_rng(3)
+    ids = rng.integers(0, 8, 200)
+    sorted_ids, expert_ids, padded = orc.moe_align(ids, 8, 16)
+    swapped = sorted_ids.copy()
+    swapped[[0, 1]] = swapped[[1, 0]]  # two pairs of expert 0 out of order
+    with pytest.raises(AssertionError):
+        check_moe_align(swapped, expert_ids, padded, ids, 8, 16)
+    shifted = expert_ids.copy()
+    shifted[0] = 1
+    with pytest.raises(AssertionError):
+        check_moe_align(sorted_ids, shifted, padded, ids, 8, 16)
+    with pytest.raises(AssertionError):
+        check_moe_align(sorted_ids, expert_ids, padded + 16, ids, 8, 16)
