@@ -8,6 +8,8 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdint>
+#include <map>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -520,8 +522,8 @@ void quant_operand(dmoe::QuantProjArgs& q, const void* x, int x_dtype, int64_t x
     }
 }
 
-// Router + routed experts of one layer (dmoe_fp8_moe_layer): the validated
-// call.
+// Router + routed experts of one layer (dmoe_fp8_moe_layer and its
+// no-allocation variant): the validated call.
 struct LayerCall {
     BankGeom g;
     Activations a;
@@ -545,6 +547,35 @@ LayerCall check_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64
     const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
                                   ids_out, weights_out, weights_dtype};
     return LayerCall{g, a, route, pairs};
+}
+
+// ------------------------------------------------- decode without allocation
+// dmoe_fp8_moe_layer_noalloc keeps its scratch in this file-scope array: one
+// copy per GPU, at that GPU's own address, held until the process ends.
+// 8 MiB holds the decode layout of every call the decode kernels take (256
+// route pairs at H 8192, I 4096; the layout check pins this).  The host-side
+// name is only a stand-in for the device copy: host code must use the address
+// static_scratch() looks up, never `scratch` itself.
+using dmoe::kStaticScratchBytes;
+static __device__ __align__(256) __attribute__((used)) uint8_t scratch[kStaticScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+void* static_scratch() {
+    static std::mutex mu;
+    static std::map<int, void*> by_device;
+    int dev = -1;
+    const hipError_t dev_err = hipGetDevice(&dev);
+    if (dev_err != hipSuccess) throw std::runtime_error(std::string("hipGetDevice failed: ") + hipGetErrorString(dev_err));
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = by_device.find(dev);
+    if (it != by_device.end()) return it->second;
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+        throw std::runtime_error(std::string("no device address for the static scratch: ") + hipGetErrorString(err));
+    by_device.emplace(dev, ptr);
+    return ptr;
 }
 
 }  // namespace
@@ -773,6 +804,25 @@ int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dtype, int6
         }
         fp8_call(g, call_a, c.route, ids_out, DMOE_I64, weights_out, weights_dtype, c.pairs, top_k, gu_dtype, out,
                  out_dtype, out_row_stride, nullptr, workspace, workspace_bytes, status, as_stream(stream));
+    });
+}
+
+int dmoe_fp8_moe_layer_noalloc(const DmoeFp8Bank* bank, const void* x, int x_dtype, int64_t x_row_stride,
+                               int tokens, const float* logits, int64_t logits_row_stride, int top_k,
+                               int renormalize, int64_t* ids_out, void* weights_out, int weights_dtype,
+                               int x_group, int gu_dtype, void* out, int out_dtype, int64_t out_row_stride,
+                               int* status, void* stream) {
+    return checked([&] {
+        const LayerCall c = check_layer(bank, x, x_dtype, x_row_stride, tokens, logits, logits_row_stride, top_k,
+                                        renormalize, ids_out, weights_out, weights_dtype, x_group, gu_dtype, out,
+                                        out_dtype, out_row_stride);
+        require(c.pairs <= dmoe::kMaxDecodePairs,
+                "the no-allocation layer takes decode calls of at most 256 route pairs (tokens * top_k)");
+        const size_t need = fp8_workspace_layout(c.pairs, c.g.H, c.g.I, nullptr, nullptr);
+        require(need <= kStaticScratchBytes, "call needs more scratch than the 8 MiB static scratch holds");
+        void* ws = static_scratch();
+        fp8_decode_call(c.g, c.a, c.route, weights_out, weights_dtype, c.pairs, top_k, gu_dtype, out, out_dtype,
+                        out_row_stride, nullptr, ws, kStaticScratchBytes, status, as_stream(stream));
     });
 }
 

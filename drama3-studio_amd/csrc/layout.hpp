@@ -83,6 +83,10 @@ inline size_t head_bytes() {
     return c.size();
 }
 
+// Fixed scratch of the no-allocation decode entry point: holds the decode
+// layout of every call the decode kernels take.
+constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+
 // Decode calls (<= kMaxDecodePairs pairs): the grouping record, FP8
 // activation rows, fp32 h and the FP8 hidden of the three-launch decode.
 struct DecodeWorkspace {

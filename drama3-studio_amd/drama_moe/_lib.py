@@ -73,6 +73,8 @@ _SIGNATURES = {
                        ctypes.c_size_t, _P, _P], _I),
     "dmoe_fp8_moe_layer": ([ctypes.POINTER(Fp8Bank), _P, _I, _L, _I, _P, _L, _I, _I, _P, _P, _I, _I, _I,
                             _P, _I, _L, _P, ctypes.c_size_t, _P, _P], _I),
+    "dmoe_fp8_moe_layer_noalloc": ([ctypes.POINTER(Fp8Bank), _P, _I, _L, _I, _P, _L, _I, _I, _P, _P, _I, _I,
+                                    _I, _P, _I, _L, _P, _P], _I),
     "dmoe_rotate_quantize": ([_P, _I, _L, _I, _I, _P, _P, _P], _I),
     "dmoe_quant_workspace_bytes": ([_P, _I, _I], ctypes.c_size_t),
     "dmoe_quant_projection_workspace_bytes": ([_I, _I, _I, _I], ctypes.c_size_t),

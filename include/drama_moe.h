@@ -253,6 +253,24 @@ DMOE_API int dmoe_fp8_moe_layer(const DmoeFp8Bank* bank, const void* x, int x_dt
                                 int gu_dtype, void* out, int out_dtype, int64_t out_row_stride,
                                 void* workspace, size_t workspace_bytes, int* status, void* stream);
 
+/* dmoe_fp8_moe_layer for decode calls (tokens * top_k <= 256) that ALLOCATES
+ * NOTHING: no workspace argument, no hipMalloc, no allocating library call.
+ * No counterpart in the reference; it is for callers that cannot allocate --
+ * code under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Its scratch is one fixed 8 MiB device array per GPU inside the
+ * library (zero at load, held until the process ends; the library looks up
+ * its address once per device).  Larger calls are rejected with an error.
+ * Every call on a GPU shares that GPU's scratch and leaves its contents for
+ * the next call: calls that overlap on one GPU (other streams, other host
+ * threads) race -- order them.  Outputs are bit-identical to
+ * dmoe_fp8_moe_layer's. */
+DMOE_API int dmoe_fp8_moe_layer_noalloc(const DmoeFp8Bank* bank, const void* x, int x_dtype,
+                                        int64_t x_row_stride, int tokens, const float* logits,
+                                        int64_t logits_row_stride, int top_k, int renormalize,
+                                        int64_t* ids_out, void* weights_out, int weights_dtype,
+                                        int x_group, int gu_dtype, void* out, int out_dtype,
+                                        int64_t out_row_stride, int* status, void* stream);
+
 /* ------------------------------------------------ packed-integer expert banks
  *
  * One projection bank of a packed mode (the reference's QuantizedStore,

@@ -6,7 +6,8 @@
 // counters, call counters, hand-off words) has the same offsets and sizes in
 // every layout; and no region of any layout intersects the head regions of
 // any other layout -- so nothing a grouped or packed call writes can be read
-// back by the single-launch decode as a tagged hand-off word.
+// back by the single-launch decode as a tagged hand-off word.  Also: the
+// largest decode layout fits the no-allocation entry point's fixed scratch.
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -107,6 +108,14 @@ int main() {
                     ++layouts;
                 }
         }
+    {  // the no-allocation decode's fixed scratch holds the largest decode layout
+        dmoe::Carver c(nullptr);
+        dmoe::decode_layout(c, dmoe::kMaxDecodePairs, dmoe::kMaxHidden, dmoe::kMaxInter);
+        if (c.size() > dmoe::kStaticScratchBytes) {
+            std::printf("FAIL largest decode layout %zu > static scratch %zu\n", c.size(), dmoe::kStaticScratchBytes);
+            ++failures;
+        }
+    }
     if (failures) {
         std::printf("%d layout failures\n", failures);
         return 1;
