@@ -665,6 +665,43 @@ int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts, int32_t
     });
 }
 
+size_t dmoe_moe_align_workspace_bytes(int pairs, int experts, int block_m) {
+    if (pairs < 1 || pairs > dmoe::kMaxPermutePairs || experts < 1 || experts > dmoe::kMaxExperts ||
+        block_m < 1 || block_m > 1024)
+        return 0;
+    dmoe::Carver c(nullptr);
+    dmoe::align_layout(c, pairs, experts, block_m);
+    return c.size();
+}
+
+int dmoe_moe_align(const void* ids, int ids_dtype, int pairs, int experts, int block_m, int32_t* sorted_ids,
+                   int32_t* expert_ids, int32_t* padded, int max_blocks, void* workspace, size_t workspace_bytes,
+                   int* status, void* stream) {
+    return checked([&] {
+        require(ids && sorted_ids && expert_ids && padded, "moe_align buffers are required");
+        require(is_id_dtype(ids_dtype), "route ids must be int32 or int64");
+        require(experts >= 1 && experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 1048576]");
+        require(block_m >= 1 && block_m <= 1024, "block_m outside [1, 1024]");
+        const int tiles = dmoe::max_block_tiles(pairs, experts, block_m);
+        require(max_blocks >= tiles, "expert_ids must hold ceil(pairs / block_m) + experts blocks");
+        dmoe::Carver measure(nullptr);
+        dmoe::align_layout(measure, pairs, experts, block_m);
+        require(workspace != nullptr && workspace_bytes >= measure.size(), "workspace too small");
+        require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+        dmoe::Carver c(workspace);
+        const dmoe::AlignWorkspace w = dmoe::align_layout(c, pairs, experts, block_m);
+        hipStream_t st = as_stream(stream);
+        dmoe::PermuteArgs pa{ids, ids_dtype, pairs, experts, w.order, w.counts, w.offsets, status,
+                             w.permute_scratch, w.permute_scratch + pairs, nullptr, block_m, max_blocks,
+                             expert_ids, w.tile_m0, w.tile_count};
+        dmoe::launch_permute(pa, st);
+        const dmoe::AlignArgs aa{w.order, w.offsets, expert_ids, w.tile_m0, w.tile_count, pairs, block_m,
+                                 max_blocks, sorted_ids, padded};
+        dmoe::launch_align_expand(aa, st);
+    });
+}
+
 size_t dmoe_fp8_workspace_bytes(const DmoeFp8Bank* bank, int pairs) {
     if (!bank || pairs < 1 || pairs > dmoe::kMaxPermutePairs) return 0;
     if (pairs <= dmoe::kMaxDecodePairs) return fp8_workspace_layout(pairs, bank->w13.k, bank->w13.n / 2, nullptr, nullptr);

@@ -240,6 +240,21 @@ void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stre
 void launch_route_topk(const RouteArgs& a, hipStream_t stream);
 void launch_route_quantize(const RouteArgs& r, const QuantArgs& q, hipStream_t stream);
 void launch_permute(const PermuteArgs& a, hipStream_t stream);
+
+// moe_align expansion of a tile map: row r of tile i holds the pair at sorted
+// position tile_m0[i] + r of expert tile_expert[i], or the sentinel `pairs`
+// past that expert's last pair and in every tile past tile_count.
+struct AlignArgs {
+    const int32_t* order;
+    const int32_t* offsets;
+    const int32_t* tile_expert;
+    const int32_t* tile_m0;
+    const int32_t* tile_count;
+    int pairs, block_m, max_tiles;
+    int32_t* sorted_ids;    // [max_tiles * block_m]
+    int32_t* padded;        // tile_count * block_m
+};
+void launch_align_expand(const AlignArgs& a, hipStream_t stream);
 void launch_fp8_grouped_gateup(const GroupedGateUpArgs& a, hipStream_t stream);
 void launch_fp8_grouped_down(const GroupedDownArgs& a, hipStream_t stream);
 void launch_combine(const CombineArgs& a, hipStream_t stream);

@@ -149,6 +149,30 @@ inline PrefillWorkspace prefill_layout(Carver& c, int pairs, int experts, int H,
     return w;
 }
 
+// moe_align calls: the permutation and the tile rows (the tile experts go
+// straight to the caller's expert_ids).
+struct AlignWorkspace {
+    Head head;
+    int32_t* permute_scratch;
+    int32_t* order;
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* tile_m0;
+    int32_t* tile_count;
+};
+
+inline AlignWorkspace align_layout(Carver& c, int pairs, int experts, int block_m) {
+    AlignWorkspace w{};
+    w.head = carve_head(c);
+    w.permute_scratch = c.take<int32_t>("permute scratch", permute_scratch_bytes(pairs, experts));
+    w.order = c.take<int32_t>("order", (size_t)pairs * 4);
+    w.counts = c.take<int32_t>("counts", (size_t)experts * 4);
+    w.offsets = c.take<int32_t>("offsets", (size_t)(experts + 1) * 4);
+    w.tile_m0 = c.take<int32_t>("tile rows", (size_t)max_block_tiles(pairs, experts, block_m) * 4);
+    w.tile_count = c.take<int32_t>("tile count", 4);
+    return w;
+}
+
 // Packed-bank calls: the permutation with its active-expert list, the INT8
 // activation rows (modes 1-3), the bf16 hidden and its INT8 form, and the
 // fp32 partials.

@@ -467,6 +467,28 @@ __global__ __launch_bounds__(kPermuteBlock) void permute_scatter_kernel(PermuteA
     a.order[a.hist[(int64_t)blockIdx.x * a.experts + e] + r] = (int32_t)i;
 }
 
+// One thread per sorted_ids entry (tile, row); reads stay inside the tile map
+// (tile < tile_count), offsets [experts + 1] and order [pairs].
+__global__ __launch_bounds__(256) void align_expand_kernel(AlignArgs a) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)a.max_tiles * a.block_m) return;
+    const int tile = (int)(idx / a.block_m), r = (int)(idx % a.block_m);
+    const int count = *a.tile_count;
+    int32_t v = a.pairs;
+    if (tile < count) {
+        const int e = a.tile_expert[tile];
+        const int pos = a.tile_m0[tile] + r;
+        if (pos < a.offsets[e + 1]) v = a.order[pos];
+    }
+    a.sorted_ids[idx] = v;
+    if (idx == 0) *a.padded = count * a.block_m;
+}
+
+void launch_align_expand(const AlignArgs& a, hipStream_t stream) {
+    const int64_t n = (int64_t)a.max_tiles * a.block_m;
+    hipLaunchKernelGGL(align_expand_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a);
+}
+
 void launch_permute(const PermuteArgs& a, hipStream_t stream) {
     if (a.pairs <= kSmallPermute) {
         hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(1024), 0, stream, a);

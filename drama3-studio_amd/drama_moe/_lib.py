@@ -61,6 +61,8 @@ _SIGNATURES = {
     "dmoe_route_topk": ([_P, _L, _I, _I, _I, _I, _P, _P, _I, _P], _I),
     "dmoe_permute_workspace_bytes": ([_I, _I], ctypes.c_size_t),
     "dmoe_permute": ([_P, _I, _I, _I, _P, _P, _P, _P, ctypes.c_size_t, _P, _P], _I),
+    "dmoe_moe_align_workspace_bytes": ([_I, _I, _I], ctypes.c_size_t),
+    "dmoe_moe_align": ([_P, _I, _I, _I, _I, _P, _P, _P, _I, _P, ctypes.c_size_t, _P, _P], _I),
     "dmoe_fp8_workspace_bytes": ([ctypes.POINTER(Fp8Bank), _I], ctypes.c_size_t),
     "dmoe_fp8_moe_forward": ([ctypes.POINTER(Fp8Bank), _P, _I, _L, _I, _P, _I, _P, _I, _I, _I, _I,
                               _P, _I, _L, _P, ctypes.c_size_t, _P, _P], _I),

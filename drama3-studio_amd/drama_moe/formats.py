@@ -49,7 +49,10 @@ class ProjectionFormat:
 # per-channel scales; GPTQ int32 words with fp16 group scales; INT8 rows with
 # a channel scale; 6-bit (nibble + 2-bit planes) and 4-bit codebook codes
 # with E4M3 group-16 scale bytes followed by the fp32 channel scale (and, in
-# mode 3, the codebook).
+# mode 3, the codebook).  Modes 4 and 5 have no reference counterpart: 4-bit
+# (level = code - 8) and 6-bit (level = code - 32, the mode-2 planes) codes
+# with one fp16 scale per (row, 128-group), computed on FP8 per-token
+# activations (W4A8-g128 / W6A8-g128).
 BANK_FORMATS: dict = {
     "fp8": ProjectionFormat(FP8_DTYPE, lambda k: k, torch.float32,
                             lambda n, k: ((n // FP8_BLOCK_SIZE, k // FP8_BLOCK_SIZE), (n, 1))),
@@ -57,7 +60,10 @@ BANK_FORMATS: dict = {
     1: ProjectionFormat(torch.int8, lambda k: k, torch.float32, lambda n, k: ((n, 1),)),
     2: ProjectionFormat(torch.int8, lambda k: 3 * k // 4, torch.uint8, lambda n, k: ((n, k // 16 + 4),)),
     3: ProjectionFormat(torch.int8, lambda k: k // 2, torch.uint8, lambda n, k: ((n, k // 16 + 8),)),
+    4: ProjectionFormat(torch.int8, lambda k: k // 2, torch.float16, lambda n, k: ((n, k // 128),)),
+    5: ProjectionFormat(torch.int8, lambda k: 3 * k // 4, torch.float16, lambda n, k: ((n, k // 128),)),
 }
+G128_MODES = (4, 5)
 
 
 def check_bank_buffers(fmt, buffers: dict, experts: int, hidden: int, inter: int) -> None:
@@ -238,8 +244,10 @@ def nibble_pack(codes: torch.Tensor) -> torch.Tensor:
 @dataclass(frozen=True)
 class QuantizedStore:
     """Packed expert bank of one mode (quantized_model.py:26-68):
-    mode 0 W4A16 GPTQ, 1 INT8 ConvRot, 2 W6A8, 3 W4A8 codebook.  ``w13_zeros`` /
-    ``w2_zeros`` (GPTQ qzeros [E, K/128, N/8] int32) make mode 0 asymmetric."""
+    mode 0 W4A16 GPTQ, 1 INT8 ConvRot, 2 W6A8, 3 W4A8 codebook; ``w13_zeros`` /
+    ``w2_zeros`` (GPTQ qzeros [E, K/128, N/8] int32) make mode 0 asymmetric.
+    Modes 4 (W4A8-g128) and 5 (W6A8-g128) hold 4- / 6-bit codes with fp16
+    scales per (row, 128-group) and run on FP8 per-token activations."""
 
     w13_weight: torch.Tensor
     w13_scale_inv: torch.Tensor
@@ -270,7 +278,7 @@ class QuantizedStore:
         return {name: getattr(self, name) for name in EXPERT_BUFFER_NAMES}
 
     def validate(self) -> None:
-        if self.mode not in (0, 1, 2, 3):
+        if self.mode not in (0, 1, 2, 3, 4, 5):
             raise ValueError("Unknown quantized bank format")
         if self.w13_weight.ndim != 3:
             raise ValueError("Quantized banks are stacked [experts, rows, columns] tensors")
@@ -298,7 +306,13 @@ def random_quantized_bank(mode: int, experts: int, hidden: int, inter: int, *,
 
     tensors = {}
     for prefix, n, k in (("w13", 2 * inter, hidden), ("w2", hidden, inter)):
-        if mode == 0:
+        if mode in G128_MODES:
+            codes = randint(16 if mode == 4 else 64, experts, n, k)
+            tensors[prefix + "_weight"] = nibble_pack(codes) if mode == 4 else six_pack(codes)
+            levels = 7.5 if mode == 4 else 31.5  # largest |level| of the format
+            tensors[prefix + "_scale_inv"] = ((rand(experts, n, k // 128) * 0.5 + 0.75)
+                                              * (0.02 * 2.5 / levels)).half()
+        elif mode == 0:
             codes = randint(16, experts, n, k)
             tensors[prefix + "_weight"] = gptq_pack(codes)
             tensors[prefix + "_scale_inv"] = ((rand(experts, n, k // 128) * 0.5 + 0.75)

@@ -7,6 +7,9 @@ hybrid_decode.py:182-183:
 * ``quantize_groups(kernel, x, columns)`` with ``kernel`` = ``quant_kernel``
   (FP8 128-groups of x) or ``silu_mul_quant_kernel`` (SiLU(gate) * up of a
   gate|up row, then FP8 128-groups), returning ``(q e4m3, fp32 scales)``;
+* ``moe_align(ids, num_experts, block_m)`` -> ``(sorted_ids, expert_ids,
+  padded)``, the block-padded expert-sorted pair layout
+  (offload.py:299-306, hybrid_layer.py:39);
 * ``fp8_moe_forward(x, ids, weights, w13, s13, w2, s2)``;
 * ``fp8_gemm_supported(devices)``.
 """
@@ -63,6 +66,35 @@ def quantize_groups(kernel, x: torch.Tensor, columns: int):
     else:
         raise ValueError(f"Unknown quantization kernel {kernel!r}")
     return q, scales
+
+
+def moe_align(ids: torch.Tensor, num_experts: int, block_m: int):
+    """Route pairs sorted by expert and padded per expert to whole blocks of
+    ``block_m`` rows, on the current stream: ``sorted_ids`` int32
+    [blocks * block_m] (pair indices, the sentinel ``pairs`` in padding rows),
+    ``expert_ids`` int32 [blocks] (-1 past the last block) and ``padded``, a
+    device int32 [1] holding the padded row count; blocks = ceil(pairs /
+    block_m) + num_experts is the capacity."""
+    if ids.device.type != "cuda":
+        raise RuntimeError("moe_align requires a ROCm GPU tensor")
+    from .offload import device_state
+
+    flat = ids.reshape(-1).contiguous()
+    pairs = flat.numel()
+    blocks = -(-pairs // block_m) + num_experts
+    sorted_ids = torch.empty(blocks * block_m, dtype=torch.int32, device=ids.device)
+    expert_ids = torch.empty(blocks, dtype=torch.int32, device=ids.device)
+    padded = torch.zeros(1, dtype=torch.int32, device=ids.device)
+    if pairs == 0:
+        return sorted_ids.fill_(0), expert_ids.fill_(-1), padded
+    lib = _lib.library()
+    state = device_state(ids.device)
+    ws = state.workspace_for(lib.dmoe_moe_align_workspace_bytes(pairs, num_experts, block_m))
+    _lib.check(lib.dmoe_moe_align(_lib.ptr(flat), _lib.dtype_code(flat.dtype), pairs, num_experts, block_m,
+                                  _lib.ptr(sorted_ids), _lib.ptr(expert_ids), _lib.ptr(padded), blocks,
+                                  _lib.ptr(ws), ws.numel(), _lib.ptr(state.status),
+                                  _lib.stream_handle(ids.device)))
+    return sorted_ids, expert_ids, padded
 
 
 def fp8_moe_forward(x, ids, weights, w13, s13, w2, s2):

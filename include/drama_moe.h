@@ -152,6 +152,25 @@ DMOE_API int dmoe_permute(const void* ids, int ids_dtype, int pairs, int experts
                           int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes,
                           int* status, void* stream);
 
+/* Workspace bytes of dmoe_moe_align (0 outside pairs in [1, 2^20], experts
+ * in [1, 512], block_m in [1, 1024]). */
+DMOE_API size_t dmoe_moe_align_workspace_bytes(int pairs, int experts, int block_m);
+
+/* moe_align: the route pairs (flattened ids, int32 or int64) sorted by expert
+ * and padded per expert to whole blocks of block_m rows.  sorted_ids
+ * [max_blocks * block_m] int32: for each expert in ascending order its pair
+ * indices in ascending order, then the sentinel `pairs` up to the next
+ * multiple of block_m; expert_ids [max_blocks] int32: the expert of each
+ * block, -1 past the last; *padded (device int32) = blocks * block_m.
+ * max_blocks >= ceil(pairs / block_m) + experts.  Ids outside [0, experts)
+ * are left out and flagged in `status`.  The grouped FP8 GEMMs run on the
+ * same tile map with block_m = 64.  Replaces moe_align(ids, E, block_m) of the
+ * fish fp8_moe module (call sites offload.py:299-306, hybrid_layer.py:39). */
+DMOE_API int dmoe_moe_align(const void* ids, int ids_dtype, int pairs, int experts, int block_m,
+                            int32_t* sorted_ids, int32_t* expert_ids, int32_t* padded,
+                            int max_blocks, void* workspace, size_t workspace_bytes, int* status,
+                            void* stream);
+
 /* Workspace bytes of an FP8 call over `pairs` route pairs (0 outside
  * [1, 2^20]).  A workspace is 256-byte aligned, zero-filled as a whole once
  * when allocated, and reused by later calls of any kind and size it covers

@@ -129,26 +129,51 @@ ORC_API int orc_quantize_fp8(const float* x, int64_t rows, int64_t cols, int64_t
 
 /* ------------------------------------------------ FP8 expert bank and GEMV */
 
-/* One projection bank: weight bytes [E, N, K] (K contiguous) and fp32 scales
- * addressed as s[e*se + (n / n_div)*sn + (kb / kb_div)*sk] for 128-column block
- * kb.  Reference block layout [E, N/128, K/128] is n_div=128, kb_div=1
- * (offload.py:157-169); a per-output-channel layout [E, N, 1] is n_div=1, sk=0. */
+/* One projection bank [E, N, K] whose weights are multiplied by FP8
+ * activations.  wfmt selects how a weight is stored:
+ *   0  E4M3 bytes [E, N, K] (K contiguous) with fp32 scales addressed as
+ *      s[e*se + (n / n_div)*sn + (kb / kb_div)*sk] for 128-column block kb.
+ *      Reference block layout [E, N/128, K/128] is n_div=128, kb_div=1
+ *      (offload.py:157-169); per output channel [E, N, 1] is n_div=1, sk=0;
+ *   1  4-bit codes, two per byte along K (even k in the low nibble) [E, N, K/2],
+ *      level = code - 8;
+ *   2  6-bit codes in the W6 planes of tests/test_quantized_kernels.py:18-24
+ *      ([E, N, K/2] low nibbles, then [E, N, K/4] 2-bit high parts, LSB
+ *      first), level = code - 32.
+ * Formats 1 and 2 (the W4A8 / W6A8 variants with group-128 scales and FP8
+ * per-token activations; no reference counterpart) scale each (row, 128-group)
+ * by an fp16 value at s[e*se + n*sn + kb*sk]. */
 typedef struct {
     const uint8_t* w;
     const float* s;
     int64_t N, K;
     int64_t se, sn, sk;
     int64_t n_div, kb_div;
+    int64_t wfmt;
 } OrcFp8Proj;
 
 static float proj_scale(const OrcFp8Proj* p, int64_t e, int64_t n, int64_t kb) {
+    if (p->wfmt != 0) return orc_f32_from_f16(((const uint16_t*)p->s)[e * p->se + n * p->sn + kb * p->sk]);
     return p->s[e * p->se + (n / p->n_div) * p->sn + (kb / p->kb_div) * p->sk];
+}
+
+/* Integer level of weight (e, n, k) of a format-1 / format-2 bank. */
+static float int_level(const OrcFp8Proj* p, int64_t e, int64_t n, int64_t k) {
+    if (p->wfmt == 1) {
+        const uint8_t b = p->w[(e * p->N + n) * (p->K / 2) + k / 2];
+        return (float)(((k & 1) ? b >> 4 : b & 15) - 8);
+    }
+    const uint8_t* row = p->w + (e * p->N + n) * (p->K * 3 / 4);
+    const int low = (k & 1) ? row[k / 2] >> 4 : row[k / 2] & 15;
+    const int high = (row[p->K / 2 + k / 4] >> (2 * (k % 4))) & 3;
+    return (float)((low | (high << 4)) - 32);
 }
 
 /* One output row of a block-scaled W8A8 projection.
  * Reference: native/src/runtime.cpp:162-172 (row) with the scalar dot of
  * fp8_reference.cpp:95-104: per 128-column block a sequential fp32 dot, then
- * acc = fma(dot * s_x[kb], s_w[n, kb], acc).  `xs_stride` is 1 for 128-groups
+ * acc = fma(dot * s_x[kb], s_w[n, kb], acc).  Integer formats 1 and 2 follow
+ * the same chain with the block's integer levels and its fp16 group scale.  `xs_stride` is 1 for 128-groups
  * and 0 for a single per-token scale. */
 static float fp8_table[256];
 static int fp8_table_ready = 0;
@@ -163,7 +188,10 @@ static float proj_row(const OrcFp8Proj* p, int64_t e, int64_t n, const float* xq
     float acc = 0.0f;
     for (int64_t kb = 0; kb < p->K / 128; ++kb) {
         float dot = 0.0f;
-        for (int k = 0; k < 128; ++k) dot += fp8_table[w[kb * 128 + k]] * xq[kb * 128 + k];
+        if (p->wfmt == 0)
+            for (int k = 0; k < 128; ++k) dot += fp8_table[w[kb * 128 + k]] * xq[kb * 128 + k];
+        else
+            for (int k = 0; k < 128; ++k) dot += int_level(p, e, n, kb * 128 + k) * xq[kb * 128 + k];
         acc = fmaf(dot * xs[kb * xs_stride], proj_scale(p, e, n, kb), acc);
     }
     return acc;

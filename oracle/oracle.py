@@ -66,7 +66,7 @@ class _Fp8Proj(ctypes.Structure):
     _fields_ = [("w", ctypes.c_void_p), ("s", ctypes.c_void_p),
                 ("N", ctypes.c_int64), ("K", ctypes.c_int64),
                 ("se", ctypes.c_int64), ("sn", ctypes.c_int64), ("sk", ctypes.c_int64),
-                ("n_div", ctypes.c_int64), ("kb_div", ctypes.c_int64)]
+                ("n_div", ctypes.c_int64), ("kb_div", ctypes.c_int64), ("wfmt", ctypes.c_int64)]
 
 
 class _QuantProj(ctypes.Structure):
@@ -129,6 +129,26 @@ class Fp8Bank:
                                sa * sb, sb, 1 if sb > 1 else 0, N // sa, (K // 128) // sb)
 
 
+class G128Bank:
+    """Host copy of one projection bank of the group-128 integer formats
+    (W4A8-g128: mode 4, 4-bit codes [E, N, K/2], level = code - 8; W6A8-g128:
+    mode 5, the 6-bit planes [E, N, 3K/4], level = code - 32) with fp16
+    scales [E, N, K/128].  Usable wherever an Fp8Bank is: the FP8 W8A8
+    contract with these weights (integer level x group scale)."""
+
+    def __init__(self, mode, weight, scales):
+        if mode not in (4, 5):
+            raise ValueError("group-128 integer banks are modes 4 and 5")
+        self.w = np.ascontiguousarray(weight).view(np.uint8)
+        self.s = np.ascontiguousarray(scales, dtype=np.float16)
+        E, N, cols = self.w.shape
+        K = cols * 2 if mode == 4 else cols * 4 // 3
+        if self.s.shape != (E, N, K // 128):
+            raise ValueError("scales must be [E, N, K/128] fp16")
+        self.struct = _Fp8Proj(self.w.ctypes.data, self.s.ctypes.data, N, K, N * (K // 128), K // 128, 1,
+                               1, 1, 1 if mode == 4 else 2)
+
+
 def fp8_expert_pairs(w13: Fp8Bank, w2: Fp8Bank, x, ids, weights, *, x_group=128, gu_dtype="bf16"):
     """Ordered weighted fp32 partials for one row (runtime.cpp:173-237)."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
@@ -156,6 +176,67 @@ def fp8_moe_forward(w13: Fp8Bank, w2: Fp8Bank, x, ids, weights, *, x_group=128,
         ctypes.c_int64(top_k), ctypes.c_int(DTYPE_CODES[gu_dtype]),
         ctypes.c_int(DTYPE_CODES[out_dtype]), _ptr(out)), "moe_forward")
     return out
+
+
+# ------------------------------------------- O2: dequantize, then matmul
+
+def _round_to(values, dtype):
+    values = np.asarray(values, np.float32)
+    if dtype == "fp32":
+        return values
+    if dtype == "bf16":
+        return bf16_round(values)
+    return values.astype(np.float16).astype(np.float32)  # IEEE round-to-nearest-even
+
+
+def dequantize_fp8_blocks(weight_bytes, scale_inv, dtype="bf16"):
+    """W = fp32(E4M3 value * 128x128 block scale) rounded to the compute
+    dtype (offload.py:44-56)."""
+    w = fp8_decode(np.asarray(weight_bytes, np.uint8))
+    n, k = w.shape
+    rb, cb = scale_inv.shape
+    if n != rb * 128 or k != cb * 128:
+        raise ValueError("FP8 weight shape does not match its 128x128 block scales")
+    scaled = (w.reshape(rb, 128, cb, 128) * np.asarray(scale_inv, np.float32)[:, None, :, None]).astype(np.float32)
+    return _round_to(scaled.reshape(n, k), dtype)
+
+
+def o2_expert_pairs(w13: "Fp8Bank", w2: "Fp8Bank", x, ids, weights, dtype="bf16"):
+    """TorchExpertBackend.forward_pairs (offload.py:214-244): per expert the
+    dequantized W13 / W2 in the compute dtype; gate, up = x @ W13^T and
+    values = (silu(gate) * up) @ W2^T, each product accumulated exactly
+    (float64) and rounded once to the compute dtype, silu and the product
+    rounded to it too; the weighted value in fp32.  x [pairs, H] (compute
+    dtype values as fp32), ids / weights [pairs]; returns fp32 [pairs, H]."""
+    x = np.asarray(x, np.float32)
+    ids = np.asarray(ids, np.int64).reshape(-1)
+    weights = np.asarray(weights, np.float32).reshape(-1)
+    out = np.empty((ids.size, w2.w.shape[1]), np.float32)
+    inter = w13.w.shape[1] // 2
+    for e in np.unique(ids):
+        rows = np.flatnonzero(ids == e)
+        m13 = dequantize_fp8_blocks(w13.w[e], w13.s[e], dtype).astype(np.float64)
+        m2 = dequantize_fp8_blocks(w2.w[e], w2.s[e], dtype).astype(np.float64)
+        gu = _round_to(x[rows].astype(np.float64) @ m13.T, dtype)
+        gate, up = gu[:, :inter], gu[:, inter:]
+        act = _round_to(_round_to(silu(gate), dtype) * up, dtype)
+        values = _round_to(act.astype(np.float64) @ m2.T, dtype)
+        out[rows] = values * weights[rows, None]
+    return out
+
+
+def o2_moe_forward(w13: "Fp8Bank", w2: "Fp8Bank", x, ids, weights, dtype="bf16"):
+    """TorchExpertBackend.forward (offload.py:202-212): the pairs of each
+    token summed over the top-k slots in fp32, rounded to the compute dtype."""
+    ids = np.asarray(ids, np.int64)
+    tokens, top_k = ids.shape
+    rows = np.repeat(np.asarray(x, np.float32), top_k, axis=0)
+    pairs = o2_expert_pairs(w13, w2, rows, ids.reshape(-1), np.asarray(weights).reshape(-1), dtype)
+    part = pairs.reshape(tokens, top_k, -1)
+    acc = part[:, 0].copy()
+    for j in range(1, top_k):
+        acc = (acc + part[:, j]).astype(np.float32)
+    return _round_to(acc, dtype)
 
 
 # ------------------------------------------------------------------ routing

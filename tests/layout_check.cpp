@@ -100,7 +100,8 @@ int main() {
                     check(run("prefill", [&](dmoe::Carver& c) { dmoe::prefill_layout(c, p, e, H, I); }));
                     check(run("packed", [&](dmoe::Carver& c) { dmoe::quant_layout(c, (p + 7) / 8, p, e, H, I); }));
                     check(run("packed rows", [&](dmoe::Carver& c) { dmoe::quant_layout(c, p, p, e, H, I); }));
-                    layouts += 3;
+                    check(run("moe_align", [&](dmoe::Carver& c) { dmoe::align_layout(c, p, e, 16); }));
+                    layouts += 4;
                 }
             for (int p : decode_pairs)
                 for (int e : experts) {

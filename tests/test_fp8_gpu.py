@@ -150,6 +150,27 @@ def test_route_topk_ties_take_the_lower_index(cuda):
     np.testing.assert_array_equal(ids.cpu().numpy(), orc.route_topk(logits.numpy(), 4)[0])
 
 
+def test_route_topk_orders_equal_probabilities_by_logit(cuda):
+    """Distinct logits whose fp32 softmax probabilities tie: the router kernel
+    and the single-launch decode's in-kernel router put the larger logit
+    first, as the oracle does (the documented (logit desc, index asc) rule)."""
+    print_case("route_topk equal probabilities")
+    from test_oracle import _equal_probability_logits
+
+    logits = torch.from_numpy(_equal_probability_logits())
+    eids, ew = orc.route_topk(logits.numpy(), 3)
+    w, ids = router.route_topk(logits.to(cuda), 3, dtype=torch.float32)
+    np.testing.assert_array_equal(ids.cpu().numpy(), eids)
+    np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=1e-6, atol=0)  # softmax sum order: last place
+    staged = to_device(random_fp8_bank(8, 256, 256, generator=torch.Generator().manual_seed(11)), cuda)
+    x = torch.randn(3, 256, device=cuda).bfloat16()
+    _, w2, i2 = HipExpertBackend().forward_routed(x, logits.to(cuda), 3, staged, weights_dtype=torch.float32)
+    np.testing.assert_array_equal(i2.cpu().numpy(), eids)
+    np.testing.assert_allclose(w2.cpu().numpy(), ew, rtol=1e-6, atol=0)
+    for got in (w.cpu().numpy(), w2.cpu().numpy()):  # tied probabilities keep equal weights
+        assert got[0, 0] == got[0, 1] and got[1, 0] == got[1, 1] and got[2, 0] == got[2, 1] == got[2, 2]
+
+
 @pytest.mark.parametrize("tokens,experts", [(1, 128), (16, 128), (2048, 128), (300, 7), (64, 512), (12500, 128)])
 def test_permute_bit_exact_against_stable_argsort(cuda, tokens, experts):
     print_case("permute", tokens, experts)
@@ -510,3 +531,31 @@ def test_stage_down_requires_prepared_workspace_geometry(cuda):
     with pytest.raises(ValueError, match="256 route pairs"):
         fp8_decode.staged_forward(x.expand(200, 256).contiguous(), ids.expand(200, 2).contiguous(),
                                   w.expand(200, 2).contiguous(), staged)
+
+
+@pytest.mark.parametrize("tokens", [1, 4])
+def test_o2_error_reported_for_information(cuda, tokens):
+    """The W8A8 path against O2 -- the reference's dequantize-then-matmul
+    TorchExpertBackend (offload.py:199-244): bf16 weights, unquantized bf16
+    activations.  Reported, not gated to 2e-2: the FP8 activation and hidden
+    quantization of the W8A8 contract alone put it a few percent from O2.
+    The check is only that it stays inside that band (< 10%), while the
+    contract oracle stays within 2e-2."""
+    print_case("O2 error", tokens)
+    g = torch.Generator().manual_seed(20261205 + tokens)
+    staged = random_fp8_bank(32, 2048, 768, generator=g)
+    dev = to_device(staged, cuda)
+    x = torch.randn(tokens, 2048, generator=g).bfloat16()
+    ids, w = orc.route_topk(torch.randn(tokens, 32, generator=g).numpy(), 8)
+    weights = torch.from_numpy(w).bfloat16()
+    out = HipExpertBackend().forward(x.to(cuda), torch.from_numpy(ids).to(cuda), weights.to(cuda), dev)
+    got = out.float().cpu().numpy()
+    b13, b2 = oracle_banks(staged)
+    o2 = orc.o2_moe_forward(b13, b2, x.float().numpy(), ids, weights.float().numpy())
+    contract = orc.fp8_moe_forward(b13, b2, x.float().numpy(), ids, weights.float().numpy())
+    o2_inf = rel_inf(got, o2)
+    o2_rms = float(np.sqrt(np.mean((got - o2) ** 2) / np.mean(o2 ** 2)))
+    print(f"[O2] tokens={tokens} W8A8 vs O2: rel_inf {o2_inf:.4f} rel_rms {o2_rms:.4f}; "
+          f"vs contract oracle: rel_inf {rel_inf(got, contract):.2e}", flush=True)
+    assert rel_inf(got, contract) < TOL
+    assert o2_inf < 0.1

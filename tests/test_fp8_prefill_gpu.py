@@ -13,7 +13,8 @@ import pytest
 import torch
 
 from conftest import print_case
-from drama_moe import router
+from drama_moe import fp8_moe, router
+from moe_align_props import check_moe_align
 from drama_moe.formats import StagedExperts, random_fp8_bank
 from drama_moe.offload import HipExpertBackend
 from oracle import oracle as orc
@@ -167,8 +168,11 @@ def test_grouped_layer_in_hipgraph(cuda):
 @pytest.mark.parametrize("x_group", ["token", 128])
 def test_prefill_2048_tokens_full_shape(cuda, x_group):
     """The prefill workload: 2048 tokens, top-8 of 128 Zipf(1.1) experts,
-    H 2048, I 768, per-channel FP8 weights; ids bit-exact for every token,
-    outputs against the oracle on a spread of 24 tokens."""
+    H 2048, I 768, per-channel FP8 weights.  ids bit-exact for every token;
+    every token's output within the bar of the decode kernels (pinned to the
+    oracle by the decode tests) run on the same routes in 32-token calls, so
+    every tile of every expert is covered; and 64 spread tokens against the
+    oracle directly."""
     print_case("prefill 2048", x_group)
     experts, hidden, inter, tokens = 128, 2048, 768, 2048
     staged = random_fp8_bank(experts, hidden, inter, layout="channel", device=cuda,
@@ -181,10 +185,47 @@ def test_prefill_2048_tokens_full_shape(cuda, x_group):
     np.testing.assert_array_equal(ids.cpu().numpy(), eids)
     counts = np.bincount(eids.reshape(-1), minlength=experts)
     assert counts.max() > 1000
-    pick = np.linspace(0, tokens - 1, 24).astype(int)
+    backend = HipExpertBackend(x_group=x_group)
+    xd = x.to(cuda)
+    decode = torch.cat([backend.forward(xd[t:t + 32], ids[t:t + 32], weights[t:t + 32], staged)
+                        for t in range(0, tokens, 32)])
+    got, ref = out.float(), decode.float()
+    per_token = ((got - ref).abs().amax(1) / ref.abs().amax(1).clamp_min(1e-30)).cpu().numpy()
+    assert per_token.max() < TOL, (int(per_token.argmax()), float(per_token.max()))
+    pick = np.linspace(0, tokens - 1, 64).astype(int)
     b13, b2 = oracle_banks(staged)
     expected = orc.fp8_moe_forward(b13, b2, x.float().numpy()[pick], eids[pick],
                                    weights.float().cpu().numpy()[pick],
                                    x_group=128 if x_group == 128 else hidden)
     assert rel_inf(out.float().cpu().numpy()[pick], expected) < TOL
     assert torch.isfinite(out.float()).all()
+
+
+@pytest.mark.parametrize("pairs,experts,block_m,zipf", [
+    (16384, 128, 64, True),    # the prefill workload's tile map (one-launch placement)
+    (16384, 128, 16, True),
+    (16384, 128, 32, True),
+    (600, 32, 16, False),      # single-workgroup permutation
+    (100000, 128, 64, False),  # scan + scatter permutation
+    (5000, 512, 128, False),
+])
+def test_moe_align_tile_map(cuda, pairs, experts, block_m, zipf):
+    """dmoe_moe_align (the permutation kernels' tile map expanded to the
+    moe_align layout) bit-exact against the oracle, and the properties that
+    fix the layout: every valid pair in exactly one block of its expert,
+    ascending within the expert, sentinels only at each expert's tail."""
+    print_case("moe_align", pairs, experts, block_m)
+    if zipf:
+        ids, _ = orc.route_topk(zipf_logits(pairs // 8, experts, 20261203).numpy(), 8)
+    else:
+        rng = np.random.default_rng(pairs + block_m)
+        ids = rng.integers(0, experts, pairs)
+        ids[rng.integers(0, pairs, 4)] = [-3, experts, experts + 1, -1]
+    for dtype in (torch.int64, torch.int32):
+        sorted_ids, expert_ids, padded = fp8_moe.moe_align(torch.from_numpy(ids).to(dtype).to(cuda), experts,
+                                                           block_m)
+        esorted, eexperts, epadded = orc.moe_align(ids, experts, block_m)
+        assert int(padded.item()) == epadded
+        np.testing.assert_array_equal(expert_ids.cpu().numpy(), eexperts)
+        np.testing.assert_array_equal(sorted_ids.cpu().numpy(), esorted)
+        check_moe_align(sorted_ids.cpu().numpy(), expert_ids.cpu().numpy(), epadded, ids, experts, block_m)

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+from drama_moe.formats import random_fp8_bank
 from oracle import oracle as orc
 from oracle import ref_native
 
@@ -291,6 +292,35 @@ def test_route_topk_ties_resolve_to_the_lower_index():
     np.testing.assert_array_equal(np.sort(ids[:, :2], -1), t.numpy())
 
 
+def _equal_probability_logits():
+    """Rows where two DISTINCT logits give the SAME fp32 softmax probability
+    (exp(-2^-30) rounds to 1.0): the larger logit is the larger probability
+    in exact arithmetic, but fp32 ties them."""
+    logits = np.full((3, 8), -4.0, np.float32)
+    logits[0, [1, 5]] = [np.float32(-2.0 ** -30), 0.0]      # higher index has the larger logit
+    logits[1, [2, 6]] = [0.0, np.float32(-2.0 ** -30)]      # lower index has the larger logit
+    logits[2, [0, 3, 7]] = [np.float32(-2.0 ** -28), np.float32(-2.0 ** -29), 0.0]
+    return logits
+
+
+def test_route_topk_orders_equal_probabilities_by_logit():
+    """The router's rule is (logit desc, index asc): on distinct logits whose
+    fp32 probabilities tie, the larger logit goes first -- the exact-arithmetic
+    order of the probabilities.  The reference calls probabilities.topk
+    (backbone_graph.py:319-320), whose order among equal values torch leaves
+    unspecified; both rules pick the same set."""
+    logits = _equal_probability_logits()
+    probs = torch.softmax(torch.from_numpy(logits), -1)
+    assert probs[0, 1] == probs[0, 5] and probs[1, 2] == probs[1, 6]
+    assert probs[2, 0] == probs[2, 3] == probs[2, 7]
+    ids, weights = orc.route_topk(logits, 3)
+    np.testing.assert_array_equal(ids[:, :2], [[5, 1], [2, 6], [7, 3]])
+    assert ids[2, 2] == 0
+    assert weights[0, 0] == weights[0, 1]
+    t = probs.topk(2, -1).indices.sort(-1).values.numpy()
+    np.testing.assert_array_equal(np.sort(ids[:2, :2], -1), t[:2])
+
+
 def test_route_without_renormalisation_returns_probabilities():
     logits = torch.randn(4, 32, generator=torch.Generator().manual_seed(1))
     ids, weights = orc.route_topk(logits.numpy(), 4, renormalize=False)
@@ -469,3 +499,134 @@ def test_moe_align_checker_catches_planted_mistakes():
         check_moe_align(sorted_ids, shifted, padded, ids, 8, 16)
     with pytest.raises(AssertionError):
         check_moe_align(sorted_ids, expert_ids, padded + 16, ids, 8, 16)
+
+
+# ------------------------------------------------- O2 dequantize-then-matmul
+
+def _torch_o2_pairs(b13_w, b13_s, b2_w, b2_s, x, ids, weights, dtype):
+    """The same pipeline on torch's CPU kernels: dequantize in fp32, cast to
+    the compute dtype, F.linear in that dtype, silu, product, weighted in fp32."""
+    import torch.nn.functional as F
+
+    out = []
+    for r in range(x.shape[0]):
+        e = int(ids[r])
+        def deq(w, s):
+            v = torch.from_numpy(w[e]).view(torch.float8_e4m3fn).float()
+            n, k = v.shape
+            blocks = v.view(n // 128, 128, k // 128, 128) * torch.from_numpy(s[e])[:, None, :, None]
+            return blocks.reshape(n, k).to(dtype)
+        gate, up = F.linear(x[r:r + 1].to(dtype), deq(b13_w, b13_s)).chunk(2, dim=-1)
+        values = F.linear(F.silu(gate) * up, deq(b2_w, b2_s))
+        out.append(values.float() * float(weights[r]))
+    return torch.cat(out).numpy()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_o2_pairs_match_torch_cpu_linear(dtype):
+    """O2 (TorchExpertBackend semantics) against torch's own CPU bf16 / fp16
+    kernels: the only freedom is the accumulation order inside F.linear
+    before its single rounding, so nearly every value is bit-identical and
+    the rest differ by a last-place rounding."""
+    torch_dtype = torch.bfloat16 if dtype == "bf16" else torch.float16
+    g = torch.Generator().manual_seed(77)
+    bank = random_fp8_bank(4, 256, 256, generator=g)
+    b13 = orc.Fp8Bank(bank.w13_weight.view(torch.uint8).numpy(), bank.w13_scale_inv.numpy())
+    b2 = orc.Fp8Bank(bank.w2_weight.view(torch.uint8).numpy(), bank.w2_scale_inv.numpy())
+    x = torch.randn(6, 256, generator=g).to(torch_dtype)
+    ids = np.array([0, 3, 1, 3, 2, 0])
+    weights = np.array([0.5, 0.25, 1.0, 0.125, 0.75, 2.0], np.float32)
+    got = orc.o2_expert_pairs(b13, b2, x.float().numpy(), ids, weights, dtype)
+    want = _torch_o2_pairs(b13.w, b13.s, b2.w, b2.s, x, ids, weights, torch_dtype)
+    assert np.mean(got == want) > 0.95
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-2
+    # a planted mistake -- each row block scaled by another block's scale -- is far off
+    bad = orc.Fp8Bank(b13.w, np.ascontiguousarray(b13.s[:, ::-1, :]))  # block scales of the wrong rows
+    wrong = orc.o2_expert_pairs(bad, b2, x.float().numpy(), ids, weights, dtype)
+    assert np.max(np.abs(wrong - want)) / np.max(np.abs(want)) > 5e-2
+
+
+def test_o2_layer_sums_slots_in_order():
+    g = torch.Generator().manual_seed(5)
+    bank = random_fp8_bank(4, 128, 128, generator=g)
+    b13 = orc.Fp8Bank(bank.w13_weight.view(torch.uint8).numpy(), bank.w13_scale_inv.numpy())
+    b2 = orc.Fp8Bank(bank.w2_weight.view(torch.uint8).numpy(), bank.w2_scale_inv.numpy())
+    x = torch.randn(2, 128, generator=g).bfloat16().float().numpy()
+    ids = np.array([[1, 2, 3], [0, 0, 2]])
+    w = np.array([[0.5, 0.3, 0.2], [0.6, 0.3, 0.1]], np.float32)
+    out = orc.o2_moe_forward(b13, b2, x, ids, w)
+    pairs = orc.o2_expert_pairs(b13, b2, np.repeat(x, 3, 0), ids.reshape(-1), w.reshape(-1)).reshape(2, 3, -1)
+    expect = orc.bf16_round(((pairs[:, 0] + pairs[:, 1]).astype(np.float32) + pairs[:, 2]).astype(np.float32))
+    np.testing.assert_array_equal(out, expect)
+
+
+# ------------------------------------ W4A8 / W6A8 with group-128 scales
+
+def _g128_case(mode, E=3, H=256, I=128, seed=0):
+    from drama_moe.formats import nibble_pack, six_pack
+
+    rng = np.random.default_rng(seed + mode)
+    top = 16 if mode == 4 else 64
+    bias = 8 if mode == 4 else 32
+    codes = {"w13": rng.integers(0, top, (E, 2 * I, H)), "w2": rng.integers(0, top, (E, H, I))}
+    scales = {"w13": rng.uniform(0.002, 0.006, (E, 2 * I, H // 128)).astype(np.float16),
+              "w2": rng.uniform(0.002, 0.006, (E, H, I // 128)).astype(np.float16)}
+    pack = nibble_pack if mode == 4 else six_pack
+    banks = {k: orc.G128Bank(mode, pack(torch.from_numpy(codes[k])).numpy(), scales[k]) for k in codes}
+    dense = {k: (codes[k] - bias).astype(np.float64) * np.repeat(scales[k].astype(np.float64), 128, axis=-1)
+             for k in codes}
+    return banks, dense, codes, scales
+
+
+def _g128_brute(dense, x, e, weight, H, I):
+    """fp64 W8A8 arithmetic: per-token FP8 activation, gate/up rounded to bf16,
+    silu(gate) * up, FP8 128-group hidden, down, route weight."""
+    q, s = orc.quantize_fp8(x[None], H)
+    xq = orc.fp8_decode(q[0]).astype(np.float64) * np.float64(s[0, 0])
+    gu = orc.bf16_round((dense["w13"][e] @ xq).astype(np.float32))
+    h = (gu[:I] / (1 + np.exp(-gu[:I].astype(np.float64))) * gu[I:]).astype(np.float32)
+    hq, hs = orc.quantize_fp8(h[None], 128)
+    hv = orc.fp8_decode(hq[0]).astype(np.float64) * np.repeat(hs[0].astype(np.float64), 128)
+    return dense["w2"][e] @ hv * weight
+
+
+@pytest.mark.parametrize("mode", [4, 5])
+def test_g128_pairs_match_fp64_brute_force(mode):
+    """The oracle's group-128 integer formats against an fp64 evaluation from
+    the raw codes (not the packed bytes), so packing, level offset, scale
+    indexing and the per-token activation scale are all pinned."""
+    H, I = 256, 128
+    banks, dense, _, _ = _g128_case(mode, H=H, I=I)
+    rng = np.random.default_rng(9)
+    x = orc.bf16_round(rng.standard_normal(H).astype(np.float32))
+    ids = np.array([2, 0, 2, 1])
+    w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    got = orc.fp8_expert_pairs(banks["w13"], banks["w2"], x, ids, w, x_group=H)
+    want = np.stack([_g128_brute(dense, x, e, wt, H, I) for e, wt in zip(ids, w)])
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 5e-3
+    # plausible mistakes are far outside that: swapped nibbles, a level
+    # offset off by one, the other projection's scales
+    swapped = dict(dense)
+    c = _g128_case(mode, H=H, I=I)[2]
+    bias = 8 if mode == 4 else 32
+    perm = np.arange(H).reshape(-1, 2)[:, ::-1].reshape(-1)
+    swapped["w13"] = (c["w13"][..., perm] - bias) * np.repeat(_g128_case(mode, H=H, I=I)[3]["w13"].astype(np.float64),
+                                                               128, axis=-1)
+    off = {k: v + np.repeat(_g128_case(mode, H=H, I=I)[3][k].astype(np.float64), 128, axis=-1)
+           for k, v in dense.items()}
+    for bad in (swapped, off):  # each would fail the 5e-3 check above by a wide margin
+        wrong = np.stack([_g128_brute(bad, x, e, wt, H, I) for e, wt in zip(ids, w)])
+        assert np.max(np.abs(got - wrong)) / np.max(np.abs(wrong)) > 2e-2
+
+
+def test_g128_layer_combines_in_slot_order():
+    H, I = 256, 128
+    banks, dense, _, _ = _g128_case(4, H=H, I=I, seed=4)
+    rng = np.random.default_rng(1)
+    x = orc.bf16_round(rng.standard_normal((2, H)).astype(np.float32))
+    ids = np.array([[0, 1], [2, 2]])
+    w = np.array([[0.7, 0.3], [0.5, 0.5]], np.float32)
+    out = orc.fp8_moe_forward(banks["w13"], banks["w2"], x, ids, w, x_group=H)
+    for t in range(2):
+        pairs = orc.fp8_expert_pairs(banks["w13"], banks["w2"], x[t], ids[t], w[t], x_group=H)
+        np.testing.assert_array_equal(out[t], orc.bf16_round((pairs[0] + pairs[1]).astype(np.float32)))

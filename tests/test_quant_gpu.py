@@ -249,12 +249,15 @@ def test_w4a16_fp16_activations_dequantize_to_fp16(cuda):
     assert rel_inf(out.float().cpu().numpy(), expected.numpy()) < TOL
 
 
-@pytest.mark.parametrize("mode", [0, 2])
-def test_forward_pairs_and_invalid_ids(cuda, mode):
-    print_case("quant pairs invalid", mode)
-    g = torch.Generator().manual_seed(55 + mode)
-    store = random_quantized_bank(mode, 8, 512, 256, generator=g)
-    rows = 40
+@pytest.mark.parametrize("mode,rows,asymmetric", [(0, 40, False), (2, 40, False), (0, 200, True),
+                                                   (0, 40, True), (2, 200, False)])
+def test_forward_pairs_and_invalid_ids(cuda, mode, rows, asymmetric):
+    """Ordered partials of single-pair rows; 40 rows take the small-call
+    kernels, 200 rows the grouped projection kernel (with qzeros for the
+    asymmetric W4A16 bank)."""
+    print_case("quant pairs invalid", mode, rows, asymmetric)
+    g = torch.Generator().manual_seed(55 + mode + rows)
+    store = random_quantized_bank(mode, 8, 512, 256, asymmetric=asymmetric, generator=g)
     x = torch.randn(rows, 512, generator=g).bfloat16()
     ids = torch.randint(0, 8, (rows, 1), generator=g)
     ids[5, 0] = 8
@@ -306,11 +309,14 @@ def test_quant_layer_in_hipgraph(cuda):
 @pytest.mark.parametrize("mode", MODES)
 def test_full_size_decode_and_prefill(cuda, mode):
     """Layer shape E=128, H=2048, I=768, top-8: decode T=1 in full, and a
-    512-token prefill checked on 6 spread tokens."""
+    512-token prefill (4096 pairs: the grouped projection kernel) checked on
+    6 spread tokens.  W4A16 uses asymmetric banks (GPTQ qzeros), the format
+    of the 512-token W4A16 benchmark."""
     print_case("quant full size", mode)
     g = torch.Generator().manual_seed(20261204 + mode)
-    dev = random_quantized_bank(mode, 128, 2048, 768, device=cuda,
+    dev = random_quantized_bank(mode, 128, 2048, 768, device=cuda, asymmetric=mode == 0,
                                 generator=torch.Generator(device=cuda).manual_seed(20261204 + mode))
+    assert (dev.w13_zeros is not None) == (mode == 0)
     store = dev  # the oracle copies it to the host
     backend = quantized.QuantizedExpertBackend(mode)
     for tokens, pick in ((1, [0]), (512, list(np.linspace(0, 511, 6).astype(int)))):
