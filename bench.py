@@ -270,7 +270,8 @@ def run_prefill(reps: int = 10):
     return result
 
 
-QUANT_NAMES = {0: "w4a16_asym_g128", 1: "int8_convrot", 2: "w6a8", 3: "w4a8_codebook"}
+QUANT_NAMES = {0: "w4a16_asym_g128", 1: "int8_convrot", 2: "w6a8", 3: "w4a8_codebook", 4: "w4a8_g128_fp8",
+               5: "w6a8_g128_fp8"}
 
 
 def quant_expert_bytes(mode: int) -> int:
@@ -283,8 +284,12 @@ def quant_expert_bytes(mode: int) -> int:
             total += n * k + n * 4
         elif mode == 2:
             total += n * k * 3 // 4 + n * (k // 16 + 4)
-        else:
+        elif mode == 3:
             total += n * k // 2 + n * (k // 16 + 8)
+        elif mode == 4:
+            total += n * k // 2 + n * (k // 128) * 2
+        else:
+            total += n * k * 3 // 4 + n * (k // 128) * 2
     return total
 
 
@@ -312,20 +317,21 @@ def _graph_time_us(fn, steps_per_graph: int, replays: int, stream) -> float:
 def run_quant(layers: int = 24, window: int = 16, replays: int = 16):
     """Packed-bank MoE layers (H 2048, 128 experts x I 768, top-8), all
     experts resident.  Per mode: a hipGraph of `window` decode steps through
-    `layers` distinct layer banks, each (step, layer) with its own seeded
-    top-8 route (T=1), replayed so that `window * replays` steps run; plus
-    the 512-token W4A16 prefill."""
+    its layer banks (`layers` distinct banks for the 24-layer formats,
+    LAYERS for the others), each (step, layer) a router + experts call on its
+    own seeded logits (T=1), replayed so that `window * replays` steps run;
+    plus the 512-token W4A16 prefill."""
     import torch
 
-    from drama_moe import router
     from drama_moe.formats import random_quantized_bank
     from drama_moe.quantized import QuantizedExpertBackend
 
     device = torch.device("cuda", 0)
     stream = torch.cuda.Stream(device)
     result = {}
-    for mode in (0, 2, 3, 1):
-        n_layers = layers if mode in (2, 3) else LAYERS
+    for mode in (0, 2, 3, 4, 5, 1):
+        step_layers = mode in (2, 3, 4, 5)
+        n_layers = layers if step_layers else LAYERS
         banks = [random_quantized_bank(mode, EXPERTS, HIDDEN, INTER, asymmetric=mode == 0, device=device,
                                        generator=torch.Generator(device=device).manual_seed(SEED + 1000 * mode + l))
                  for l in range(n_layers)]
@@ -333,25 +339,28 @@ def run_quant(layers: int = 24, window: int = 16, replays: int = 16):
         g = torch.Generator(device=device).manual_seed(SEED + 7 * mode)
         xs = torch.randn(window, n_layers, 1, HIDDEN, device=device, generator=g).bfloat16()
         logits = torch.randn(window, n_layers, 1, EXPERTS, device=device, generator=g)
-        weights, ids = router.route_topk(logits.reshape(-1, EXPERTS), TOP_K)
-        weights = weights.reshape(window, n_layers, 1, TOP_K)
-        ids = ids.reshape(window, n_layers, 1, TOP_K)
         outs = torch.empty_like(xs)
 
         def steps():
             for t in range(window):
                 for l in range(n_layers):
-                    backend.forward(xs[t, l], ids[t, l], weights[t, l], banks[l], out=outs[t, l])
+                    backend.forward_routed(xs[t, l], logits[t, l], TOP_K, banks[l], out=outs[t, l])
 
         layer_us = _graph_time_us(steps, window * n_layers, replays, stream)
-        uniq = [len(set(r)) for r in ids.reshape(-1, TOP_K).cpu().tolist()]
-        layer_bytes = sum(uniq) / len(uniq) * quant_expert_bytes(mode) + 2 * HIDDEN * 2
+        status = backend.status(device)
+        if status:
+            raise RuntimeError(f"packed mode {mode} steps raised device status bits {status:#x}")
+        _, step_uniq = step_bytes(logits.reshape(-1, 1, EXPERTS), 1)
+        layer_bytes = step_uniq * quant_expert_bytes(mode) + 2 * HIDDEN * 2 + EXPERTS * 4
         entry = {"layer_us": round(layer_us, 2), "expert_bytes": quant_expert_bytes(mode),
-                 "hbm_frac": round(layer_bytes / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-        if mode in (2, 3):
+                 "hbm_frac": round(layer_bytes / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                 "routing": "in the timed region"}
+        if step_layers:
             entry.update({"layers": n_layers, "step_us": round(layer_us * n_layers, 1),
                           "steps_timed": window * replays})
         if mode == 0:  # 512-token prefill
+            from drama_moe import router
+
             x = torch.randn(512, HIDDEN, device=device, generator=g).bfloat16()
             w, i = router.route_topk(torch.randn(512, EXPERTS, device=device, generator=g), TOP_K)
             out = torch.empty_like(x)
@@ -366,57 +375,125 @@ def run_quant(layers: int = 24, window: int = 16, replays: int = 16):
     return result
 
 
-def cpu_baseline(budget_s: float = 12.0):
-    """The reference CPU expert executor (oracle/_ref), one token per call with
-    8 route slots over 8 worker threads, block-128 FP8 banks of the same layer
-    shape.  Falls back to the scalar C oracle port if _ref is absent."""
+def host_cpu() -> dict:
+    """The host the CPU lanes run on: model string, vector ISA the reference
+    executor selects (AVX-512 > AVX2 > scalar, as its cpuid dispatch), cores
+    this process may use and physical cores."""
+    model, flags, cores = "unknown", set(), set()
+    try:
+        phys = None
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            key, _, value = line.partition(":")
+            key, value = key.strip(), value.strip()
+            if key == "model name" and model == "unknown":
+                model = value
+            elif key == "flags" and not flags:
+                flags = set(value.split())
+            elif key == "physical id":
+                phys = value
+            elif key == "core id":
+                cores.add((phys, value))
+    except OSError:
+        pass
+    isa = "avx512" if {"avx512f", "avx512bw"} <= flags else "avx2" if "avx2" in flags else "scalar"
+    return {"model": model, "isa": isa, "affinity_cpus": len(os.sched_getaffinity(0)),
+            "physical_cores": len(cores) or os.cpu_count()}
+
+
+def _timed(fn, budget_s: float, min_calls: int = 2):
+    fn()
+    calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or calls < min_calls:
+        fn()
+        calls += 1
+    return (time.perf_counter() - t0) * 1e6 / calls, calls
+
+
+def cpu_baseline(budget_s: float = 8.0):
+    """CPU lanes beside the GPU, on this host's cores.
+
+    Headline (value): the reference's own CPU expert executor (compiled from
+    its sources into oracle/_ref; scalar C oracle port without it), one token
+    per call, its 8 route slots over 8 worker threads (the most it uses:
+    it parallelises over route slots only), on a 128-expert bank of the
+    decode layer's shape and weight distribution -- N(0, 0.02) weights, but
+    with the 128x128 block scales the executor takes (the GPU leg uses
+    per-channel scales) -- and 8 distinct random experts per call (the GPU
+    leg routes N(0,1) logits).  Also: 1 thread; 4 tokens as 4 consecutive
+    calls (the executor is batch-one); and the torch-CPU
+    dequantize-then-matmul lanes (oracle/torch_cpu.py) of the FP8 and packed
+    formats with torch's CPU threads."""
     import numpy as np
+    import torch
 
-    from oracle import ref_native
+    from drama_moe.formats import random_fp8_bank, random_quantized_bank
+    from oracle import ref_native, torch_cpu
 
+    device = torch.device("cuda", 0)
     rng = np.random.default_rng(SEED)
-
-    def fp8_bytes(shape):
-        b = rng.integers(0, 256, size=shape, dtype=np.uint8)
-        b[(b & 0x7F) == 0x7F] = 0x3F  # no NaN codes
-        return b
-
-    w13 = fp8_bytes((EXPERTS, 2 * INTER, HIDDEN))
-    w2 = fp8_bytes((EXPERTS, HIDDEN, INTER))
-    s13 = rng.uniform(1e-4, 2e-4, (EXPERTS, 2 * INTER // 128, HIDDEN // 128)).astype(np.float32)
-    s2 = rng.uniform(1e-4, 2e-4, (EXPERTS, HIDDEN // 128, INTER // 128)).astype(np.float32)
-    x = (rng.standard_normal(HIDDEN).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    gen = torch.Generator(device=device).manual_seed(SEED + 17)
+    bank = random_fp8_bank(EXPERTS, HIDDEN, INTER, layout="block", generator=gen, device=device)
+    host = {name: t.cpu() for name, t in bank.buffers().items()}
+    w13, s13 = host["w13_weight"].view(torch.uint8).numpy(), host["w13_scale_inv"].numpy()
+    w2, s2 = host["w2_weight"].view(torch.uint8).numpy(), host["w2_scale_inv"].numpy()
+    xt = torch.randn(4, HIDDEN, generator=torch.Generator().manual_seed(SEED)).bfloat16()
+    x = xt.view(torch.int16).numpy().view(np.uint16)
     weights = np.full(TOP_K, 1.0 / TOP_K, np.float32)
-    threads = 8
+    lanes = {}
+    info = host_cpu()
+
+    def ids():
+        return rng.choice(EXPERTS, TOP_K, replace=False).astype(np.int64)
+
     if ref_native.available():
         lib = ref_native.RefLibrary()
         kind = "reference"
-        with ref_native.RefExecutor(lib, HIDDEN, INTER, capacity=TOP_K, threads=threads) as ex:
-            out = np.empty((TOP_K, HIDDEN), np.float32)
-            ex.forward(w13, s13, w2, s2, x, rng.choice(EXPERTS, TOP_K, replace=False), weights, out)
-            calls, t0 = 0, time.perf_counter()
-            while time.perf_counter() - t0 < budget_s or calls < 3:
-                ids = rng.choice(EXPERTS, TOP_K, replace=False).astype(np.int64)
-                ex.forward(w13, s13, w2, s2, x, ids, weights, out)
-                calls += 1
-            elapsed = time.perf_counter() - t0
-        sample = (f"{calls} layer decodes (1 token, 8 distinct random experts of 128, H 2048, I 768, "
-                  f"block-128 FP8 scales) on the reference's drama_native executor, {threads} threads")
+        out = np.empty((TOP_K, HIDDEN), np.float32)
+        for threads in (8, 1):
+            with ref_native.RefExecutor(lib, HIDDEN, INTER, capacity=TOP_K, threads=threads) as ex:
+                us, calls = _timed(lambda: ex.forward(w13, s13, w2, s2, x[0], ids(), weights, out),
+                                   budget_s if threads == 8 else budget_s / 3)
+                lanes[f"reference_executor_t1_threads{threads}"] = {"us_per_layer": round(us, 1), "calls": calls}
+                if threads == 8:
+                    def four():
+                        for t in range(4):
+                            ex.forward(w13, s13, w2, s2, x[t], ids(), weights, out)
+                    us4, calls4 = _timed(four, budget_s / 4)
+                    lanes["reference_executor_t4_threads8"] = {"us_per_layer": round(us4, 1), "calls": calls4}
+        value, cores = lanes["reference_executor_t1_threads8"]["us_per_layer"], 8
+        sample = (f"{lanes['reference_executor_t1_threads8']['calls']} one-token layer decodes on the reference's "
+                  "drama_native executor, 8 threads over the 8 route slots")
     else:
         from oracle import oracle as orc
 
-        threads, kind = 1, "port"
+        kind, cores = "port", 1
         b13, b2 = orc.Fp8Bank(w13, s13), orc.Fp8Bank(w2, s2)
-        xf = (x.astype(np.uint32) << 16).view(np.float32)
-        calls, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < budget_s or calls < 1:
-            ids = rng.choice(EXPERTS, TOP_K, replace=False)
-            orc.fp8_expert_pairs(b13, b2, xf, ids, weights)
-            calls += 1
-        elapsed = time.perf_counter() - t0
-        sample = f"{calls} layer decodes on the scalar C oracle port, 1 thread"
-    return {"value": elapsed * 1e6 / calls, "unit": "us", "cores": threads, "kind": kind,
-            "sample": sample}
+        xf = xt[0].float().numpy()
+        value, calls = _timed(lambda: orc.fp8_expert_pairs(b13, b2, xf, ids(), weights), budget_s, 1)
+        lanes["scalar_oracle_t1_threads1"] = {"us_per_layer": round(value, 1), "calls": calls}
+        sample = f"{calls} one-token layer decodes on the scalar C oracle port, 1 thread"
+
+    threads = torch.get_num_threads()
+    torch.set_num_threads(info["affinity_cpus"])
+    try:
+        tids = torch.from_numpy(ids()[None])
+        tw = torch.full((1, TOP_K), 1.0 / TOP_K)
+        bank_cpu = type(bank)(**host)
+        us, calls = _timed(lambda: torch_cpu.fp8_layer(bank_cpu, xt[:1], tids, tw), budget_s / 8)
+        lanes["torch_cpu_fp8_o2_t1"] = {"us_per_layer": round(us, 1), "calls": calls}
+        for mode in (0, 1, 2, 3, 4, 5):
+            store = random_quantized_bank(mode, EXPERTS, HIDDEN, INTER, asymmetric=mode == 0, device=device,
+                                          generator=torch.Generator(device=device).manual_seed(SEED + 31 * mode))
+            store = type(store)(**{f: (getattr(store, f).cpu() if isinstance(getattr(store, f), torch.Tensor)
+                                       else getattr(store, f)) for f in store.__dataclass_fields__})
+            us, calls = _timed(lambda: torch_cpu.layer(store, xt[:1], tids, tw), budget_s / 8)
+            lanes[f"torch_cpu_{QUANT_NAMES[mode]}_t1"] = {"us_per_layer": round(us, 1), "calls": calls}
+    finally:
+        torch.set_num_threads(threads)
+    return {"value": round(value, 2), "unit": "us", "cores": cores, "kind": kind, "sample": sample,
+            "host": info, "torch_threads": info["affinity_cpus"], "lanes": lanes,
+            "inputs": "N(0,0.02) weights with 128x128 block scales (executor and O2 lanes; the GPU uses "
+                      "per-channel scales), N(0,1) bf16 activations, 8 distinct random experts per token"}
 
 
 TRAFFIC_SUMMARY = ROOT / "profiles" / "fp8_fused_decode_kernel_moe_layer_b1_hbm_traffic.txt"

@@ -522,6 +522,87 @@ void quant_operand(dmoe::QuantProjArgs& q, const void* x, int x_dtype, int64_t x
     }
 }
 
+// ------------------------------------------- group-128 integer banks (4, 5)
+// W4A8-g128 / W6A8-g128 packed banks run on the FP8 decode kernels: their
+// integer levels expand exactly into E4M3 MFMA operands (wfmt.hpp), with the
+// activations quantized to FP8 per token.
+
+bool is_g128_mode(int mode) { return mode == 4 || mode == 5; }
+
+dmoe::Fp8Proj g128_proj(const DmoeQuantProj& p, int mode) {
+    require(p.weight && p.scale, "packed weight and scale pointers are required");
+    require(p.zeros == nullptr, "zero points apply to W4A16 banks only");
+    require(p.k >= 128 && p.k % 128 == 0, "group-128 banks need K a positive multiple of 128");
+    require(p.n >= 16 && p.n % 8 == 0, "group-128 banks need N a multiple of 8 and at least 16");
+    const int64_t wcols = mode == 4 ? (int64_t)p.k / 2 : (int64_t)p.k * 3 / 4;
+    require(p.weight_stride_n >= wcols && p.weight_stride_n % 16 == 0 && p.weight_stride_e >= 0 &&
+                p.weight_stride_e % 16 == 0 && reinterpret_cast<uintptr_t>(p.weight) % 16 == 0,
+            "packed weight rows must be contiguous and 16-byte aligned");
+    require(p.scale_stride_n >= (int64_t)(p.k / 128) * 2 && p.scale_stride_n % 2 == 0 && p.scale_stride_e >= 0 &&
+                p.scale_stride_e % 2 == 0 && reinterpret_cast<uintptr_t>(p.scale) % 2 == 0,
+            "group-128 scales must be fp16 [E, N, K/128] with contiguous rows");
+    dmoe::Fp8Proj k{};
+    k.w = static_cast<const uint8_t*>(p.weight);
+    k.s = static_cast<const float*>(p.scale);  // fp16 elements, read as such by the kernels
+    k.w_se = p.weight_stride_e;
+    k.w_sn = p.weight_stride_n;
+    k.s_se = p.scale_stride_e / 2;
+    k.s_sn = p.scale_stride_n / 2;
+    k.s_sk = 1;
+    k.n_div = 1;
+    k.kb_div = 1;
+    k.N = p.n;
+    k.K = p.k;
+    k.wfmt = mode == 4 ? dmoe::kWfInt4 : dmoe::kWfInt6;
+    return k;
+}
+
+BankGeom check_g128_bank(const DmoeQuantBank* bank) {
+    BankGeom g{g128_proj(bank->w13, bank->mode), g128_proj(bank->w2, bank->mode), bank->experts, bank->w13.k,
+               bank->w13.n / 2};
+    require(g.experts >= 1 && g.experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+    require(bank->w13.n % 2 == 0 && g.I % 128 == 0, "gate/up rows must be 2 * I with I a multiple of 128");
+    require(bank->w2.n == g.H && bank->w2.k == g.I, "w2 must be [E, H, I] for w13 [E, 2I, H]");
+    require(g.H <= dmoe::kMaxHidden && g.I <= dmoe::kMaxInter, "hidden or intermediate size too large");
+    return g;
+}
+
+size_t element_size(int dtype) { return dtype == DMOE_F32 || dtype == DMOE_I32 ? 4 : dtype == DMOE_I64 ? 8 : 2; }
+
+// A group-128 call of any size from route ids as consecutive decode calls of
+// at most kMaxDecodePairs pairs, in order on the stream (pairs of a chunk
+// read rows of their own; layer outputs are cut at whole tokens).
+void g128_forward(const BankGeom& g, const void* x, int x_dtype, int64_t x_row_stride, int rows, int row_div,
+                  const void* ids, int ids_dtype, const void* weights, int weights_dtype, int pairs, int top_k,
+                  void* out, int out_dtype, int64_t out_row_stride, float* out_pairs, void* workspace,
+                  size_t workspace_bytes, int* status, hipStream_t stream) {
+    const Activations full{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, rows, row_div, g.H};
+    check_activations(g, full, pairs);
+    require(out_pairs != nullptr || top_k <= dmoe::kMaxDecodePairs, "top_k above 256 for a group-128 layer call");
+    const int gu_dtype = x_dtype;
+    for (int p0 = 0; p0 < pairs;) {
+        const int r0 = p0 / row_div;
+        int count, div = row_div;
+        if (row_div <= dmoe::kMaxDecodePairs) {
+            count = std::min(pairs - p0, (dmoe::kMaxDecodePairs / row_div) * row_div);
+        } else {  // many pairs per row: a chunk stays inside one row
+            count = std::min({pairs - p0, dmoe::kMaxDecodePairs, (r0 + 1) * row_div - p0});
+            div = count;
+        }
+        const Activations a{static_cast<const char*>(x) + (int64_t)r0 * x_row_stride * element_size(x_dtype), x_dtype,
+                            x_row_stride, nullptr, nullptr, 0, 0, (count - 1) / div + 1, div, g.H};
+        const void* cw = static_cast<const char*>(weights) + (int64_t)p0 * element_size(weights_dtype);
+        const dmoe::RouteSource route =
+            ids_source(static_cast<const char*>(ids) + (int64_t)p0 * element_size(ids_dtype), ids_dtype);
+        void* cout = out_pairs ? nullptr
+                               : static_cast<char*>(out) + (int64_t)(p0 / top_k) * out_row_stride * element_size(out_dtype);
+        fp8_decode_call(g, a, route, cw, weights_dtype, count, out_pairs ? 1 : top_k, gu_dtype, cout, out_dtype,
+                        out_row_stride, out_pairs ? out_pairs + (int64_t)p0 * g.H : nullptr, workspace,
+                        workspace_bytes, status, stream);
+        p0 += count;
+    }
+}
+
 // Router + routed experts of one layer (dmoe_fp8_moe_layer and its
 // no-allocation variant): the validated call.
 struct LayerCall {
@@ -884,6 +965,8 @@ size_t dmoe_quant_workspace_bytes(const DmoeQuantBank* bank, int rows, int pairs
         bank->experts > dmoe::kMaxExperts)
         return 0;
     const int H = std::max(bank->w13.k, bank->w2.n), I = std::max(bank->w2.k, bank->w13.n / 2);
+    if (is_g128_mode(bank->mode))  // consecutive decode calls of at most 256 pairs
+        return fp8_workspace_layout(std::min(pairs, dmoe::kMaxDecodePairs), H, I, nullptr, nullptr);
     return quant_workspace_layout(rows, pairs, bank->experts, H, I, nullptr, nullptr);
 }
 
@@ -934,6 +1017,18 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
         require(bank != nullptr, "packed bank descriptor is required");
         const int E = bank->experts, mode = bank->mode;
         require(E >= 1 && E <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        if (is_g128_mode(mode)) {
+            const BankGeom g = check_g128_bank(bank);
+            require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 1048576]");
+            require(row_div >= 1 && rows >= 1 && (int64_t)(pairs - 1) / row_div < rows,
+                    "pairs read past the activation rows");
+            check_routes(ids, ids_dtype, weights, weights_dtype);
+            if (out_pairs == nullptr) check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
+            g128_forward(g, x, x_dtype, x_row_stride, rows, row_div, ids, ids_dtype, weights, weights_dtype, pairs,
+                         top_k, out, out_dtype, out_row_stride, out_pairs, workspace, workspace_bytes, status,
+                         as_stream(stream));
+            return;
+        }
         dmoe::QuantProjArgs up = check_quant_proj(bank->w13, mode, E);
         dmoe::QuantProjArgs dn = check_quant_proj(bank->w2, mode, E);
         const int H = up.K, I = up.N / 2;
@@ -996,6 +1091,41 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
                                        out, out_dtype, out_row_stride};
             dmoe::launch_combine(ca, st);
         }
+    });
+}
+
+int dmoe_quant_moe_layer(const DmoeQuantBank* bank, const void* x, int x_dtype, int64_t x_row_stride, int tokens,
+                         const float* logits, int64_t logits_row_stride, int top_k, int renormalize, int64_t* ids_out,
+                         void* weights_out, int weights_dtype, void* out, int out_dtype, int64_t out_row_stride,
+                         void* workspace, size_t workspace_bytes, int* status, void* stream) {
+    return checked([&] {
+        require(bank != nullptr, "packed bank descriptor is required");
+        require(bank->experts >= 1 && bank->experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        require(tokens >= 1 && top_k >= 1 && top_k <= bank->experts && top_k <= 64, "bad token count or top_k");
+        require(logits != nullptr && logits_row_stride >= bank->experts, "router logits [tokens, experts] required");
+        require(ids_out && weights_out && is_float_dtype(weights_dtype), "routing outputs are required");
+        const int pairs = checked_pairs(tokens, top_k);
+        hipStream_t st = as_stream(stream);
+        if (is_g128_mode(bank->mode) && pairs <= dmoe::kMaxDecodePairs) {
+            // one decode call that routes itself (the single-launch kernel when it fits)
+            const BankGeom g = check_g128_bank(bank);
+            const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, g.H};
+            check_activations(g, a, pairs);
+            check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
+            const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
+                                          ids_out, weights_out, weights_dtype};
+            fp8_decode_call(g, a, route, weights_out, weights_dtype, pairs, top_k, x_dtype, out, out_dtype,
+                            out_row_stride, nullptr, workspace, workspace_bytes, status, st);
+            return;
+        }
+        // route, then the experts from the written routes
+        const dmoe::RouteArgs ra{logits, logits_row_stride, tokens, bank->experts, top_k, renormalize != 0,
+                                 ids_out, weights_out, weights_dtype};
+        dmoe::launch_route_topk(ra, st);
+        if (dmoe_quant_moe_forward(bank, x, x_dtype, x_row_stride, tokens, top_k, ids_out, DMOE_I64, weights_out,
+                                   weights_dtype, pairs, top_k, out, out_dtype, out_row_stride, nullptr, workspace,
+                                   workspace_bytes, status, stream) != 0)
+            throw AbiError(g_last_error);
     });
 }
 

@@ -66,9 +66,12 @@ struct GateUpLds {
     int last;
 };
 
-// KBW = 128-column K blocks per wave (H <= 8 * 128 * KBW).
-template <int KBW>
-__global__ __launch_bounds__(kUpThreads, (KBW <= 2 ? 4 : 2)) void fp8_gateup_decode_kernel(GateUpArgs a) {
+// WF = weight format (wfmt.hpp); KBW = 128-column K blocks per wave
+// (H <= 8 * 128 * KBW).  Occupancy target: 4 workgroups per CU, 2 for larger
+// K or 6-bit weights (their expansion needs the registers).
+template <int WF, int KBW>
+__global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) void fp8_gateup_decode_kernel(
+    GateUpArgs a) {
     __shared__ GateUpLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const Grouping* gr = a.grouping;
@@ -106,18 +109,18 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 ? 4 : 2)) void fp8_gateup_dec
     v8i af[KBW];
     float sx[KBW][4];
     load_a(0, min(kRowsPerPass, M), af, sx);
-    const uint8_t* wg = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)(n0 + col) * a.w13.w_sn + grp * 32;
+    const uint8_t* wg = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)(n0 + col) * a.w13.w_sn;
     const uint8_t* wu = wg + (int64_t)I * a.w13.w_sn;
-    v8i bg[KBW], bu[KBW];
+    WRaw<WF> bg[KBW], bu[KBW];
     float swg[KBW], swu[KBW];
 #pragma unroll
     for (int i = 0; i < KBW; ++i) {
         const int kb = wave + i * kUpWaves;
         if (kb < KB) {
-            bg[i] = load32_stream(wg + kb * 128);
-            bu[i] = load32_stream(wu + kb * 128);
-            swg[i] = proj_scale(a.w13, e, n0 + col, kb);
-            swu[i] = proj_scale(a.w13, e, I + n0 + col, kb);
+            bg[i] = load_wraw<WF>(wg, H, kb, grp);
+            bu[i] = load_wraw<WF>(wu, H, kb, grp);
+            swg[i] = proj_scale<WF>(a.w13, e, n0 + col, kb);
+            swu[i] = proj_scale<WF>(a.w13, e, I + n0 + col, kb);
         }
     }
 
@@ -129,7 +132,8 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 ? 4 : 2)) void fp8_gateup_dec
         for (int i = 0; i < KBW; ++i) {
             const int kb = wave + i * kUpWaves;
             if (kb < KB) {
-                const v4f dg = mfma_fp8(af[i], bg[i], zero), du = mfma_fp8(af[i], bu[i], zero);
+                const v8i ap = a_operand<WF>(af[i]);
+                const v4f dg = mfma_w<WF>(ap, bg[i], zero), du = mfma_w<WF>(ap, bu[i], zero);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     acc_g[r] = fmaf(dg[r] * sx[i][r], swg[i], acc_g[r]);
@@ -192,34 +196,33 @@ struct DownLds {
     float hs[kDownQuantBytes / 128];
 };
 
-template <int KB2>
+template <int WF, int KB2>
 struct DownBatch {
-    v8i b[KB2];
+    WRaw<WF> b[KB2];
     float sw[KB2];
     int ai0, ai1;  // active indices of the two experts (ai1 = -1: none)
 };
 
 // Batch bi = active experts 2 bi and 2 bi + 1 (if any).
-template <int KB2>
+template <int WF, int KB2>
 __device__ __forceinline__ void load_down_batch(const DownArgs& a, int num_active, int bi, int n0, int col, int grp,
-                                                int KB, DownBatch<KB2>& bt) {
-    const v8i zero8i = {0, 0, 0, 0, 0, 0, 0, 0};
+                                                int KB, DownBatch<WF, KB2>& bt) {
     bt.ai0 = 2 * bi;
     bt.ai1 = 2 * bi + 1 < num_active ? 2 * bi + 1 : -1;
     const int ai = col < 8 ? bt.ai0 : bt.ai1;
     const int e = ai >= 0 ? a.grouping->expert[ai] : -1;
     const int n = n0 + (col & 7);
-    const uint8_t* wrow = a.w2.w + (int64_t)(e < 0 ? 0 : e) * a.w2.w_se + (int64_t)n * a.w2.w_sn + grp * 32;
+    const uint8_t* wrow = a.w2.w + (int64_t)(e < 0 ? 0 : e) * a.w2.w_se + (int64_t)n * a.w2.w_sn;
 #pragma unroll
     for (int kb = 0; kb < KB2; ++kb) {
-        bt.b[kb] = (e >= 0 && kb < KB) ? load32_stream(wrow + kb * 128) : zero8i;
-        bt.sw[kb] = (e >= 0 && kb < KB) ? proj_scale(a.w2, e, n, kb) : 0.0f;
+        bt.b[kb] = (e >= 0 && kb < KB) ? load_wraw<WF>(wrow, a.w2.K, kb, grp) : zero_wraw<WF>();
+        bt.sw[kb] = (e >= 0 && kb < KB) ? proj_scale<WF>(a.w2, e, n, kb) : 0.0f;
     }
 }
 
-// KB2 = upper bound of the 128-column K blocks of the down projection
-// (I <= 128 * KB2); the runtime count KB guards every block.
-template <int KB2>
+// WF = weight format; KB2 = upper bound of the 128-column K blocks of the
+// down projection (I <= 128 * KB2); the runtime count KB guards every block.
+template <int WF, int KB2>
 __global__ __launch_bounds__(kDnThreads) void fp8_down_decode_kernel(DownArgs a) {
     __shared__ DownLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -256,8 +259,8 @@ __global__ __launch_bounds__(kDnThreads) void fp8_down_decode_kernel(DownArgs a)
     for (int i = threadIdx.x; i < a.pairs * 8; i += kDnThreads) s.part[i / 8][i % 8] = 0.0f;
     const int num_active = a.grouping->num_active;
     const int batches = (num_active + 1) / 2;
-    DownBatch<KB2> cur;
-    if (wave < batches) load_down_batch<KB2>(a, num_active, wave, n0, col, grp, KB, cur);
+    DownBatch<WF, KB2> cur;
+    if (wave < batches) load_down_batch<WF, KB2>(a, num_active, wave, n0, col, grp, KB, cur);
     if (a.quantize_hidden) {
 #pragma unroll
         for (int q = 0; q < kQuantPasses; ++q) {
@@ -289,9 +292,9 @@ __global__ __launch_bounds__(kDnThreads) void fp8_down_decode_kernel(DownArgs a)
         for (int kb = 0; kb < KB2; ++kb)
             af[kb] = (arow0 >= 0 && kb < KB) ? load32(hq + (int64_t)arow0 * I + kb * 128 + grp * 32) : zero8i;
         // the next batch's weights go out after this batch's activation loads
-        DownBatch<KB2> nxt;
+        DownBatch<WF, KB2> nxt;
         const bool more = bi + kDnWaves < batches;
-        if (more) load_down_batch<KB2>(a, num_active, bi + kDnWaves, n0, col, grp, KB, nxt);
+        if (more) load_down_batch<WF, KB2>(a, num_active, bi + kDnWaves, n0, col, grp, KB, nxt);
         for (int pass = 0; pass < passes; ++pass) {
             if (pass > 0) {
                 const int ar = a_row(pass, col);
@@ -310,7 +313,7 @@ __global__ __launch_bounds__(kDnThreads) void fp8_down_decode_kernel(DownArgs a)
 #pragma unroll
             for (int kb = 0; kb < KB2; ++kb) {
                 if (kb < KB) {
-                    const v4f d = mfma_fp8(af[kb], cur.b[kb], zero);
+                    const v4f d = mfma_w<WF>(a_operand<WF>(af[kb]), cur.b[kb], zero);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float sxv = crow[r] >= 0 ? hs[(int64_t)crow[r] * KB + kb] : 0.0f;
@@ -344,24 +347,42 @@ __global__ __launch_bounds__(kDnThreads) void fp8_down_decode_kernel(DownArgs a)
     }
 }
 
-void launch_fp8_gateup_decode(const GateUpArgs& a, int max_active, hipStream_t stream) {
+namespace {
+
+template <int WF>
+void launch_gateup_format(const GateUpArgs& a, int max_active, hipStream_t stream) {
     const dim3 grid(max_active, a.w13.N / 2 / 16), block(kUpThreads);
     const int kbw = (a.w13.K / 128 + kUpWaves - 1) / kUpWaves;
-    if (kbw <= 1) hipLaunchKernelGGL(fp8_gateup_decode_kernel<1>, grid, block, 0, stream, a);
-    else if (kbw <= 2) hipLaunchKernelGGL(fp8_gateup_decode_kernel<2>, grid, block, 0, stream, a);
-    else if (kbw <= 4) hipLaunchKernelGGL(fp8_gateup_decode_kernel<4>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(fp8_gateup_decode_kernel<8>, grid, block, 0, stream, a);
+    if (kbw <= 1) hipLaunchKernelGGL((fp8_gateup_decode_kernel<WF, 1>), grid, block, 0, stream, a);
+    else if (kbw <= 2) hipLaunchKernelGGL((fp8_gateup_decode_kernel<WF, 2>), grid, block, 0, stream, a);
+    else if (kbw <= 4) hipLaunchKernelGGL((fp8_gateup_decode_kernel<WF, 4>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((fp8_gateup_decode_kernel<WF, 8>), grid, block, 0, stream, a);
+}
+
+template <int WF>
+void launch_down_format(const DownArgs& a, hipStream_t stream) {
+    const dim3 grid(a.w2.N / 8), block(kDnThreads);
+    const int kb = a.w2.K / 128;
+    if (kb <= 2) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 2>), grid, block, 0, stream, a);
+    else if (kb <= 4) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 4>), grid, block, 0, stream, a);
+    else if (kb <= 6) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 6>), grid, block, 0, stream, a);
+    else if (kb <= 8) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 8>), grid, block, 0, stream, a);
+    else if (kb <= 16) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 16>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 32>), grid, block, 0, stream, a);
+}
+
+}  // namespace
+
+void launch_fp8_gateup_decode(const GateUpArgs& a, int max_active, hipStream_t stream) {
+    if (a.w13.wfmt == kWfInt4) launch_gateup_format<kWfInt4>(a, max_active, stream);
+    else if (a.w13.wfmt == kWfInt6) launch_gateup_format<kWfInt6>(a, max_active, stream);
+    else launch_gateup_format<kWfFp8>(a, max_active, stream);
 }
 
 void launch_fp8_down_decode(const DownArgs& a, hipStream_t stream) {
-    const dim3 grid(a.w2.N / 8), block(kDnThreads);
-    const int kb = a.w2.K / 128;
-    if (kb <= 2) hipLaunchKernelGGL(fp8_down_decode_kernel<2>, grid, block, 0, stream, a);
-    else if (kb <= 4) hipLaunchKernelGGL(fp8_down_decode_kernel<4>, grid, block, 0, stream, a);
-    else if (kb <= 6) hipLaunchKernelGGL(fp8_down_decode_kernel<6>, grid, block, 0, stream, a);
-    else if (kb <= 8) hipLaunchKernelGGL(fp8_down_decode_kernel<8>, grid, block, 0, stream, a);
-    else if (kb <= 16) hipLaunchKernelGGL(fp8_down_decode_kernel<16>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(fp8_down_decode_kernel<32>, grid, block, 0, stream, a);
+    if (a.w2.wfmt == kWfInt4) launch_down_format<kWfInt4>(a, stream);
+    else if (a.w2.wfmt == kWfInt6) launch_down_format<kWfInt6>(a, stream);
+    else launch_down_format<kWfFp8>(a, stream);
 }
 
 }  // namespace dmoe

@@ -5,12 +5,17 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "wfmt.hpp"
 
 namespace dmoe {
 
-// Scale of weight row n, 128-column block kb of expert e.
+// Scale of weight row n, 128-column block kb of expert e (fp32 for E4M3
+// banks, fp16 for the integer formats).
+template <int WF = kWfFp8>
 __device__ __forceinline__ float proj_scale(const Fp8Proj& p, int e, int n, int kb) {
-    return p.s[(int64_t)e * p.s_se + (int64_t)(n / p.n_div) * p.s_sn + (int64_t)(kb / p.kb_div) * p.s_sk];
+    const int64_t i = (int64_t)e * p.s_se + (int64_t)(n / p.n_div) * p.s_sn + (int64_t)(kb / p.kb_div) * p.s_sk;
+    if constexpr (WF == kWfFp8) return p.s[i];
+    else return f16_to_f32(((const uint16_t*)p.s)[i]);
 }
 
 // 32 contiguous bytes (16-byte aligned) as one FP8 MFMA operand.

@@ -16,8 +16,11 @@ constexpr int kDownQuantPairs = 16;
 // Activation bytes the gate/up kernel stages in LDS at entry (all rows a call reads).
 constexpr int kStageBytes = 16384;
 
-// One FP8 projection bank [E, N, K] (K contiguous) with fp32 scales addressed
-// as s[e*s_se + (n / n_div)*s_sn + (kb / kb_div)*s_sk] for 128-column block kb.
+// One projection bank [E, N, K] of the FP8-MFMA kernels, rows at
+// w + e*w_se + n*w_sn, scales addressed as
+// s[e*s_se + (n / n_div)*s_sn + (kb / kb_div)*s_sk] for 128-column block kb.
+// wfmt (wfmt.hpp): kWfFp8 E4M3 bytes with fp32 scales, or kWfInt4 / kWfInt6
+// integer codes with fp16 scales (then n_div = kb_div = 1).
 struct Fp8Proj {
     const uint8_t* w;
     const float* s;
@@ -25,6 +28,7 @@ struct Fp8Proj {
     int64_t s_se, s_sn, s_sk;
     int32_t n_div, kb_div;
     int32_t N, K;
+    int32_t wfmt;
 };
 
 // Where a decode kernel takes its routes from: caller ids, or router logits
@@ -230,6 +234,9 @@ bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k
 // Launches the fused decode; false (nothing enqueued) when the device cannot
 // hold the grid the kernel needs.
 bool launch_fp8_fused_decode(const FusedDecodeArgs& a, hipStream_t stream);
+// Its integer-weight instances (fp8_fused_w4.hip, fp8_fused_w6.hip).
+bool launch_fused_int4(const FusedDecodeArgs& a, hipStream_t stream);
+bool launch_fused_int6(const FusedDecodeArgs& a, hipStream_t stream);
 
 void launch_moe_prep(const PrepArgs& a, hipStream_t stream);
 int quantize_blocks(const QuantArgs& a);

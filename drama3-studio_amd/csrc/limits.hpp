@@ -26,6 +26,10 @@ constexpr int kGroupM = 64;
 constexpr int kFusedMaxPairs = 64;
 constexpr int kFusedMaxI = 1024;
 
+// Weight formats of the FP8-MFMA kernels (wfmt.hpp): E4M3 bytes, or 4- / 6-bit
+// integer codes with group-128 fp16 scales.
+enum { kWfFp8 = 0, kWfInt4 = 1, kWfInt6 = 2 };
+
 // Expert grouping of the route pairs of one decode call, written once by the
 // prep kernel and read by both decode kernels: the ascending active experts
 // and, per active expert, a bitmask of its pairs (pair p <-> bit p).

@@ -17,7 +17,8 @@ from . import _lib
 from .formats import QuantizedStore
 from .offload import MAX_PAIRS, _device_of, device_state
 
-MODE_NAMES = ("W4A16-GPTQ", "INT8-ConvRot/BF16", "W6A8/BF16", "W4A8-Codebook/BF16")
+MODE_NAMES = ("W4A16-GPTQ", "INT8-ConvRot/BF16", "W6A8/BF16", "W4A8-Codebook/BF16", "W4A8-G128/FP8",
+              "W6A8-G128/FP8")
 
 
 class QuantProj(ctypes.Structure):
@@ -33,7 +34,7 @@ class QuantBank(ctypes.Structure):
 
 def _k_of(bank: Tensor, mode: int) -> int:
     cols = bank.shape[-1]
-    return cols * 8 if mode == 0 else cols if mode == 1 else cols * 4 // 3 if mode == 2 else cols * 2
+    return cols * 8 if mode == 0 else cols if mode == 1 else cols * 4 // 3 if mode in (2, 5) else cols * 2
 
 
 def _bytes_stride(t: Tensor, dim: int) -> int:
@@ -108,7 +109,7 @@ class QuantizedExpertBackend:
     combine.  Never synchronizes the host."""
 
     def __init__(self, mode: int) -> None:
-        if mode not in (0, 1, 2, 3):
+        if mode not in (0, 1, 2, 3, 4, 5):
             raise ValueError("Unknown quantized bank format")
         self.mode = mode
         self.quantized_mode = MODE_NAMES[mode]
@@ -174,3 +175,34 @@ class QuantizedExpertBackend:
         return out
 
     forward_decode_pairs = forward_pairs
+
+    def forward_routed(self, x: Tensor, logits: Tensor, top_k: int, staged: QuantizedStore, *,
+                       renormalize: bool = True, weights_dtype: torch.dtype | None = None,
+                       out: Tensor | None = None):
+        """Router + routed experts in one call with no host sync (graph
+        capturable): returns (out [T, H], weights [T, top_k], ids [T, top_k])."""
+        if x.ndim != 2 or logits.ndim != 2 or logits.shape[0] != x.shape[0]:
+            raise ValueError("Expected x [T, H] and router logits [T, E]")
+        if staged.mode != self.mode:
+            raise ValueError(f"Bank is mode {staged.mode}, backend is mode {self.mode}")
+        if x.shape[-1] != staged.hidden or x.stride(-1) != 1:
+            raise ValueError(f"Expected hidden rows [N, {staged.hidden}] with contiguous columns")
+        if logits.dtype != torch.float32 or logits.stride(-1) != 1:
+            logits = logits.float().contiguous()
+        device = _device_of(x)
+        tokens = x.shape[0]
+        out = torch.empty_like(x) if out is None else out
+        ids = torch.empty((tokens, top_k), dtype=torch.int64, device=device)
+        weights = torch.empty((tokens, top_k), dtype=weights_dtype or x.dtype, device=device)
+        if tokens == 0:
+            return out, weights, ids
+        bank = bank_struct(staged)
+        lib = _lib.library()
+        state = device_state(device)
+        ws = state.workspace_for(lib.dmoe_quant_workspace_bytes(ctypes.byref(bank), tokens, tokens * top_k))
+        _lib.check(lib.dmoe_quant_moe_layer(
+            ctypes.byref(bank), _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), tokens, _lib.ptr(logits),
+            logits.stride(0), top_k, int(renormalize), _lib.ptr(ids), _lib.ptr(weights),
+            _lib.dtype_code(weights.dtype), _lib.ptr(out), _lib.dtype_code(out.dtype), out.stride(0), _lib.ptr(ws),
+            ws.numel(), _lib.ptr(state.status), _lib.stream_handle(device)))
+        return out, weights, ids

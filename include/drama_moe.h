@@ -303,9 +303,21 @@ DMOE_API int dmoe_fp8_moe_layer_noalloc(const DmoeFp8Bank* bank, const void* x, 
  *                        scale = aux uint8 [E, N, K/16 + 4] (E4M3 relative
  *                        scale per 16 values, then the fp32 channel scale);
  *   mode 3 W4A8 book:    weight int8 [E, N, K/2], aux uint8 [E, N, K/16 + 8]
- *                        whose rows 0..15 hold the 16 fp32 levels at byte K/16+4.
+ *                        whose rows 0..15 hold the 16 fp32 levels at byte K/16+4;
+ *   mode 4 W4A8-g128:    weight int8 [E, N, K/2] (even k low nibble), level =
+ *                        code - 8, scale fp16 [E, N, K/128];
+ *   mode 5 W6A8-g128:    weight int8 [E, N, 3K/4] (the mode-2 planes), level =
+ *                        code - 32, scale fp16 [E, N, K/128].
+ * Modes 4 and 5 have no reference counterpart: they are the W4A8 / W6A8
+ * variants with one scale per (row, 128-group), computed on activations
+ * quantized to FP8 per token (scale = max(amax, 1e-10) * fl(1/448) over the
+ * row), with the FP8 W8A8 contract otherwise (block fma chain, gate/up
+ * rounded through the activation dtype, FP8 128-group hidden, slot-order
+ * combine); they run on the FP8 decode kernels, calls above 256 route pairs
+ * as consecutive decode calls.
  * Strides are in bytes (zeros: int32 elements per expert).  K is a multiple
- * of 128 (mode 0) or 256 (modes 1-3), at most 4096; N a multiple of 16. */
+ * of 128 (modes 0, 4, 5) or 256 (modes 1-3), at most 4096 (modes 0-3) or
+ * 8192 (modes 4, 5); N a multiple of 16. */
 typedef struct DmoeQuantProj {
     const void* weight;
     const void* scale;
@@ -320,7 +332,7 @@ typedef struct DmoeQuantBank {
     DmoeQuantProj w13; /* [E, 2I, H]: gate rows 0..I-1, up rows I..2I-1 */
     DmoeQuantProj w2;  /* [E, H, I] */
     int32_t experts;
-    int32_t mode;      /* 0..3 as above */
+    int32_t mode;      /* 0..5 as above */
 } DmoeQuantBank;
 
 /* ConvRot activation quantization: rows x [rows, k] (k % 256 == 0) rotated in
@@ -363,6 +375,22 @@ DMOE_API int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, in
                                     int top_k, void* out, int out_dtype, int64_t out_row_stride,
                                     float* out_pairs, void* workspace, size_t workspace_bytes,
                                     int* status, void* stream);
+
+/* Whole MoE routed-expert layer of a packed bank: router softmax/top-k of
+ * logits [tokens, experts] fp32 (as dmoe_route_topk; the routing is also
+ * written to ids_out [tokens, top_k] int64 and weights_out in weights_dtype),
+ * then the routed experts and slot-order combine as dmoe_quant_moe_forward
+ * with one row per token.  Modes 4 and 5 route inside the single-launch
+ * decode when the call fits it.  No host sync, so decode steps can be
+ * captured in hipGraphs.  Workspace: dmoe_quant_workspace_bytes(bank, tokens,
+ * tokens * top_k).  Replaces the router of backbone_graph.py:317-323 followed
+ * by QuantizedExpertBackend.forward (quantized_kernels.py:217-229). */
+DMOE_API int dmoe_quant_moe_layer(const DmoeQuantBank* bank, const void* x, int x_dtype,
+                                  int64_t x_row_stride, int tokens, const float* logits,
+                                  int64_t logits_row_stride, int top_k, int renormalize,
+                                  int64_t* ids_out, void* weights_out, int weights_dtype, void* out,
+                                  int out_dtype, int64_t out_row_stride, void* workspace,
+                                  size_t workspace_bytes, int* status, void* stream);
 
 #ifdef __cplusplus
 }

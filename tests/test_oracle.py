@@ -630,3 +630,73 @@ def test_g128_layer_combines_in_slot_order():
     for t in range(2):
         pairs = orc.fp8_expert_pairs(banks["w13"], banks["w2"], x[t], ids[t], w[t], x_group=H)
         np.testing.assert_array_equal(out[t], orc.bf16_round((pairs[0] + pairs[1]).astype(np.float32)))
+
+
+# ------------------------------------------- torch-CPU baseline restatements
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4, 5])
+def test_torch_cpu_layer_matches_the_oracle(mode):
+    """The torch-CPU dequantize-then-matmul lane that bench.py times as the
+    reference's CPU path for the packed formats agrees with the C oracle:
+    modes 0-3 with quant_projection (projection_torch semantics), modes 4-5
+    with the O2 reading of the group-128 formats."""
+    from drama_moe.formats import random_quantized_bank
+    from oracle import torch_cpu
+
+    g = torch.Generator().manual_seed(40 + mode)
+    store = random_quantized_bank(mode, 6, 512, 256, asymmetric=mode == 0, generator=g)
+    x = torch.randn(3, 512, generator=g).bfloat16()
+    ids, w = orc.route_topk(torch.randn(3, 6, generator=g).numpy(), 4)
+    weights = torch.from_numpy(w).bfloat16()
+    got = torch_cpu.layer(store, x, torch.from_numpy(ids), weights).float().numpy()
+    if mode < 4:
+        def bank(prefix, n, k):
+            zeros = getattr(store, prefix + "_zeros")
+            return orc.QuantBank(mode, getattr(store, prefix + "_weight").numpy(),
+                                 getattr(store, prefix + "_scale_inv").numpy(), n, k,
+                                 None if zeros is None else zeros.numpy())
+        b13, b2 = bank("w13", 512, 512), bank("w2", 512, 256)
+        flat = ids.reshape(-1)
+        up = orc.quant_projection(b13, np.repeat(x.float().numpy(), 4, 0), flat, np.ones(flat.size, np.float32))
+        act = orc.bf16_round(orc.bf16_round(orc.silu(up[:, :256])) * up[:, 256:])
+        part = orc.quant_projection(b2, act, flat, weights.float().numpy().reshape(-1), weighted=True)
+        want = orc.bf16_round(part.reshape(3, 4, -1).sum(1, dtype=np.float32))
+    else:
+        # group-128 formats: level * fp16 scale, unquantized activations
+        def dense(prefix, k):
+            from oracle import torch_cpu as tc
+            wt, sc = getattr(store, prefix + "_weight"), getattr(store, prefix + "_scale_inv")
+            return np.stack([tc.dequantize(mode, wt[e], sc[e], k).numpy() for e in range(6)])
+        m13, m2 = dense("w13", 512), dense("w2", 256)
+        want = np.zeros((3, 512), np.float64)
+        for t in range(3):
+            for j in range(4):
+                e = ids[t, j]
+                gu = orc.bf16_round((m13[e].astype(np.float64) @ x[t].float().numpy()).astype(np.float32))
+                act = orc.bf16_round(orc.bf16_round(orc.silu(gu[:256])) * gu[256:])
+                want[t] += orc.bf16_round((m2[e].astype(np.float64) @ act).astype(np.float32)) * w[t, j]
+        want = orc.bf16_round(want.astype(np.float32))
+        # and the level decode itself against the packing helpers' codes
+        from drama_moe.formats import nibble_pack, six_pack
+        codes = torch.randint(0, 16 if mode == 4 else 64, (32, 256), generator=g)
+        packed = (nibble_pack if mode == 4 else six_pack)(codes)
+        ones = torch.ones(32, 2, dtype=torch.float16)
+        level = torch_cpu.dequantize(mode, packed, ones, 256)
+        assert torch.equal(level, codes.float() - (8 if mode == 4 else 32))
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 2e-2
+
+
+def test_torch_cpu_fp8_layer_is_o2():
+    from oracle import torch_cpu
+
+    g = torch.Generator().manual_seed(12)
+    bank = random_fp8_bank(4, 256, 128, generator=g)
+    x = torch.randn(2, 256, generator=g).bfloat16()
+    ids = np.array([[0, 3], [2, 2]])
+    w = np.array([[0.6, 0.4], [0.5, 0.5]], np.float32)
+    got = torch_cpu.fp8_layer(bank, x, torch.from_numpy(ids), torch.from_numpy(w)).float().numpy()
+    b13 = orc.Fp8Bank(bank.w13_weight.view(torch.uint8).numpy(), bank.w13_scale_inv.numpy())
+    b2 = orc.Fp8Bank(bank.w2_weight.view(torch.uint8).numpy(), bank.w2_scale_inv.numpy())
+    want = orc.o2_moe_forward(b13, b2, x.float().numpy(), ids, w)
+    assert np.mean(got == want) > 0.95
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-2
