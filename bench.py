@@ -74,6 +74,7 @@ def decode_graph_us(backend, xs, logits, banks, outs, stream, steps: int, warmup
     def step(i):
         backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
 
+    stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the current stream
     with torch.cuda.stream(stream):  # workspace and descriptor caches, outside capture
         for i in range(layers):
             step(i)
@@ -187,29 +188,41 @@ def run_gpu(steps: int, warmup: int):
     }
 
 
-def pmc_pass(rounds: int = 8, copy_mib: int = 256):
+def pmc_pass(workload: str = "decode", rounds: int = 8, copy_mib: int = 256):
     """Eager workload for hardware-counter runs: `rounds` passes of the
-    decode step over the layer banks, then a plain fp32 copy of `copy_mib`
-    MiB (read once, written once) whose counter readings calibrate the
-    bytes-per-count of the HBM counters."""
+    decode step over the layer banks (or `rounds` 2048-token prefill layer
+    calls with per-token activation scales), then a plain fp32 copy of
+    `copy_mib` MiB (read once, written once) whose counter readings calibrate
+    the bytes-per-count of the HBM counters."""
     import torch
 
     from drama_moe.offload import HipExpertBackend
 
     device = torch.device("cuda", 0)
-    banks = [make_layer_bank(layer, device) for layer in range(LAYERS)]
-    xs, logits, outs = decode_inputs(1, device, SEED)
-    backend = HipExpertBackend()
-    for _ in range(rounds):
-        for i in range(LAYERS):
-            backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
+    if workload == "prefill":
+        bank = make_layer_bank(LAYERS, device)
+        g = torch.Generator(device=device).manual_seed(PREFILL_SEED)
+        x = torch.randn(PREFILL_TOKENS, HIDDEN, device=device, generator=g).bfloat16()
+        logits = zipf_logits(PREFILL_TOKENS, EXPERTS, PREFILL_SEED).to(device)
+        out = torch.empty_like(x)
+        backend = HipExpertBackend(x_group="token")
+        for _ in range(rounds):
+            backend.forward_routed(x, logits, TOP_K, bank, out=out)
+    else:
+        banks = [make_layer_bank(layer, device) for layer in range(LAYERS)]
+        xs, logits, outs = decode_inputs(1, device, SEED)
+        backend = HipExpertBackend()
+        for _ in range(rounds):
+            for i in range(LAYERS):
+                backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
     src = torch.ones(copy_mib << 18, device=device)
     dst = torch.empty_like(src)
     for _ in range(4):
         torch.mul(src, 1.0, out=dst)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_pass": {"decode_steps": rounds * LAYERS, "copy_bytes_read": src.numel() * 4,
-                                   "copy_bytes_written": dst.numel() * 4}}), flush=True)
+    print(json.dumps({"pmc_pass": {"workload": workload, "calls": rounds * (1 if workload == "prefill" else LAYERS),
+                                   "copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}}),
+          flush=True)
 
 
 PREFILL_TOKENS = 2048
@@ -296,6 +309,7 @@ def quant_expert_bytes(mode: int) -> int:
 def _graph_time_us(fn, steps_per_graph: int, replays: int, stream) -> float:
     import torch
 
+    stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the current stream
     with torch.cuda.stream(stream):
         fn()
     torch.cuda.synchronize()
@@ -519,8 +533,8 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-prefill", action="store_true")
     parser.add_argument("--no-quant", action="store_true")
-    parser.add_argument("--pmc-pass", action="store_true",
-                        help="run the eager counter-collection workload instead of the benchmark")
+    parser.add_argument("--pmc-pass", nargs="?", const="decode", choices=("decode", "prefill"),
+                        help="run the eager counter-collection workload (decode or prefill) instead of the benchmark")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path is built and "
@@ -530,7 +544,7 @@ def main():
         print("bench.py runs as a single process on one GPU", file=sys.stderr)
         sys.exit(2)
     if args.pmc_pass:
-        pmc_pass()
+        pmc_pass(args.pmc_pass)
         return
     steps = max(1, args.steps)
     gpu = run_gpu(steps, args.warmup)

@@ -22,7 +22,7 @@
 //            16-byte stores of the fp32 partial rows of the original pairs.
 //
 // Persistent launch: one workgroup per CU walks its list of tiles as one
-// continuous stream of 128-column K blocks.  The work is split by role: two
+// continuous stream of 128-column K blocks.  The work is split by role: four
 // copy waves issue every global -> LDS copy (a CU moves only about 50 bytes
 // per clock into LDS, so issuing a block's 40 KB stalls the issuing wave for
 // longer than the block's MFMAs take) and four waves only multiply and run the
@@ -54,9 +54,9 @@ constexpr int kGThreads = (kMmaWaves + kCopyWaves) * kWave;
 constexpr int kXcds = 8;
 constexpr int kTileN = 256;                         // weight rows of a tile
 constexpr int kStages = 3;                          // K-block ring depth
-constexpr int kAInst = kGroupM / 8 / kCopyWaves;    // A copy instructions per copy wave per block (4)
-constexpr int kBInst = kTileN / 8 / kCopyWaves;     // B copy instructions per copy wave per block (16)
-constexpr int kScaleInst = 4 / kCopyWaves;          // weight-scale (and row-scale) copies per copy wave (2)
+constexpr int kAInst = kGroupM / 8 / kCopyWaves;    // A copy instructions per copy wave per block (2)
+constexpr int kBInst = kTileN / 8 / kCopyWaves;     // B copy instructions per copy wave per block (8)
+constexpr int kScaleInst = 4 / kCopyWaves;          // weight-scale (and row-scale) copies per copy wave (1)
 constexpr int kCopies = kAInst + kBInst + 2 * kScaleInst;  // vector-memory instructions per copy wave per block
 constexpr int kLeanCopies = kAInst + kBInst;                // the same without scale copies
 constexpr int kChunk = 16;                          // tiles whose metadata a workgroup holds at once
