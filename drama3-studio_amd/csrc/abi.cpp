@@ -495,6 +495,13 @@ void check_quant_rows(const void* x, int x_dtype, int64_t x_row_stride, int rows
     require(row_div >= 1 && (int64_t)(pairs - 1) / row_div < rows, "pairs read past the activation rows");
 }
 
+// A grouped packed projection: the tiled W4A16 GEMM where its tile shape
+// fits, else the column-group kernel.
+void launch_projection(const dmoe::QuantProjArgs& q, int max_active, hipStream_t stream) {
+    if (dmoe::w4a16_grouped_fits(q)) dmoe::launch_w4a16_grouped(q, max_active, stream);
+    else dmoe::launch_quant_projection(q, max_active, stream);
+}
+
 // Permutation with the active-expert list (the grouping of every packed call).
 void quant_group(const void* ids, int ids_dtype, int pairs, int experts, const QuantWorkspace& ws, int* status,
                  hipStream_t stream) {
@@ -1005,7 +1012,7 @@ int dmoe_quant_projection(const DmoeQuantProj* proj, int experts, int mode, cons
         q.out = out;
         q.out_row_stride = out_row_stride;
         q.status = status;
-        dmoe::launch_quant_projection(q, std::min(pairs, experts), st);
+        launch_projection(q, std::min(pairs, experts), st);
     });
 }
 
@@ -1060,7 +1067,7 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
             up.gateup = 1;
             up.act = ws.act;
             up.status = status;
-            dmoe::launch_quant_projection(up, max_active, st);
+            launch_projection(up, max_active, st);
         }
 
         if (small_dn) {
@@ -1081,7 +1088,7 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
         dn.out = out_pairs ? out_pairs : ws.partial;
         dn.out_row_stride = H;
         dn.status = status;
-        dmoe::launch_quant_projection(dn, max_active, st);
+        launch_projection(dn, max_active, st);
 
         if (out_pairs) {
             const dmoe::CombineArgs za{out_pairs, H, ids, ids_dtype, E, pairs, 1, H, nullptr, DMOE_F32, 0};

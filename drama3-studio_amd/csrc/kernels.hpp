@@ -312,6 +312,10 @@ struct QuantProjArgs {
 
 void launch_rotate_quant(const RotateArgs& a, hipStream_t stream);
 void launch_quant_projection(const QuantProjArgs& a, int max_active, hipStream_t stream);
+// Tiled grouped W4A16 projection (w4a16_grouped.hip): mode 0 with gate/up
+// I % 64 == 0, or plain N % 128 == 0.
+bool w4a16_grouped_fits(const QuantProjArgs& a);
+void launch_w4a16_grouped(const QuantProjArgs& a, int max_active, hipStream_t stream);
 
 // Small packed calls (at most 64 route pairs): two launches that group the
 // pairs themselves from the route ids (no permutation launch).

@@ -326,3 +326,26 @@ def test_full_size_decode_and_prefill(cuda, mode):
         out = backend.forward(x.to(cuda), torch.from_numpy(ids).to(cuda), weights.to(cuda), dev)
         expected = oracle_layer(store, x.float().numpy()[pick], ids[pick], weights.float().numpy()[pick])
         assert rel_inf(out.float().cpu().numpy()[pick], expected) < TOL, tokens
+
+
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float16])
+def test_w4a16_tiled_prefill_every_token(cuda, x_dtype):
+    """The tiled W4A16 GEMM at the layer shape (E=128, H=2048, I=768, top-8,
+    asymmetric GPTQ banks): every token of a 512-token call against the
+    torch-CPU dequantize-then-matmul restatement of projection_torch /
+    QuantizedExpertBackend.forward (quantized_kernels.py:48-112, 217-229),
+    with bf16 and fp16 activations (fp16 rounds the gate/up weights to fp16)."""
+    from oracle import torch_cpu
+
+    print_case("w4a16 tiled prefill", x_dtype)
+    g = torch.Generator().manual_seed(20261205)
+    store = random_quantized_bank(0, 128, 2048, 768, asymmetric=True, generator=g)
+    x = torch.randn(512, 2048, generator=g).to(x_dtype)
+    ids, w = orc.route_topk(torch.randn(512, 128, generator=g).numpy(), 8)
+    ids = torch.from_numpy(ids)
+    weights = torch.from_numpy(w).bfloat16()
+    out = quantized.QuantizedExpertBackend(0).forward(x.to(cuda), ids.to(cuda), weights.to(cuda),
+                                                      to_device(store, cuda))
+    expected = torch_cpu.layer(store, x, ids, weights)
+    assert out.dtype == x_dtype
+    assert rel_inf(out.float().cpu().numpy(), expected.float().numpy()) < TOL
