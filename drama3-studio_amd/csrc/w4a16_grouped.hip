@@ -76,21 +76,37 @@ __device__ __forceinline__ W4Raw w4_fetch(const QuantProjArgs& a, const uint8_t*
     return r;
 }
 
-// The four MFMA B operands (8 values each) of a lane's 32 codes.
+// (u & mask) | magic in one instruction (the compiler splits it: two
+// literals exceed what one VOP3 instruction takes; magic lives in a VGPR).
+__device__ __forceinline__ uint32_t and_or(uint32_t u, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(u), "s"(mask), "v"(magic));
+    return r;
+}
+
 template <bool F16>
 __device__ __forceinline__ void w4_dequant(const W4Raw& r, int n, v4i (&op)[4]) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));  // keep it in a VGPR
     const float scale = f16_to_f32((uint16_t)r.scale);
-    const int zp = (int)((r.zeros >> (4 * (n % 8))) & 15u);
-    const float bias = -(float)zp * scale;  // exact: 4 x 11 significant bits
+    const float zp = (float)((r.zeros >> (4 * (n % 8))) & 15u);
+    const float s1 = scale, b1 = -(1024.0f + zp) * scale;                      // codes in bits 0-3
+    const float s16 = scale * 0.0625f, b16 = -(64.0f + zp) * scale;             // codes in bits 4-7
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const uint32_t u = (uint32_t)r.codes[t];
+        const uint32_t hiu = __builtin_amdgcn_perm(u, u, 0x07030501u);  // bytes 1, 3 -> 0, 2
+        const h2 c04 = __builtin_bit_cast(h2, and_or(u, 0x000F000Fu, magic));
+        const h2 c15 = __builtin_bit_cast(h2, and_or(u, 0x00F000F0u, magic));
+        const h2 c26 = __builtin_bit_cast(h2, and_or(hiu, 0x000F000Fu, magic));
+        const h2 c37 = __builtin_bit_cast(h2, and_or(hiu, 0x00F000F0u, magic));
+        const float v[8] = {fmaf((float)c04[0], s1, b1), fmaf((float)c15[0], s16, b16),
+                            fmaf((float)c26[0], s1, b1), fmaf((float)c37[0], s16, b16),
+                            fmaf((float)c04[1], s1, b1), fmaf((float)c15[1], s16, b16),
+                            fmaf((float)c26[1], s1, b1), fmaf((float)c37[1], s16, b16)};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float v0 = fmaf((float)((u >> (8 * i)) & 15u), scale, bias);      // exact
-            const float v1 = fmaf((float)((u >> (8 * i + 4)) & 15u), scale, bias);
-            op[t][i] = (int)pack2(v0, v1, F16);
-        }
+        for (int i = 0; i < 4; ++i) op[t][i] = (int)pack2(v[2 * i], v[2 * i + 1], F16);
     }
 }
 
