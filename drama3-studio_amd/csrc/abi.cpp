@@ -951,6 +951,81 @@ int dmoe_fp8_moe_layer_noalloc(const DmoeFp8Bank* bank, const void* x, int x_dty
     });
 }
 
+// ------------------------------------------------------ MoE block (router GEMV, shared expert)
+
+namespace {
+
+bool bf16_rows_ok(const void* p, int64_t stride, int width, int rows) {
+    return p != nullptr && reinterpret_cast<uintptr_t>(p) % 16 == 0 && stride >= width && (stride * 2) % 16 == 0 &&
+           rows >= 1;
+}
+
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                   hipSuccess)
+        return 1;
+    return cus > 0 ? cus : 1;
+}
+
+}  // namespace
+
+int dmoe_moe_block_pre(const void* x, int64_t x_row_stride, int tokens, int hidden, const void* router_w,
+                       int64_t router_row_stride, int experts, const void* shared_gate_w, const void* gate_proj,
+                       int64_t gate_row_stride, const void* up_proj, int64_t up_row_stride, int shared_inter,
+                       float* logits, int64_t logits_row_stride, void* shared_gate_out, void* shared_act,
+                       int64_t act_row_stride, void* stream) {
+    return checked([&] {
+        require(tokens >= 1, "tokens must be positive");
+        require(dmoe::block_fits(hidden, shared_inter),
+                "hidden and shared_inter must be multiples of 8 in [8, 4096]");
+        require(experts >= 1 && experts <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        require(bf16_rows_ok(x, x_row_stride, hidden, tokens), "x must be bf16 [tokens, hidden], 16-byte aligned rows");
+        require(bf16_rows_ok(router_w, router_row_stride, hidden, experts),
+                "router weight must be bf16 [experts, hidden], 16-byte aligned rows");
+        require(bf16_rows_ok(shared_gate_w, hidden, hidden, 1), "shared gate weight must be bf16 [hidden], 16-byte aligned");
+        require(bf16_rows_ok(gate_proj, gate_row_stride, hidden, shared_inter) &&
+                    bf16_rows_ok(up_proj, up_row_stride, hidden, shared_inter),
+                "shared gate_proj / up_proj must be bf16 [shared_inter, hidden], 16-byte aligned rows");
+        require(logits != nullptr && logits_row_stride >= experts, "logits must be fp32 [tokens, experts]");
+        require(shared_gate_out != nullptr, "shared gate output is required");
+        require(bf16_rows_ok(shared_act, act_row_stride, shared_inter, tokens),
+                "shared activation must be bf16 [tokens, shared_inter], 16-byte aligned rows");
+        dmoe::BlockPreArgs a{static_cast<const uint16_t*>(x), x_row_stride, tokens, hidden, experts, shared_inter,
+                             static_cast<const uint16_t*>(router_w), router_row_stride,
+                             static_cast<const uint16_t*>(shared_gate_w), static_cast<const uint16_t*>(gate_proj),
+                             gate_row_stride, static_cast<const uint16_t*>(up_proj), up_row_stride, logits,
+                             logits_row_stride, static_cast<uint16_t*>(shared_gate_out),
+                             static_cast<uint16_t*>(shared_act), act_row_stride};
+        dmoe::launch_block_pre(a, device_cus(), as_stream(stream));
+    });
+}
+
+int dmoe_moe_block_post(const void* shared_act, int64_t act_row_stride, int tokens, int shared_inter,
+                        const void* down_proj, int64_t down_row_stride, int hidden, const void* shared_gate,
+                        const void* experts_out, int64_t experts_row_stride, const void* residual,
+                        int64_t residual_row_stride, void* out, int64_t out_row_stride, void* stream) {
+    return checked([&] {
+        require(tokens >= 1, "tokens must be positive");
+        require(dmoe::block_fits(hidden, shared_inter),
+                "hidden and shared_inter must be multiples of 8 in [8, 4096]");
+        require(bf16_rows_ok(shared_act, act_row_stride, shared_inter, tokens),
+                "shared activation must be bf16 [tokens, shared_inter], 16-byte aligned rows");
+        require(bf16_rows_ok(down_proj, down_row_stride, shared_inter, hidden),
+                "shared down_proj must be bf16 [hidden, shared_inter], 16-byte aligned rows");
+        require(shared_gate != nullptr, "shared gate is required");
+        require(experts_out != nullptr && experts_row_stride >= hidden, "experts output must be bf16 [tokens, hidden]");
+        require(residual != nullptr && residual_row_stride >= hidden, "residual must be bf16 [tokens, hidden]");
+        require(out != nullptr && out_row_stride >= hidden, "output must be bf16 [tokens, hidden]");
+        dmoe::BlockPostArgs a{static_cast<const uint16_t*>(shared_act), act_row_stride, tokens, hidden, shared_inter,
+                              static_cast<const uint16_t*>(down_proj), down_row_stride,
+                              static_cast<const uint16_t*>(shared_gate), static_cast<const uint16_t*>(experts_out),
+                              experts_row_stride, static_cast<const uint16_t*>(residual), residual_row_stride,
+                              static_cast<uint16_t*>(out), out_row_stride};
+        dmoe::launch_block_post(a, device_cus(), as_stream(stream));
+    });
+}
+
 // ------------------------------------------------------ packed-integer banks
 
 int dmoe_rotate_quantize(const void* x, int x_dtype, int64_t x_row_stride, int rows, int k, int8_t* q,

@@ -312,6 +312,43 @@ struct QuantProjArgs {
 
 void launch_rotate_quant(const RotateArgs& a, hipStream_t stream);
 void launch_quant_projection(const QuantProjArgs& a, int max_active, hipStream_t stream);
+// The MoE block around the routed experts (moe_block.hip): router GEMV,
+// sigmoid-gated shared expert, residual adds; bf16 rows and weights.
+struct BlockPreArgs {
+    const uint16_t* x;            // [tokens, hidden] MoE input rows
+    int64_t x_row_stride;
+    int tokens, hidden, experts, shared_inter;
+    const uint16_t* router_w;     // [experts, hidden]
+    int64_t router_row_stride;
+    const uint16_t* sgate_w;      // [hidden] shared-expert gate row
+    const uint16_t* sg_w;         // [shared_inter, hidden] shared gate_proj
+    int64_t sg_row_stride;
+    const uint16_t* su_w;         // [shared_inter, hidden] shared up_proj
+    int64_t su_row_stride;
+    float* logits;                // [tokens, experts] out: bf16-rounded router logits
+    int64_t logits_row_stride;
+    uint16_t* sgate;              // [tokens] out: bf16 sigmoid gate
+    uint16_t* act;                // [tokens, shared_inter] out: bf16 bf16(silu(g)) * u
+    int64_t act_row_stride;
+};
+struct BlockPostArgs {
+    const uint16_t* act;          // [tokens, shared_inter]
+    int64_t act_row_stride;
+    int tokens, hidden, shared_inter;
+    const uint16_t* sd_w;         // [hidden, shared_inter] shared down_proj
+    int64_t sd_row_stride;
+    const uint16_t* sgate;        // [tokens]
+    const uint16_t* experts;      // [tokens, hidden] routed-expert output
+    int64_t experts_row_stride;
+    const uint16_t* residual;     // [tokens, hidden] after_mixer
+    int64_t residual_row_stride;
+    uint16_t* out;                // [tokens, hidden]
+    int64_t out_row_stride;
+};
+bool block_fits(int hidden, int shared_inter);
+void launch_block_pre(const BlockPreArgs& a, int cus, hipStream_t stream);
+void launch_block_post(const BlockPostArgs& a, int cus, hipStream_t stream);
+
 // Tiled grouped W4A16 projection (w4a16_grouped.hip): mode 0 with gate/up
 // I % 64 == 0, or plain N % 128 == 0.
 bool w4a16_grouped_fits(const QuantProjArgs& a);

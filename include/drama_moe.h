@@ -392,6 +392,36 @@ DMOE_API int dmoe_quant_moe_layer(const DmoeQuantBank* bank, const void* x, int 
                                   int out_dtype, int64_t out_row_stride, void* workspace,
                                   size_t workspace_bytes, int* status, void* stream);
 
+/* The MoE block around the routed experts, bf16 rows and weights (row
+ * strides in elements, rows 16-byte aligned; hidden and shared_inter multiples
+ * of 8, at most 4096).  Replaces BackboneDecodeGraph._route_impl's router
+ * (moe.gate, a bias-free nn.Linear), _shared_impl and _post_impl
+ * (src/drama_low_vram/backbone_graph.py:317-337) with torch's rounding at
+ * every module boundary.
+ *
+ * dmoe_moe_block_pre: for x [tokens, hidden] (post_attention_layernorm
+ * output) writes logits [tokens, experts] fp32 = bf16(x router_w^T) -- the
+ * input of dmoe_*_moe_layer --, shared_gate_out [tokens] bf16 =
+ * bf16(sigmoid(bf16(x shared_gate_w^T))) (shared_gate_w: the [1, hidden]
+ * shared_expert_gate weight) and shared_act [tokens, shared_inter] bf16 =
+ * bf16(bf16(silu(bf16(x gate_proj^T))) * bf16(x up_proj^T)). */
+DMOE_API int dmoe_moe_block_pre(const void* x, int64_t x_row_stride, int tokens, int hidden,
+                                const void* router_w, int64_t router_row_stride, int experts,
+                                const void* shared_gate_w, const void* gate_proj, int64_t gate_row_stride,
+                                const void* up_proj, int64_t up_row_stride, int shared_inter, float* logits,
+                                int64_t logits_row_stride, void* shared_gate_out, void* shared_act,
+                                int64_t act_row_stride, void* stream);
+
+/* dmoe_moe_block_post: out [tokens, hidden] bf16 = bf16(residual +
+ * bf16(experts_out + bf16(shared_gate * bf16(shared_act down_proj^T)))) with
+ * residual = after_mixer, experts_out = the routed-expert layer output and
+ * down_proj [hidden, shared_inter].  out may alias residual or experts_out. */
+DMOE_API int dmoe_moe_block_post(const void* shared_act, int64_t act_row_stride, int tokens, int shared_inter,
+                                 const void* down_proj, int64_t down_row_stride, int hidden,
+                                 const void* shared_gate, const void* experts_out, int64_t experts_row_stride,
+                                 const void* residual, int64_t residual_row_stride, void* out,
+                                 int64_t out_row_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -549,4 +549,55 @@ ORC_API int orc_quant_dequantize(const OrcQuantProj* p, int64_t e, float* out) {
     return 0;
 }
 
+/* ---------------------------------------------------------------- MoE block
+ * The block around the routed experts, as BackboneDecodeGraph runs it in bf16
+ * (src/drama_low_vram/backbone_graph.py:317-337): every nn.Linear is a
+ * bias-free x W^T accumulated in fp32 and rounded to bf16; torch.sigmoid /
+ * F.silu evaluate in fp32 and round to bf16; products and sums of bf16
+ * tensors round to bf16.  All inputs are bf16 values held in fp32 arrays. */
+static float bf16r(float v) { return round_through(v, 1); }
+
+static float dot_f32(const float* a, const float* b, int64_t n) {
+    float acc = 0.0f;
+    for (int64_t k = 0; k < n; ++k) acc += a[k] * b[k];
+    return acc;
+}
+
+/* logits [T, E] = bf16(x router_w^T) (_route_impl: moe.gate(flat).float());
+ * sgate [T] = bf16(sigmoid(bf16(x shared_gate_w^T))) (_shared_impl's
+ * torch.sigmoid(shared_expert_gate(flat))); act [T, I] =
+ * bf16(bf16(silu(bf16(x gate^T))) * bf16(x up^T)) (the shared expert's
+ * act_fn(gate_proj(x)) * up_proj(x)). */
+ORC_API int orc_block_pre(const float* x, int64_t T, int64_t H, const float* router_w, int64_t E,
+                          const float* sgate_w, const float* gate_w, const float* up_w, int64_t I,
+                          float* logits, float* sgate, float* act) {
+    if (T < 1 || H < 1 || E < 1 || I < 1) return -1;
+    for (int64_t t = 0; t < T; ++t) {
+        const float* xr = x + t * H;
+        for (int64_t e = 0; e < E; ++e) logits[t * E + e] = bf16r(dot_f32(xr, router_w + e * H, H));
+        const float g = bf16r(dot_f32(xr, sgate_w, H));
+        sgate[t] = bf16r(1.0f / (1.0f + expf(-g)));
+        for (int64_t j = 0; j < I; ++j) {
+            const float gv = bf16r(dot_f32(xr, gate_w + j * H, H));
+            const float uv = bf16r(dot_f32(xr, up_w + j * H, H));
+            act[t * I + j] = bf16r(bf16r(gv / (1.0f + expf(-gv))) * uv);
+        }
+    }
+    return 0;
+}
+
+/* out [T, H] = bf16(residual + bf16(experts + bf16(sgate * bf16(act down^T))))
+ * (_shared_impl's shared_gate * shared_expert(flat), then _post_impl's
+ * after_mixer + (expert_output + shared_output)). */
+ORC_API int orc_block_post(const float* act, int64_t T, int64_t I, const float* down_w, int64_t H,
+                           const float* sgate, const float* experts, const float* residual, float* out) {
+    if (T < 1 || H < 1 || I < 1) return -1;
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t n = 0; n < H; ++n) {
+            const float s = bf16r(sgate[t] * bf16r(dot_f32(act + t * I, down_w + n * I, I)));
+            out[t * H + n] = bf16r(residual[t * H + n] + bf16r(experts[t * H + n] + s));
+        }
+    return 0;
+}
+
 ORC_API int orc_abi_version(void) { return 1; }

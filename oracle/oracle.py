@@ -335,3 +335,37 @@ def quant_dequantize(bank: QuantBank, expert: int):
 def silu(x):
     x = np.asarray(x, np.float32)
     return x / (np.float32(1) + np.exp(-x))
+
+
+def block_pre(x, router_w, shared_gate_w, gate_w, up_w):
+    """MoE block head (backbone_graph.py:317-330): bf16-rounded router logits
+    [T, E], the sigmoid shared gate [T] and the shared expert's activation
+    [T, I], every input a bf16 value in float32 arrays."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, H = x.shape
+    E, I = router_w.shape[0], gate_w.shape[0]
+    logits = np.empty((T, E), np.float32)
+    sgate = np.empty(T, np.float32)
+    act = np.empty((T, I), np.float32)
+    _check(lib().orc_block_pre(_ptr(x), ctypes.c_int64(T), ctypes.c_int64(H),
+                               _ptr(np.ascontiguousarray(router_w, np.float32)), ctypes.c_int64(E),
+                               _ptr(np.ascontiguousarray(shared_gate_w, np.float32).reshape(-1)),
+                               _ptr(np.ascontiguousarray(gate_w, np.float32)),
+                               _ptr(np.ascontiguousarray(up_w, np.float32)), ctypes.c_int64(I),
+                               _ptr(logits), _ptr(sgate), _ptr(act)), "block_pre")
+    return logits, sgate, act
+
+
+def block_post(act, down_w, sgate, experts, residual):
+    """MoE block tail (backbone_graph.py:329-337): residual + (experts +
+    sgate * shared down projection), bf16 at every boundary."""
+    act = np.ascontiguousarray(act, np.float32)
+    T, I = act.shape
+    H = down_w.shape[0]
+    out = np.empty((T, H), np.float32)
+    _check(lib().orc_block_post(_ptr(act), ctypes.c_int64(T), ctypes.c_int64(I),
+                                _ptr(np.ascontiguousarray(down_w, np.float32)), ctypes.c_int64(H),
+                                _ptr(np.ascontiguousarray(sgate, np.float32)),
+                                _ptr(np.ascontiguousarray(experts, np.float32)),
+                                _ptr(np.ascontiguousarray(residual, np.float32)), _ptr(out)), "block_post")
+    return out

@@ -700,3 +700,52 @@ def test_torch_cpu_fp8_layer_is_o2():
     want = orc.o2_moe_forward(b13, b2, x.float().numpy(), ids, w)
     assert np.mean(got == want) > 0.95
     assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-2
+
+
+def _reference_moe_block_modules(hidden, experts, inter, g):
+    """The torch modules BackboneDecodeGraph drives (backbone_graph.py:317-337),
+    bf16, random weights: moe.gate, shared_expert_gate and a shared SwiGLU MLP."""
+    nn = torch.nn
+    gate = nn.Linear(hidden, experts, bias=False).bfloat16()
+    sgate = nn.Linear(hidden, 1, bias=False).bfloat16()
+    gp = nn.Linear(hidden, inter, bias=False).bfloat16()
+    up = nn.Linear(hidden, inter, bias=False).bfloat16()
+    down = nn.Linear(inter, hidden, bias=False).bfloat16()
+    with torch.no_grad():
+        for m, std in ((gate, 0.05), (sgate, 0.05), (gp, 0.05), (up, 0.05), (down, 0.05)):
+            m.weight.copy_(torch.randn(m.weight.shape, generator=g) * std)
+    return gate, sgate, gp, up, down
+
+
+def test_moe_block_oracle_matches_torch_modules():
+    """orc_block_pre / orc_block_post against the reference's own expressions on
+    torch's CPU bf16 modules: softmax input moe.gate(flat).float(),
+    torch.sigmoid(shared_expert_gate(flat)), down(silu(gate(x)) * up(x)),
+    after_mixer + (experts + shared).  Accumulation order differs (torch's
+    blocked bf16 GEMM vs a sequential fp32 sum), so values agree to about one
+    bf16 rounding step; a planted mistake (the sigmoid gate dropped) must fail."""
+    g = torch.Generator().manual_seed(31)
+    hidden, experts, inter, tokens = 256, 16, 64, 5
+    gate, sgate, gp, up, down = _reference_moe_block_modules(hidden, experts, inter, g)
+    flat = torch.randn(tokens, hidden, generator=g).bfloat16()
+    after = torch.randn(tokens, hidden, generator=g).bfloat16()
+    experts_out = torch.randn(tokens, hidden, generator=g).bfloat16()
+    with torch.no_grad():
+        want_logits = gate(flat).float()
+        want_sgate = torch.sigmoid(sgate(flat))
+        want_act = torch.nn.functional.silu(gp(flat)) * up(flat)
+        shared = want_sgate * down(want_act)
+        want_out = after + (experts_out + shared)
+    w = {name: m.weight.detach().float().numpy() for name, m in
+         (("gate", gate), ("sgate", sgate), ("gp", gp), ("up", up), ("down", down))}
+    logits, sg, act = orc.block_pre(flat.float().numpy(), w["gate"], w["sgate"], w["gp"], w["up"])
+    bf16_step = 2.0 ** -7  # one bf16 rounding step, relative
+    assert np.max(np.abs(logits - want_logits.numpy())) <= 2 * bf16_step * np.max(np.abs(want_logits.numpy()))
+    assert np.max(np.abs(sg - want_sgate.float().numpy().reshape(-1))) <= 2 * bf16_step
+    assert np.max(np.abs(act - want_act.float().numpy())) <= 2 * bf16_step * np.max(np.abs(want_act.float().numpy()))
+    out = orc.block_post(act, w["down"], sg, experts_out.float().numpy(), after.float().numpy())
+    ref = want_out.float().numpy()
+    assert np.max(np.abs(out - ref)) / np.max(np.abs(ref)) < 1e-2
+    # planted mistake: the sigmoid gate dropped from the shared expert
+    wrong = orc.block_post(act, w["down"], np.ones_like(sg), experts_out.float().numpy(), after.float().numpy())
+    assert np.max(np.abs(wrong - ref)) / np.max(np.abs(ref)) > 1e-2
