@@ -497,8 +497,8 @@ void check_quant_rows(const void* x, int x_dtype, int64_t x_row_stride, int rows
 
 // A grouped packed projection: the tiled W4A16 GEMM where its tile shape
 // fits, else the column-group kernel.
-void launch_projection(const dmoe::QuantProjArgs& q, int max_active, hipStream_t stream) {
-    if (dmoe::w4a16_grouped_fits(q)) dmoe::launch_w4a16_grouped(q, max_active, stream);
+void launch_projection(const dmoe::QuantProjArgs& q, int max_active, int pairs, hipStream_t stream) {
+    if (dmoe::w4a16_grouped_fits(q)) dmoe::launch_w4a16_grouped(q, max_active, stream, pairs);
     else dmoe::launch_quant_projection(q, max_active, stream);
 }
 
@@ -951,6 +951,43 @@ int dmoe_fp8_moe_layer_noalloc(const DmoeFp8Bank* bank, const void* x, int x_dty
     });
 }
 
+int dmoe_w4a16_linear(const void* x, int x_dtype, int64_t x_row_stride, int rows, const int32_t* qweight,
+                      int64_t qweight_row_stride, const uint16_t* scales, int64_t scale_row_stride, int n, int k,
+                      void* out, int64_t out_row_stride, void* stream) {
+    return checked([&] {
+        require(rows >= 1, "rows must be positive");
+        require(n >= 128 && n % 128 == 0 && k >= 128 && k % 128 == 0 && k <= dmoe::kMaxQuantK,
+                "W4A16 linear n and k must be multiples of 128, k at most 4096");
+        require(x != nullptr && (x_dtype == DMOE_BF16 || x_dtype == DMOE_F16),
+                "W4A16 activations must be bf16 or fp16");
+        require(x_row_stride >= k && (x_row_stride * 2) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
+                "W4A16 activation rows must be [rows, k] and 16-byte aligned");
+        require(qweight != nullptr && qweight_row_stride >= k / 8 && (qweight_row_stride * 4) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(qweight) % 16 == 0,
+                "qweight must be int32 [n, k/8] with 16-byte aligned rows");
+        require(scales != nullptr && scale_row_stride >= k / 128 && reinterpret_cast<uintptr_t>(scales) % 2 == 0,
+                "scales must be fp16 [n, k/128]");
+        require(out != nullptr && out_row_stride >= n, "output must be bf16 [rows, n]");
+        dmoe::QuantProjArgs q{};
+        q.mode = 0;
+        q.w = reinterpret_cast<const uint8_t*>(qweight);
+        q.s = reinterpret_cast<const uint8_t*>(scales);
+        q.z = nullptr;
+        q.w_sn = qweight_row_stride * 4;
+        q.s_sn = scale_row_stride * 2;
+        q.N = n;
+        q.K = k;
+        q.x = x;
+        q.x_f16 = x_dtype == DMOE_F16;
+        q.x_row_stride = x_row_stride;
+        q.row_div = 1;
+        q.out = out;
+        q.out_row_stride = out_row_stride;
+        q.dense_rows = rows;
+        dmoe::launch_w4a16_grouped(q, 1, as_stream(stream), rows);
+    });
+}
+
 // ------------------------------------------------------ MoE block (router GEMV, shared expert)
 
 namespace {
@@ -1087,7 +1124,7 @@ int dmoe_quant_projection(const DmoeQuantProj* proj, int experts, int mode, cons
         q.out = out;
         q.out_row_stride = out_row_stride;
         q.status = status;
-        launch_projection(q, std::min(pairs, experts), st);
+        launch_projection(q, std::min(pairs, experts), pairs, st);
     });
 }
 
@@ -1142,7 +1179,7 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
             up.gateup = 1;
             up.act = ws.act;
             up.status = status;
-            launch_projection(up, max_active, st);
+            launch_projection(up, max_active, pairs, st);
         }
 
         if (small_dn) {
@@ -1163,7 +1200,7 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
         dn.out = out_pairs ? out_pairs : ws.partial;
         dn.out_row_stride = H;
         dn.status = status;
-        launch_projection(dn, max_active, st);
+        launch_projection(dn, max_active, pairs, st);
 
         if (out_pairs) {
             const dmoe::CombineArgs za{out_pairs, H, ids, ids_dtype, E, pairs, 1, H, nullptr, DMOE_F32, 0};

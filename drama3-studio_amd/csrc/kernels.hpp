@@ -308,6 +308,9 @@ struct QuantProjArgs {
     void* out;
     int64_t out_row_stride;
     int* status;
+    // dense layer (w4a16 tiled kernel only): rows [0, dense_rows) against
+    // expert 0 in their own order; order / offsets / active are not read
+    int dense_rows;
 };
 
 void launch_rotate_quant(const RotateArgs& a, hipStream_t stream);
@@ -352,7 +355,7 @@ void launch_block_post(const BlockPostArgs& a, int cus, hipStream_t stream);
 // Tiled grouped W4A16 projection (w4a16_grouped.hip): mode 0 with gate/up
 // I % 64 == 0, or plain N % 128 == 0.
 bool w4a16_grouped_fits(const QuantProjArgs& a);
-void launch_w4a16_grouped(const QuantProjArgs& a, int max_active, hipStream_t stream);
+void launch_w4a16_grouped(const QuantProjArgs& a, int max_active, hipStream_t stream, int pairs);
 
 // Small packed calls (at most 64 route pairs): two launches that group the
 // pairs themselves from the route ids (no permutation launch).

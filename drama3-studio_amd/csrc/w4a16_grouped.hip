@@ -27,6 +27,8 @@
 // [32 g + 8 t, +8) -- the same for activations and weights.  Every weight
 // byte of a column tile is read once per 64-row chunk (once per call at 512
 // tokens), the activation rows once per column tile from L2.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -126,9 +128,10 @@ __global__ __launch_bounds__(kW4Threads) void w4a16_grouped_kernel(QuantProjArgs
     __shared__ W4Lds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int col = lane % 16, g = lane / 16;
-    if ((int)blockIdx.x >= a.active[0]) return;
-    const int e = a.active[1 + blockIdx.x];
-    const int pbeg = a.offsets[e], pend = a.offsets[e + 1];
+    const bool dense = a.dense_rows > 0;
+    if (!dense && (int)blockIdx.x >= a.active[0]) return;
+    const int e = dense ? 0 : a.active[1 + blockIdx.x];
+    const int pbeg = dense ? 0 : a.offsets[e], pend = dense ? a.dense_rows : a.offsets[e + 1];
     const int KB = a.K / 128, half = a.N / 2;
     // this lane's two weight rows
     int n[2];
@@ -156,12 +159,13 @@ __global__ __launch_bounds__(kW4Threads) void w4a16_grouped_kernel(QuantProjArgs
     // MFMA A operand of row tile mi, step t: row 16 mi + col, logical chunk 4 g + t
     auto a_off = [&](int mi, int t) { return (16 * mi + col) * 256 + (((4 * g + t) ^ col) * 16); };
 
-    for (int m0 = pbeg; m0 < pend; m0 += kW4Rows) {
+    // workgroup z of gridDim.z takes chunks z, z + gridDim.z, ... of its expert
+    for (int m0 = pbeg + (int)blockIdx.z * kW4Rows; m0 < pend; m0 += (int)gridDim.z * kW4Rows) {
         __syncthreads();  // the previous chunk is done with the row table and buffers
         if (threadIdx.x < kW4Rows) {
             const int pos = m0 + (int)threadIdx.x;
             const int pc = pos < pend ? pos : m0;
-            const int p = a.order[pc];
+            const int p = dense ? pc : a.order[pc];
             s.row[threadIdx.x] = p / a.row_div;
             s.pair[threadIdx.x] = pos < pend ? p : -1;
         }
@@ -252,8 +256,12 @@ bool w4a16_grouped_fits(const QuantProjArgs& a) {
     return a.gateup ? (a.N / 2) % 64 == 0 : a.N % 128 == 0;
 }
 
-void launch_w4a16_grouped(const QuantProjArgs& a, int max_active, hipStream_t stream) {
-    const dim3 grid((unsigned)max_active, (unsigned)(a.gateup ? a.N / 2 / 64 : a.N / 128));
+void launch_w4a16_grouped(const QuantProjArgs& a, int max_active, hipStream_t stream, int pairs) {
+    // the chunks of an expert spread over gridDim.z workgroups: about one
+    // each for the average expert (every chunk of a dense layer)
+    const int experts = a.dense_rows > 0 ? 1 : max_active;
+    const int zsplit = std::max(1, std::min(256, (pairs / experts + kW4Rows - 1) / kW4Rows));
+    const dim3 grid((unsigned)experts, (unsigned)(a.gateup ? a.N / 2 / 64 : a.N / 128), (unsigned)zsplit);
     if (a.gateup) {
         if (a.x_f16) hipLaunchKernelGGL((w4a16_grouped_kernel<true, true>), grid, dim3(kW4Threads), 0, stream, a);
         else hipLaunchKernelGGL((w4a16_grouped_kernel<true, false>), grid, dim3(kW4Threads), 0, stream, a);

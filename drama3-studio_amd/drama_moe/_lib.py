@@ -86,6 +86,7 @@ _SIGNATURES = {
                                 ctypes.c_size_t, _P, _P], _I),
     "dmoe_quant_moe_layer": ([_P, _P, _I, _L, _I, _P, _L, _I, _I, _P, _P, _I, _P, _I, _L, _P, ctypes.c_size_t,
                               _P, _P], _I),
+    "dmoe_w4a16_linear": ([_P, _I, _L, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P], _I),
     "dmoe_moe_block_pre": ([_P, _L, _I, _I, _P, _L, _I, _P, _P, _L, _P, _L, _I, _P, _L, _P, _P, _L, _P], _I),
     "dmoe_moe_block_post": ([_P, _L, _I, _I, _P, _L, _I, _P, _P, _L, _P, _L, _P, _L, _P], _I),
     "dmoe_fp8_quantized_pairs": ([ctypes.POINTER(Fp8Bank), _P, _P, _L, _L, _I, _I, _I, _P, _I, _P,

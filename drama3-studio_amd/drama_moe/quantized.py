@@ -206,3 +206,43 @@ class QuantizedExpertBackend:
             _lib.dtype_code(weights.dtype), _lib.ptr(out), _lib.dtype_code(out.dtype), out.stride(0), _lib.ptr(ws),
             ws.numel(), _lib.ptr(state.status), _lib.stream_handle(device)))
         return out, weights, ids
+
+
+class GPTQLinear(torch.nn.Module):
+    """Dense W4A16 linear kept compressed on the GPU, the reference's
+    GPTQLinear (src/drama_low_vram/quantized_model.py:71-91): GPTQ ``weight``
+    [K/8, N] int32 and ``scales`` [K/128, N] fp16 are stored transposed
+    (``qweight`` [N, K/8], ``scales`` [N, K/128]); ``forward`` multiplies rows
+    of x (bf16 or fp16, any leading shape) by the dequantized matrix with the
+    tiled W4A16 kernel (dmoe_w4a16_linear) and returns bf16 [..., N], as the
+    reference's projection(mode=0) over one expert does."""
+
+    def __init__(self, weight: Tensor, scales: Tensor, *, device, dtype=torch.bfloat16):
+        super().__init__()
+        if weight.dtype != torch.int32 or weight.ndim != 2:
+            raise ValueError("GPTQ qweight must be int32 [K/8, N]")
+        if scales.dtype != torch.float16 or scales.shape != (weight.shape[0] * 8 // 128, weight.shape[1]):
+            raise ValueError("GPTQ scales must be fp16 [K/128, N]")
+        self.in_features, self.out_features = weight.shape[0] * 8, weight.shape[1]
+        self.register_buffer("qweight", weight.T.contiguous().to(device))
+        self.register_buffer("scales", scales.T.contiguous().to(device))
+        self.register_buffer("_anchor", torch.empty(0, device=device, dtype=dtype))
+
+    @property
+    def weight(self):
+        return self._anchor
+
+    def forward(self, x: Tensor) -> Tensor:
+        if x.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("GPTQLinear inputs must be bf16 or fp16")
+        shape = x.shape
+        flat = x.reshape(-1, shape[-1])
+        if flat.stride(-1) != 1 or (flat.stride(0) * 2) % 16 or flat.data_ptr() % 16:
+            flat = flat.contiguous()
+        out = torch.empty((flat.shape[0], self.out_features), dtype=torch.bfloat16, device=x.device)
+        if flat.shape[0]:
+            _lib.check(_lib.library().dmoe_w4a16_linear(
+                _lib.ptr(flat), _lib.dtype_code(flat.dtype), flat.stride(0), flat.shape[0], _lib.ptr(self.qweight),
+                self.qweight.stride(0), _lib.ptr(self.scales), self.scales.stride(0), self.out_features,
+                self.in_features, _lib.ptr(out), out.stride(0), _lib.stream_handle(x.device)))
+        return out.reshape(*shape[:-1], self.out_features)

@@ -392,6 +392,19 @@ DMOE_API int dmoe_quant_moe_layer(const DmoeQuantBank* bank, const void* x, int 
                                   int out_dtype, int64_t out_row_stride, void* workspace,
                                   size_t workspace_bytes, int* status, void* stream);
 
+/* Dense W4A16 linear (GPTQ, group 128, symmetric: zero point 8): out [rows, n]
+ * bf16 = x [rows, k] (bf16 or fp16, 16-byte aligned rows) times the
+ * dequantized weight, each weight cd((code - 8) * scale) in the activation
+ * type, fp32 accumulation, bf16 result.  qweight [n, k/8] int32 (nibble i of
+ * word w <-> column 8 w + i; row stride in elements, rows 16-byte aligned) and
+ * scales [n, k/128] fp16 are the transposed GPTQ buffers GPTQLinear keeps;
+ * n and k multiples of 128, k <= 4096.  Replaces GPTQLinear.forward
+ * (src/drama_low_vram/quantized_model.py:71-91), its projection(mode=0) over
+ * one expert. */
+DMOE_API int dmoe_w4a16_linear(const void* x, int x_dtype, int64_t x_row_stride, int rows, const int32_t* qweight,
+                               int64_t qweight_row_stride, const uint16_t* scales, int64_t scale_row_stride, int n,
+                               int k, void* out, int64_t out_row_stride, void* stream);
+
 /* The MoE block around the routed experts, bf16 rows and weights (row
  * strides in elements, rows 16-byte aligned; hidden and shared_inter multiples
  * of 8, at most 4096).  Replaces BackboneDecodeGraph._route_impl's router

@@ -349,3 +349,24 @@ def test_w4a16_tiled_prefill_every_token(cuda, x_dtype):
     expected = torch_cpu.layer(store, x, ids, weights)
     assert out.dtype == x_dtype
     assert rel_inf(out.float().cpu().numpy(), expected.float().numpy()) < TOL
+
+
+@pytest.mark.parametrize("rows,n,k,x_dtype", [(1, 2048, 2048, torch.bfloat16), (7, 256, 512, torch.bfloat16),
+                                              (300, 1024, 768, torch.float16), (2048, 512, 2048, torch.bfloat16)])
+def test_gptq_linear_matches_dequantize_then_matmul(cuda, rows, n, k, x_dtype):
+    """Dense GPTQLinear (quantized_model.py:71-91) on the tiled W4A16 kernel
+    against the torch-CPU reconstruction of projection_torch (one expert,
+    zero point 8), including leading shapes and M in many 64-row chunks."""
+    from oracle import torch_cpu
+
+    print_case("gptq linear", rows, n, k, x_dtype)
+    g = torch.Generator().manual_seed(rows + n + k)
+    words = torch.randint(-2 ** 31, 2 ** 31 - 1, (k // 8, n), generator=g, dtype=torch.int64).to(torch.int32)
+    scales = (torch.rand(k // 128, n, generator=g) * 0.02 + 0.002).half()
+    lin = quantized.GPTQLinear(words, scales, device=cuda)
+    x = torch.randn(rows, k, generator=g).to(x_dtype)
+    out = lin(x.to(cuda).reshape(1, rows, k))
+    assert out.shape == (1, rows, n) and out.dtype == torch.bfloat16
+    matrix = torch_cpu.dequantize(0, words.T.contiguous(), scales.T.contiguous(), k, x_dtype)
+    expected = (x.float() @ matrix.T).bfloat16().float()
+    assert rel_inf(out.reshape(rows, n).float().cpu().numpy(), expected.numpy()) < 5e-3
