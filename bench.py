@@ -14,8 +14,9 @@ so the roofline line is that kernel's: algorithmic bytes of the step (distinct
 experts' FP8 rows and scales, activations, logits) over its average launch
 duration from HIP events on the launch stream; traffic = its copy-calibrated
 FETCH_SIZE + WRITE_SIZE from the committed counter summary.  Beside it: the
-same steps through the three-launch decode, 4- and 8-token decode, the
-2048-token FP8 prefill, the packed-bank formats, and the reference's own CPU
+same steps through the three-launch decode, 4-, 8- and 16-token decode, the
+whole MoE block (router GEMV, routed experts, shared expert, residual adds),
+the 2048-token FP8 prefill, the packed-bank formats, and the reference's own CPU
 expert executor (compiled from its sources into oracle/_ref) timed on this
 host's cores on a bounded sample of the same layer shape.
 
@@ -283,6 +284,67 @@ def run_prefill(reps: int = 10):
     return result
 
 
+SHARED_INTER = 768  # the shared expert's intermediate size in the block leg
+
+
+def run_block(steps: int, warmup: int):
+    """Whole MoE block of one decoder layer at batch 1 (router GEMV, FP8
+    routed experts, sigmoid-gated bf16 shared expert of SHARED_INTER, residual
+    adds: three launches), over the same LAYERS rotating banks, hipGraph-
+    replayed; beside it the two block launches alone."""
+    import torch
+
+    from drama_moe import block
+    from drama_moe.offload import HipExpertBackend
+
+    device = torch.device("cuda", 0)
+    banks = [make_layer_bank(layer, device) for layer in range(LAYERS)]
+    g = torch.Generator(device=device).manual_seed(SEED + 77)
+
+    def w(*shape):
+        return (torch.randn(*shape, device=device, generator=g) * 0.02).bfloat16()
+
+    backend = HipExpertBackend()
+    blocks = [block.MoeBlock(w(EXPERTS, HIDDEN), w(1, HIDDEN), w(SHARED_INTER, HIDDEN), w(SHARED_INTER, HIDDEN),
+                             w(HIDDEN, SHARED_INTER), banks[i], backend, top_k=TOP_K) for i in range(LAYERS)]
+    xs = torch.randn(LAYERS, 1, HIDDEN, device=device, generator=g).bfloat16()
+    after = torch.randn(LAYERS, 1, HIDDEN, device=device, generator=g).bfloat16()
+    outs = torch.empty_like(xs)
+    stream = torch.cuda.Stream(device)
+    steps = max(LAYERS, steps // LAYERS * LAYERS)
+    replays = steps // LAYERS
+
+    def whole():
+        for i in range(LAYERS):
+            blocks[i](xs[i], after[i], out=outs[i])
+
+    pre_out = [blocks[i].pre(xs[i]) for i in range(LAYERS)]
+    experts_out = torch.randn(LAYERS, 1, HIDDEN, device=device, generator=g).bfloat16()
+
+    def pre_only():
+        for i in range(LAYERS):
+            blocks[i].pre(xs[i])
+
+    def post_only():
+        for i in range(LAYERS):
+            blocks[i].post(pre_out[i][2], pre_out[i][1], experts_out[i], after[i], out=outs[i])
+
+    del warmup  # _graph_time_us replays once before timing
+    result = {"us": round(_graph_time_us(whole, LAYERS, replays, stream), 2),
+              "pre_us": round(_graph_time_us(pre_only, LAYERS, replays, stream), 2),
+              "post_us": round(_graph_time_us(post_only, LAYERS, replays, stream), 2)}
+    status = backend.status(device)
+    if status:
+        raise RuntimeError(f"block steps raised device status bits {status:#x}")
+    routed, uniq = step_bytes(torch.stack([pre_out[i][0] for i in range(LAYERS)]), 1)
+    dense = (EXPERTS * HIDDEN + HIDDEN + 3 * SHARED_INTER * HIDDEN) * 2 + 3 * HIDDEN * 2
+    nbytes = routed + dense
+    result.update({"alg_mb": round(nbytes / 1e6, 2), "unique_experts_mean": round(uniq, 2),
+                   "hbm_frac": round(nbytes / (result["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                   "shared_inter": SHARED_INTER, "launches": 3})
+    return result
+
+
 QUANT_NAMES = {0: "w4a16_asym_g128", 1: "int8_convrot", 2: "w6a8", 3: "w4a8_codebook", 4: "w4a8_g128_fp8",
                5: "w6a8_g128_fp8"}
 
@@ -533,6 +595,7 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-prefill", action="store_true")
     parser.add_argument("--no-quant", action="store_true")
+    parser.add_argument("--no-block", action="store_true")
     parser.add_argument("--pmc-pass", nargs="?", const="decode", choices=("decode", "prefill"),
                         help="run the eager counter-collection workload (decode or prefill) instead of the benchmark")
     args = parser.parse_args()
@@ -549,6 +612,8 @@ def main():
     steps = max(1, args.steps)
     gpu = run_gpu(steps, args.warmup)
     log("gpu", json.dumps(gpu))
+    moe_block = None if args.no_block else run_block(steps, args.warmup)
+    log("block", json.dumps(moe_block))
     prefill = None if args.no_prefill else run_prefill()
     log("prefill", json.dumps(prefill))
     quant = None if args.no_quant else run_quant()
@@ -584,6 +649,7 @@ def main():
         "decode_three_launch_us": round(gpu["three_launch_us"], 3),
         "decode_three_launch_identical": gpu["three_launch_identical"],
         "decode_multi_token": gpu["multi_token"],
+        "moe_block_decode": moe_block,
         "cpu_baseline": cpu,
         "prefill_fp8": prefill,
         "packed_banks": quant,
