@@ -5,9 +5,10 @@ Reference interface: ``ExpertBackend`` (src/drama_low_vram/offload.py:187-196)
 with ``forward`` / ``forward_pairs`` and the Triton backend's
 ``forward_decode_pairs`` / ``_check`` / ``.kernel`` (offload.py:247-356); the
 manager contract of ``ExpertOffloadManager`` / ``install_expert_offload``
-(offload.py:903-1063, 1534).  All experts are resident, so the staging pool,
-hot cache and host residency tiers of the reference are absent: ``staged`` is
-the whole bank and local slot ids are global expert ids.
+(offload.py:903-1063, 1534).  By default all experts are resident, so
+``staged`` is the whole bank and local slot ids are global expert ids; the
+reference's staging pool and hot cache exist as the optional host-residency
+mode of drama_moe.staging (``residency="host"``).
 
 Conventions kept from the reference: kernels run on the caller's current
 stream, outputs are freshly allocated, ``ValueError`` for geometry / dtype,
@@ -326,9 +327,11 @@ def _attached(module: nn.Module) -> bool:
 
 class ResidentExpertManager:
     """Routes ``experts(x, topk_ids, topk_weights)`` of attached modules to a
-    backend with the whole bank resident in HBM -- the caller contract of
-    ExpertOffloadManager.attach / forward (offload.py:996-1063) without its
-    staging tiers.
+    backend -- the caller contract of ExpertOffloadManager.attach / forward
+    (offload.py:996-1063).  With ``residency="hbm"`` (default) the whole bank
+    is resident in HBM (a host-held bank is copied to the device on its first
+    call); with ``residency="host"`` the staging keywords configure the host
+    tier of drama_moe.staging (``self.host``).
 
     Banks are resolved once per module and reused while the module keeps the
     same buffers.  FP8 banks run on ``backend`` (default HipExpertBackend);
@@ -338,12 +341,30 @@ class ResidentExpertManager:
     device status word so calls can be captured in hipGraphs.
     """
 
-    def __init__(self, *, backend=None, validate_ids: bool = True) -> None:
+    def __init__(self, *, backend=None, validate_ids: bool = True, residency: str = "hbm", **staging) -> None:
+        from .staging import RESIDENCY_MODES, HostResidency, check_staging_sizes
+
+        if residency not in RESIDENCY_MODES:
+            raise ValueError(f"residency must be one of {RESIDENCY_MODES}, got {residency!r}")
+        unknown = set(staging) - STAGING_KEYWORDS
+        if unknown:
+            raise TypeError(f"unexpected staging keywords {sorted(unknown)}")
+        for flag in ("pin_memory", "profile_transfers", "combined_decode_bank", "packed_staging"):
+            if flag in staging and not isinstance(staging[flag], bool):
+                raise TypeError(f"{flag} must be a boolean")
+        sizes = {k: staging[k] for k in ("max_staged_experts", "max_pair_rows", "cache_experts", "hot_cache_experts")
+                 if k in staging}
+        check_staging_sizes(sizes.get("max_staged_experts", 8), sizes.get("max_pair_rows", 64),
+                       sizes.get("cache_experts", 0), sizes.get("hot_cache_experts"))
         self.backend = backend if backend is not None else HipExpertBackend()
         self.validate_ids = validate_ids
+        self.residency = residency
+        # host mode: the staging tier; hbm mode: the sizes are checked and unused
+        self.host = HostResidency(pin_memory=staging.get("pin_memory", True), **sizes) if residency == "host" else None
         self.modules: dict[str, nn.Module] = {}
         self.forward_calls = 0
         self._banks: dict[int, tuple] = {}
+        self._device_banks: dict[int, tuple] = {}
         self._packed_backends: dict[int, object] = {}
         self._closed = False
 
@@ -386,9 +407,27 @@ class ResidentExpertManager:
         self.forward_calls += 1
         if x.shape[0] == 0:
             return torch.zeros_like(x)
+        backend = self._backend_for(bank)
+        if self.host is not None:
+            return self.host.forward(id(module), bank, backend, x, topk_ids, topk_weights)
         if self.validate_ids:
             check_id_range(topk_ids, bank.count)
-        return self._backend_for(bank).forward(x, topk_ids, topk_weights, bank)
+        return backend.forward(x, topk_ids, topk_weights, self._on_device(module, bank, x.device))
+
+    def _on_device(self, module: nn.Module, bank, device: torch.device):
+        """The bank itself when it lives on ``device``, else its whole copy
+        there, made on the module's first call and kept while the module
+        holds the same buffers."""
+        from .staging import bank_device, bank_key, device_copy
+
+        if bank_device(bank) == device:
+            return bank
+        key = (bank_key(bank), device)
+        cached = self._device_banks.get(id(module))
+        if cached is None or cached[0] != key:
+            cached = (key, device_copy(bank, device))
+            self._device_banks[id(module)] = cached
+        return cached[1]
 
     def close(self) -> None:
         for module in self.modules.values():
@@ -400,22 +439,32 @@ class ResidentExpertManager:
                     module.forward = routed.shadowed
         self.modules.clear()
         self._banks.clear()
+        self._device_banks.clear()
+        self.host = None
         self._closed = True
 
 
 # Keywords of the reference's install_expert_offload (offload.py:1534-1546)
-# that configure its host staging tiers; with every expert resident they have
-# nothing to configure and are accepted for call-site compatibility.
+# that configure its host staging tiers.  With residency="host" the sizes
+# and pin_memory configure the staging tier of drama_moe.staging; with every
+# expert resident (the default) they are checked and have nothing to
+# configure.  profile_transfers, combined_decode_bank and packed_staging are
+# accepted for call-site compatibility: banks are always staged packed, and a
+# decode token whose experts are split between the hot cache and the pool
+# runs as grouped pair calls.
 STAGING_KEYWORDS = frozenset({"max_staged_experts", "max_pair_rows", "cache_experts", "hot_cache_experts",
                               "pin_memory", "profile_transfers", "combined_decode_bank", "packed_staging"})
 
 
-def install_expert_offload(backbone: nn.Module, *, backend=None, validate_ids: bool = True,
+def install_expert_offload(backbone: nn.Module, *, backend=None, validate_ids: bool = True, residency: str = "hbm",
                            **staging) -> ResidentExpertManager:
-    """Attach a resident manager to every routed expert module of a backbone
-    (modules holding w13_weight and w2_weight, offload.py:1479-1484, 1534).
+    """Attach a manager to every routed expert module of a backbone (modules
+    holding w13_weight and w2_weight, offload.py:1479-1484, 1534).
     ``backend`` is a backend object, or "hip" / "triton" (both mean the gfx950
-    FP8 backend).  Every bank is checked before any forward is replaced."""
+    FP8 backend).  ``residency`` "hbm" (default) runs every bank from device
+    memory, copying a host-held bank to the device once; "host" keeps banks in
+    host memory and stages the routed experts per call.  Every bank is
+    checked before any forward is replaced."""
     unknown = set(staging) - STAGING_KEYWORDS
     if unknown:
         raise TypeError(f"install_expert_offload() got unexpected keywords {sorted(unknown)}")
@@ -431,7 +480,7 @@ def install_expert_offload(backbone: nn.Module, *, backend=None, validate_ids: b
         store_from_module(module)
         if _attached(module):
             raise ValueError("Backbone already has an expert offload manager")
-    manager = ResidentExpertManager(backend=backend, validate_ids=validate_ids)
+    manager = ResidentExpertManager(backend=backend, validate_ids=validate_ids, residency=residency, **staging)
     for name, module in targets:
         manager.attach(name, module)
     return manager

@@ -154,7 +154,15 @@ def test_install_checks_every_bank_and_keyword(bank):
     with pytest.raises(ValueError):
         install_expert_offload(broken)
     assert "forward" not in broken.a.__dict__  # nothing attached when any bank is bad
-    manager = install_expert_offload(backbone, backend="triton", **{k: None for k in STAGING_KEYWORDS})
+    flags = {"max_staged_experts": 8, "max_pair_rows": 64, "cache_experts": 4, "hot_cache_experts": None,
+             "pin_memory": True, "profile_transfers": False, "combined_decode_bank": True, "packed_staging": False}
+    assert set(flags) == STAGING_KEYWORDS
+    with pytest.raises(ValueError, match="positive"):
+        install_expert_offload(backbone, **{**flags, "max_pair_rows": 0})
+    with pytest.raises(TypeError, match="boolean"):
+        install_expert_offload(backbone, **{**flags, "packed_staging": 1})
+    manager = install_expert_offload(backbone, backend="triton", **flags)
+    assert manager.residency == "hbm" and manager.host is None
     assert sorted(manager.modules) == ["a", "b"]
     with pytest.raises(ValueError, match="already has an expert offload manager"):
         install_expert_offload(backbone)
