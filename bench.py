@@ -191,8 +191,9 @@ def run_gpu(steps: int, warmup: int):
 
 def pmc_pass(workload: str = "decode", rounds: int = 8, copy_mib: int = 256):
     """Eager workload for hardware-counter runs: `rounds` passes of the
-    decode step over the layer banks (or `rounds` 2048-token prefill layer
-    calls with per-token activation scales), then a plain fp32 copy of
+    decode step over the layer banks (or `rounds` 2048-token FP8 prefill layer
+    calls with per-token activation scales, or `rounds` 512-token asymmetric
+    W4A16 prefill calls), then a plain fp32 copy of
     `copy_mib` MiB (read once, written once) whose counter readings calibrate
     the bytes-per-count of the HBM counters."""
     import torch
@@ -200,7 +201,20 @@ def pmc_pass(workload: str = "decode", rounds: int = 8, copy_mib: int = 256):
     from drama_moe.offload import HipExpertBackend
 
     device = torch.device("cuda", 0)
-    if workload == "prefill":
+    if workload == "w4a16":
+        from drama_moe import router
+        from drama_moe.formats import random_quantized_bank
+        from drama_moe.quantized import QuantizedExpertBackend
+
+        g = torch.Generator(device=device).manual_seed(SEED)
+        bank = random_quantized_bank(0, EXPERTS, HIDDEN, INTER, asymmetric=True, device=device, generator=g)
+        x = torch.randn(512, HIDDEN, device=device, generator=g).bfloat16()
+        w, i = router.route_topk(torch.randn(512, EXPERTS, device=device, generator=g), TOP_K)
+        out = torch.empty_like(x)
+        backend = QuantizedExpertBackend(0)
+        for _ in range(rounds):
+            backend.forward(x, i, w, bank, out=out)
+    elif workload == "prefill":
         bank = make_layer_bank(LAYERS, device)
         g = torch.Generator(device=device).manual_seed(PREFILL_SEED)
         x = torch.randn(PREFILL_TOKENS, HIDDEN, device=device, generator=g).bfloat16()
@@ -221,7 +235,7 @@ def pmc_pass(workload: str = "decode", rounds: int = 8, copy_mib: int = 256):
     for _ in range(4):
         torch.mul(src, 1.0, out=dst)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_pass": {"workload": workload, "calls": rounds * (1 if workload == "prefill" else LAYERS),
+    print(json.dumps({"pmc_pass": {"workload": workload, "calls": rounds * (LAYERS if workload == "decode" else 1),
                                    "copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}}),
           flush=True)
 
@@ -596,8 +610,9 @@ def main():
     parser.add_argument("--no-prefill", action="store_true")
     parser.add_argument("--no-quant", action="store_true")
     parser.add_argument("--no-block", action="store_true")
-    parser.add_argument("--pmc-pass", nargs="?", const="decode", choices=("decode", "prefill"),
-                        help="run the eager counter-collection workload (decode or prefill) instead of the benchmark")
+    parser.add_argument("--pmc-pass", nargs="?", const="decode", choices=("decode", "prefill", "w4a16"),
+                        help="run the eager counter-collection workload (decode, 2048-token FP8 prefill or "
+                             "512-token W4A16 prefill) instead of the benchmark")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path is built and "
