@@ -1128,26 +1128,19 @@ int dmoe_quant_projection(const DmoeQuantProj* proj, int experts, int mode, cons
     });
 }
 
-int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype, int64_t x_row_stride, int rows,
-                           int row_div, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
-                           int pairs, int top_k, void* out, int out_dtype, int64_t out_row_stride, float* out_pairs,
-                           void* workspace, size_t workspace_bytes, int* status, void* stream) {
-    return checked([&] {
+// The packed-bank forward of dmoe_quant_moe_forward (modes 0-3).  With
+// `route`, the pairs are routed from its logits first (ids / weights are
+// then its outputs): inside the small-call gate/up kernel when both small
+// kernels take the call, else by the router kernel.
+static void quant_forward_impl(const DmoeQuantBank* bank, const void* x, int x_dtype, int64_t x_row_stride,
+                               int rows, int row_div, const void* ids, int ids_dtype, const void* weights,
+                               int weights_dtype, int pairs, int top_k, void* out, int out_dtype,
+                               int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes,
+                               int* status, hipStream_t st, const dmoe::RouteSource* route) {
+    {
         require(bank != nullptr, "packed bank descriptor is required");
         const int E = bank->experts, mode = bank->mode;
         require(E >= 1 && E <= dmoe::kMaxExperts, "expert count outside [1, 512]");
-        if (is_g128_mode(mode)) {
-            const BankGeom g = check_g128_bank(bank);
-            require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 1048576]");
-            require(row_div >= 1 && rows >= 1 && (int64_t)(pairs - 1) / row_div < rows,
-                    "pairs read past the activation rows");
-            check_routes(ids, ids_dtype, weights, weights_dtype);
-            if (out_pairs == nullptr) check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
-            g128_forward(g, x, x_dtype, x_row_stride, rows, row_div, ids, ids_dtype, weights, weights_dtype, pairs,
-                         top_k, out, out_dtype, out_row_stride, out_pairs, workspace, workspace_bytes, status,
-                         as_stream(stream));
-            return;
-        }
         dmoe::QuantProjArgs up = check_quant_proj(bank->w13, mode, E);
         dmoe::QuantProjArgs dn = check_quant_proj(bank->w2, mode, E);
         const int H = up.K, I = up.N / 2;
@@ -1157,18 +1150,32 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
         check_routes(ids, ids_dtype, weights, weights_dtype);
         if (out_pairs == nullptr) check_output(BankGeom{{}, {}, E, H, I}, out, out_dtype, out_row_stride, pairs, top_k);
         const QuantWorkspace ws = take_quant_workspace(rows, pairs, E, H, I, workspace, workspace_bytes);
-        hipStream_t st = as_stream(stream);
         // small calls: launches that group the pairs themselves and keep the
         // activation rotation (modes 1-3) and the combine inside
         const bool small_up = fused_enabled() && dmoe::quant_gateup_decode_fits(mode, pairs, rows, H, I, x, x_dtype,
                                                                                  x_row_stride);
         const bool small_dn = fused_enabled() && dmoe::quant_down_decode_fits(mode, pairs, H, I);
+        const bool self_routed = route != nullptr && small_up && small_dn &&
+                                 dmoe::quant_gateup_decode_routes(E, route->top_k);
+        if (route != nullptr && !self_routed) {
+            const dmoe::RouteArgs ra{route->logits, route->logits_row_stride, rows, E, route->top_k,
+                                     route->renormalize != 0, route->ids_out, route->weights_out, route->w_dtype};
+            dmoe::launch_route_topk(ra, st);
+        }
         if (!small_up || !small_dn) quant_group(ids, ids_dtype, pairs, E, ws, status, st);
         const int max_active = std::min(pairs, E);
 
         if (small_up) {
-            const dmoe::QuantGateUpArgs ga{up, x, x_dtype, x_row_stride, rows, row_div, ids, ids_dtype, E, pairs,
-                                           ws.act, status};
+            dmoe::QuantGateUpArgs ga{up, x, x_dtype, x_row_stride, rows, row_div, ids, ids_dtype, E, pairs,
+                                     ws.act, status};
+            if (self_routed) {
+                ga.logits = route->logits;
+                ga.logits_row_stride = route->logits_row_stride;
+                ga.renormalize = route->renormalize;
+                ga.ids_out = route->ids_out;
+                ga.weights_out = route->weights_out;
+                ga.w_dtype = route->w_dtype;
+            }
             dmoe::launch_quant_gateup_decode(ga, st);
         } else {
             quant_operand(up, x, x_dtype, x_row_stride, rows, H, ws.xq, ws.xs, st);
@@ -1210,6 +1217,32 @@ int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype
                                        out, out_dtype, out_row_stride};
             dmoe::launch_combine(ca, st);
         }
+    }
+}
+
+int dmoe_quant_moe_forward(const DmoeQuantBank* bank, const void* x, int x_dtype, int64_t x_row_stride, int rows,
+                           int row_div, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                           int pairs, int top_k, void* out, int out_dtype, int64_t out_row_stride, float* out_pairs,
+                           void* workspace, size_t workspace_bytes, int* status, void* stream) {
+    return checked([&] {
+        require(bank != nullptr, "packed bank descriptor is required");
+        const int E = bank->experts, mode = bank->mode;
+        require(E >= 1 && E <= dmoe::kMaxExperts, "expert count outside [1, 512]");
+        if (is_g128_mode(mode)) {
+            const BankGeom g = check_g128_bank(bank);
+            require(pairs >= 1 && pairs <= dmoe::kMaxPermutePairs, "pair count outside [1, 1048576]");
+            require(row_div >= 1 && rows >= 1 && (int64_t)(pairs - 1) / row_div < rows,
+                    "pairs read past the activation rows");
+            check_routes(ids, ids_dtype, weights, weights_dtype);
+            if (out_pairs == nullptr) check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
+            g128_forward(g, x, x_dtype, x_row_stride, rows, row_div, ids, ids_dtype, weights, weights_dtype, pairs,
+                         top_k, out, out_dtype, out_row_stride, out_pairs, workspace, workspace_bytes, status,
+                         as_stream(stream));
+            return;
+        }
+        quant_forward_impl(bank, x, x_dtype, x_row_stride, rows, row_div, ids, ids_dtype, weights, weights_dtype,
+                           pairs, top_k, out, out_dtype, out_row_stride, out_pairs, workspace, workspace_bytes, status,
+                           as_stream(stream), nullptr);
     });
 }
 
@@ -1237,14 +1270,13 @@ int dmoe_quant_moe_layer(const DmoeQuantBank* bank, const void* x, int x_dtype, 
                             out_row_stride, nullptr, workspace, workspace_bytes, status, st);
             return;
         }
-        // route, then the experts from the written routes
-        const dmoe::RouteArgs ra{logits, logits_row_stride, tokens, bank->experts, top_k, renormalize != 0,
-                                 ids_out, weights_out, weights_dtype};
-        dmoe::launch_route_topk(ra, st);
-        if (dmoe_quant_moe_forward(bank, x, x_dtype, x_row_stride, tokens, top_k, ids_out, DMOE_I64, weights_out,
-                                   weights_dtype, pairs, top_k, out, out_dtype, out_row_stride, nullptr, workspace,
-                                   workspace_bytes, status, stream) != 0)
-            throw AbiError(g_last_error);
+        // the experts from routes the call computes first (inside the
+        // small-call gate/up kernel when it takes the call)
+        const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
+                                      ids_out, weights_out, weights_dtype};
+        quant_forward_impl(bank, x, x_dtype, x_row_stride, tokens, top_k, ids_out, DMOE_I64, weights_out,
+                           weights_dtype, pairs, top_k, out, out_dtype, out_row_stride, nullptr, workspace,
+                           workspace_bytes, status, st, &route);
     });
 }
 

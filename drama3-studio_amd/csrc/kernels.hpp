@@ -376,12 +376,24 @@ struct QuantGateUpArgs {
     int ids_dtype, experts, pairs;
     uint16_t* act;
     int* status;
+    // With logits: the pairs are routed in the kernel instead (row_div =
+    // top_k, pairs = rows * top_k; ids unused); workgroup (0, 0) writes the
+    // routes to ids_out (int64) and weights_out (w_dtype).
+    const float* logits;
+    int64_t logits_row_stride;
+    int renormalize;
+    int64_t* ids_out;
+    void* weights_out;
+    int w_dtype;
 };
 // Calls of at most 64 pairs over at most 4 rows whose activation rows are
 // 16-byte aligned (pointer and row stride).
 bool quant_gateup_decode_fits(int mode, int pairs, int rows, int H, int I, const void* x, int x_dtype,
                               int64_t x_row_stride);
 void launch_quant_gateup_decode(const QuantGateUpArgs& a, hipStream_t stream);
+// Whether the small-call gate/up kernel can route the call itself (up to 2 *
+// 64 experts and top-8: one wave per token, the router kernel's sorting network).
+inline bool quant_gateup_decode_routes(int experts, int top_k) { return experts <= 128 && top_k <= 8; }
 
 // Down projection * route weight + the slot-order combine of a small call,
 // from the bf16 hidden rows [pairs, I].

@@ -29,6 +29,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "route.hpp"
 
 namespace dmoe {
 
@@ -649,6 +650,7 @@ struct QGateUpLds {
     float sa[kQgMaxRows];
     uint32_t rmax[kQgMaxRows];  // row maxima (non-negative float bits)
     float book[16];
+    int rid[kSmallPairs];               // routed in the kernel: expert of each pair
     alignas(16) int8_t qtab[256 * 16];  // mode 3: INT8 weight of (scale byte, code)
     union {
         float tb[kQWaves][kRotWaveDwords];  // rotation transposes
@@ -672,8 +674,21 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
     const int n0 = blockIdx.y * (NT == 3 ? 24 : 16);
 
     // loads are issued unconditionally (clamped indexes): a load merged with
-    // a constant on another path is waited for at the merge
-    const uint2 idb = load_id_bits(a.ids, min(lane, P - 1), a.ids_dtype);
+    // a constant on another path is waited for at the merge.  Two words per
+    // lane: the pair's route id, or (routing in the kernel) this wave's
+    // token's logits of experts lane and lane + 64 (waves past the tokens
+    // load the last token's and ignore them).
+    const uint32_t *p0, *p1;
+    if (a.logits) {
+        const float* lrow = a.logits + (int64_t)min(wave, rows - 1) * a.logits_row_stride;
+        p0 = (const uint32_t*)(lrow + min(lane, a.experts - 1));
+        p1 = (const uint32_t*)(lrow + min(lane + kWave, a.experts - 1));
+    } else {
+        const int i = min(lane, P - 1);
+        p0 = a.ids_dtype == kI64 ? (const uint32_t*)a.ids + 2 * i : (const uint32_t*)a.ids + i;
+        p1 = a.ids_dtype == kI64 ? p0 + 1 : p0;
+    }
+    const uint2 idb = {*p0, *p1};
     // activation rows: every load issued now (clamped to the last unit)
     const int nb = H / 256, units = rows * nb;
     const int my_u = kQgUnits * wave + lane / 16;  // this lane's block (16 lanes each)
@@ -697,7 +712,30 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
             if (i < chunks) *(v4i*)(s.x.h + (i / cpr) * H + (i % cpr) * 8) = c16[j];
         }
     }
-    if (wave == 0) {
+    if (a.logits) {
+        // router softmax / top-k / renormalization of token `wave`, the router
+        // kernel's bits (route_topk_kernel's sorting network)
+        if (wave < rows) {
+            float l[kRouteLaneSlots];
+#pragma unroll
+            for (int j = 0; j < kRouteLaneSlots; ++j) l[j] = 0.0f;
+            l[0] = __uint_as_float(idb.x);
+            l[1] = __uint_as_float(idb.y);
+            const int top_k = a.row_div;
+            int id;
+            float wgt;
+            wave_route_small(l, a.experts, top_k, a.renormalize, id, wgt);
+            if (lane < top_k) {
+                s.rid[wave * top_k + lane] = id;
+                if (blockIdx.x == 0 && blockIdx.y == 0) {
+                    a.ids_out[wave * top_k + lane] = id;
+                    store_from_f32(a.weights_out, wave * top_k + lane, a.w_dtype, wgt);
+                }
+            }
+        }
+        lds_barrier();
+        if (wave == 0) group_pairs(lane < P ? s.rid[lane] : -1, lane, s.g);
+    } else if (wave == 0) {
         const int pe = lane < P ? id_expert(idb, a.ids_dtype, a.experts) : -1;
         if (lane < P && pe < 0 && blockIdx.x == 0 && blockIdx.y == 0) raise_status(a.status, kBadExpertId);
         group_pairs(pe, lane, s.g);
