@@ -156,7 +156,37 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(PrepArgs a) {
     const RouteSource& src = a.route;
     for (int e = threadIdx.x; e < E; e += 256) flag[e] = 0;
     for (int i = threadIdx.x; i < E * (kMaxDecodePairs / 32); i += 256) (&mask[0][0])[i] = 0;
-    if (src.logits) {
+    if (src.logits && E <= 2 * kWave) {
+        // one wave per token, the logits in registers: route_tokens' router
+        // (the same bits), four tokens at a time
+        const int tokens = P / src.top_k, lane = threadIdx.x % kWave;
+        for (int t = threadIdx.x / kWave; t < tokens; t += 256 / kWave) {
+            const float* row = src.logits + (int64_t)t * src.logits_row_stride;
+            float l[kRouteLaneSlots];
+#pragma unroll
+            for (int j = 0; j < kRouteLaneSlots; ++j) {
+                const int e = lane + kWave * j;
+                l[j] = e < E ? row[e] : 0.0f;
+            }
+            int id;
+            float w;
+            if (src.top_k <= 8) wave_route_small(l, E, src.top_k, src.renormalize, id, w);
+            else wave_route_token(l, E, src.top_k, src.renormalize, id, w);
+            if (lane < src.top_k) {
+                const int p = t * src.top_k + lane;
+                sid[p] = (int16_t)id;
+                src.ids_out[p] = id;
+                store_from_f32(src.weights_out, p, src.w_dtype, w);
+            }
+        }
+        __syncthreads();  // every token's slots are in sid
+        for (int p = threadIdx.x; p < P; p += 256) {
+            if (sid[p] < 0 || sid[p] >= E) {
+                raise_status(a.status, kNonFinite);
+                sid[p] = -1;
+            }
+        }
+    } else if (src.logits) {
         const int tokens = P / src.top_k;
         const int chunk = max(1, min(kRouteTokens, kRouteElems / E));
         for (int t0 = 0; t0 < tokens; t0 += chunk)

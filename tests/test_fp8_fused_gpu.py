@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from conftest import print_case
-from drama_moe import _lib, fp8_decode, fp8_moe
+from drama_moe import _lib, fp8_decode, fp8_moe, router
 from drama_moe.formats import random_fp8_bank
 from drama_moe.offload import HipExpertBackend
 from oracle import oracle as orc
@@ -104,6 +104,30 @@ def test_fused_router_ties_and_partial_lanes(cuda, decode_mode, experts, tokens,
     assert torch.equal(fo, so)
     eids, _ = orc.route_topk(logits.cpu().numpy(), top_k)
     np.testing.assert_array_equal(fi.cpu().numpy(), eids)
+
+
+@pytest.mark.parametrize("experts,tokens,top_k,tied", [(128, 16, 8, False), (128, 32, 8, True), (100, 12, 8, True),
+                                                        (64, 20, 12, False)])
+def test_three_launch_routed_layer_matches_router_kernel(cuda, experts, tokens, top_k, tied):
+    """Routed calls past the single-launch limit (65-256 pairs) route in the
+    prep kernel, one wave per token: ids and weights equal the router
+    kernel's, the output equals the expert call on those routes, and no
+    status bit is raised (every token's slots are in place before they are
+    validated)."""
+    print_case("three-launch routed layer", experts, tokens, top_k, tied)
+    g = torch.Generator().manual_seed(4242 + experts + tokens)
+    staged = to_device(random_fp8_bank(experts, 1024, 256, layout="channel", generator=g), cuda)
+    x = torch.randn(tokens, 1024, generator=g).bfloat16().to(cuda)
+    logits = (torch.randint(0, 8, (tokens, experts), generator=g).float() / 4.0 if tied
+              else torch.randn(tokens, experts, generator=g)).to(cuda)
+    backend = HipExpertBackend()
+    backend.status(cuda)
+    out, w, ids = backend.forward_routed(x, logits, top_k, staged)
+    rw, rids = router.route_topk(logits, top_k)
+    torch.cuda.synchronize()
+    assert backend.status(cuda) == 0
+    assert torch.equal(ids, rids) and torch.equal(w, rw)
+    assert torch.equal(out, backend.forward(x, rids, rw, staged))
 
 
 def test_fused_pairs_shared_row_and_quantized_handoff(cuda, decode_mode):
