@@ -189,6 +189,17 @@ class CheckpointTensors:
             raise ValueError(f"No safetensors files in {root}")
         return cls(files)
 
+    def close(self) -> None:
+        """Drop the file handles (tensors already read stay valid)."""
+        self._where.clear()
+        self._handles.clear()
+
+    def __enter__(self) -> "CheckpointTensors":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
     def names(self):
         return self._where.keys()
 
@@ -482,16 +493,33 @@ def load_expert_bank(tensors: CheckpointTensors, layer: int, geometry: BankGeome
     return _to_device(bank, device)
 
 
+def bind_expert_bank(module, bank) -> None:
+    """Make ``module`` (a routed-expert module) hold ``bank`` the way the
+    reference's loaders bind one (quantized_model.py:106-111,
+    shared_checkpoint.py:128-130): the four bank tensors as its
+    w13_weight / w13_scale_inv / w2_weight / w2_scale_inv buffers, plus the
+    packed store itself for the packed modes, so install_expert_offload
+    finds it."""
+    bank.validate()
+    for name in ("w13_weight", "w13_scale_inv", "w2_weight", "w2_scale_inv"):
+        module._buffers[name] = getattr(bank, name)
+    if isinstance(bank, QuantizedStore):
+        module._drama_quant_store = bank
+    else:
+        module.fp8 = True
+        module.__dict__.pop("_drama_quant_store", None)
+
+
 def load_expert_banks(directory, *, device, layers=None) -> list:
     """Every layer's routed-expert bank of the checkpoint in ``directory``
     (or the layers listed), resident on ``device``."""
     root = Path(directory).resolve()
     geometry = BankGeometry.from_config(_read_json(root / "config.json"))
     fmt = expert_format(root)
-    tensors = CheckpointTensors.from_directory(root)
-    if fmt == "fp8-shared":
-        check_packed_fp8_names(tensors, geometry)
-    elif fmt == "fp8":
-        check_official_fp8_names(tensors, geometry)
-    chosen = range(geometry.layers) if layers is None else layers
-    return [load_expert_bank(tensors, layer, geometry, fmt, device=device) for layer in chosen]
+    with CheckpointTensors.from_directory(root) as tensors:
+        if fmt == "fp8-shared":
+            check_packed_fp8_names(tensors, geometry)
+        elif fmt == "fp8":
+            check_official_fp8_names(tensors, geometry)
+        chosen = range(geometry.layers) if layers is None else layers
+        return [load_expert_bank(tensors, layer, geometry, fmt, device=device) for layer in chosen]

@@ -253,3 +253,24 @@ def test_quantization_mode_and_geometry_checks(tmp_path):
                                                        "moe_intermediate_size": 8}})
     geometry = ckpt.BankGeometry.from_config(json.loads((tmp_path / "config.json").read_text()))
     assert geometry == ckpt.BankGeometry(1, 2, 128, 128)
+
+
+def test_bound_banks_are_what_the_expert_manager_runs(tmp_path):
+    """bind_expert_bank makes a module hold a loaded bank the way the
+    reference's loaders do, and the expert manager resolves exactly that bank."""
+    from torch import nn
+
+    from drama_moe import offload
+    g = torch.Generator().manual_seed(12)
+    fp8 = fp8_banks(1, 4, 128, 128)[0]
+    packed = random_quantized_bank(2, 4, 256, 256, generator=g)
+    for bank in (fp8, packed):
+        module = nn.Module()
+        ckpt.bind_expert_bank(module, bank)
+        resolved = offload.store_from_module(module)
+        assert resolved is bank if bank is packed else same_bank(resolved, bank)
+        assert module.w13_weight is bank.w13_weight
+    module = nn.Module()
+    ckpt.bind_expert_bank(module, packed)
+    ckpt.bind_expert_bank(module, fp8)  # rebinding to FP8 drops the packed store
+    assert isinstance(offload.store_from_module(module), StagedExperts)
