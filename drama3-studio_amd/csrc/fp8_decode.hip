@@ -56,6 +56,25 @@ __device__ int wave_pairs_of(const Grouping* g, int ai, int pairs, int* out) {
     return count;
 }
 
+// The same from the expert's mask words already in registers (8 words: up
+// to kMaxDecodePairs pairs).
+__device__ int wave_pairs_of_words(const uint32_t (&mw)[kMaxDecodePairs / 32], int pairs, int* out) {
+    const int lane = threadIdx.x % kWave;
+    int count = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxDecodePairs / kWave; ++j) {
+        const int c = j * kWave;
+        if (c >= pairs) break;
+        const int p = c + lane;
+        const uint32_t w = lane < 32 ? mw[2 * j] : mw[2 * j + 1];
+        const bool on = p < pairs && ((w >> (lane % 32)) & 1u);
+        const uint64_t bits = __ballot(on);
+        if (on) out[count + __popcll(bits & ((1ull << lane) - 1))] = p;
+        count += __popcll(bits);
+    }
+    return count;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- gate / up
@@ -81,9 +100,37 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
     const int n0 = blockIdx.y * 16;
     const int col = lane % 16, grp = lane / 16;
     int* rows = s.rows[wave];
-    const int M = wave_pairs_of(gr, blockIdx.x, a.pairs, rows);  // per wave: no barrier
     const v4f zero = {0, 0, 0, 0};
     const v8i zero8i = {0, 0, 0, 0, 0, 0, 0, 0};
+
+    // The expert's pair mask, then the weight stream (it needs only the
+    // expert), then the pair list from the mask words: they were issued
+    // before the weights, so they land first (loads retire in issue order)
+    // and the activation rows follow while the weights are in flight.
+    uint32_t mw[kMaxDecodePairs / 32];
+    {
+        const uint4* mp = (const uint4*)gr->mask[blockIdx.x];
+        const uint4 m0 = mp[0], m1 = mp[1];
+        mw[0] = m0.x; mw[1] = m0.y; mw[2] = m0.z; mw[3] = m0.w;
+        mw[4] = m1.x; mw[5] = m1.y; mw[6] = m1.z; mw[7] = m1.w;
+    }
+    asm volatile("" ::: "memory");
+    const uint8_t* wg = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)(n0 + col) * a.w13.w_sn;
+    const uint8_t* wu = wg + (int64_t)I * a.w13.w_sn;
+    WRaw<WF> bg[KBW], bu[KBW];
+    float swg[KBW], swu[KBW];
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+        const int kb = wave + i * kUpWaves;
+        if (kb < KB) {
+            bg[i] = load_wraw<WF>(wg, H, kb, grp);
+            bu[i] = load_wraw<WF>(wu, H, kb, grp);
+            swg[i] = proj_scale<WF>(a.w13, e, n0 + col, kb);
+            swu[i] = proj_scale<WF>(a.w13, e, I + n0 + col, kb);
+        }
+    }
+    asm volatile("" ::: "memory");
+    const int M = wave_pairs_of_words(mw, a.pairs, rows);  // per wave: no barrier
 
     // A fragments of a pass: lane (col, grp) holds row `col` (< mc), K slice
     // grp; per-row activation scales for the C rows 4 * grp + r (grp 0 only).
@@ -105,24 +152,10 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
         }
     };
 
-    // activation fragments of the first pass, then the weight stream
+    // activation fragments of the first pass
     v8i af[KBW];
     float sx[KBW][4];
     load_a(0, min(kRowsPerPass, M), af, sx);
-    const uint8_t* wg = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)(n0 + col) * a.w13.w_sn;
-    const uint8_t* wu = wg + (int64_t)I * a.w13.w_sn;
-    WRaw<WF> bg[KBW], bu[KBW];
-    float swg[KBW], swu[KBW];
-#pragma unroll
-    for (int i = 0; i < KBW; ++i) {
-        const int kb = wave + i * kUpWaves;
-        if (kb < KB) {
-            bg[i] = load_wraw<WF>(wg, H, kb, grp);
-            bu[i] = load_wraw<WF>(wu, H, kb, grp);
-            swg[i] = proj_scale<WF>(a.w13, e, n0 + col, kb);
-            swu[i] = proj_scale<WF>(a.w13, e, I + n0 + col, kb);
-        }
-    }
 
     for (int m0 = 0; m0 < M; m0 += kRowsPerPass) {
         const int mc = min(kRowsPerPass, M - m0);
