@@ -64,6 +64,8 @@ class MoeBlock:
         logits = torch.empty((tokens, self.num_experts), dtype=torch.float32, device=x.device)
         sgate = torch.empty(tokens, dtype=torch.bfloat16, device=x.device)
         act = torch.empty((tokens, self.shared_inter), dtype=torch.bfloat16, device=x.device)
+        if tokens == 0:
+            return logits, sgate, act
         lib = _lib.library()
         _lib.check(lib.dmoe_moe_block_pre(
             _lib.ptr(x), x.stride(0), tokens, self.hidden, _lib.ptr(self.router_weight), self.router_weight.stride(0),
@@ -80,6 +82,8 @@ class MoeBlock:
         if out is None:
             out = torch.empty_like(residual)
         out = _bf16_rows(out, "output", self.hidden, residual.shape[0])
+        if residual.shape[0] == 0:
+            return out
         lib = _lib.library()
         _lib.check(lib.dmoe_moe_block_post(
             _lib.ptr(act), act.stride(0), residual.shape[0], self.shared_inter, _lib.ptr(self.down_proj),
@@ -93,6 +97,10 @@ class MoeBlock:
         if mlp_input.shape != after_mixer.shape:
             raise ValueError("mlp_input and after_mixer must have the same shape")
         logits, sgate, act = self.pre(mlp_input)
+        if mlp_input.shape[0] == 0:
+            empty = torch.empty((0, self.top_k), device=mlp_input.device)
+            out = self.post(act, sgate, torch.empty_like(after_mixer), after_mixer, out=out)
+            return out, empty.to(mlp_input.dtype), empty.long()
         experts_out, weights, ids = self.backend.forward_routed(mlp_input, logits, self.top_k, self.experts,
                                                                 renormalize=self.norm_topk_prob)
         return self.post(act, sgate, experts_out, after_mixer, out=out), weights, ids

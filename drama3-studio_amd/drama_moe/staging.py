@@ -203,6 +203,8 @@ class HostResidency:
         if x.is_cuda and torch.cuda.is_current_stream_capturing():
             raise RuntimeError("Host-resident experts cannot run inside a hipGraph capture: "
                                "each call reads its route ids back")
+        if x.shape[0] == 0:
+            return torch.zeros_like(x)
         host = self.host_bank(key, bank)
         experts = host.w13_weight.shape[0]
         host_ids = ids.to("cpu", torch.int64)

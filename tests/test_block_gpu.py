@@ -120,3 +120,16 @@ def test_moe_block_in_hipgraph(cuda):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, expected), step
+
+
+def test_moe_block_empty_call(cuda):
+    g = torch.Generator().manual_seed(5)
+    rw, sw, gw, uw, dw = weights(256, 16, 64, g)
+    bank = random_fp8_bank(16, 256, 128, layout="channel", generator=g)
+    dev = StagedExperts(*(getattr(bank, n).to(cuda) for n in ("w13_weight", "w13_scale_inv", "w2_weight",
+                                                               "w2_scale_inv")))
+    blk = block.MoeBlock(rw.to(cuda), sw.to(cuda), gw.to(cuda), uw.to(cuda), dw.to(cuda), dev, HipExpertBackend(),
+                         top_k=4)
+    x = torch.zeros(0, 256, dtype=torch.bfloat16, device=cuda)
+    out, w, ids = blk(x, x.clone())
+    assert out.shape == (0, 256) and w.shape == (0, 4) and ids.shape == (0, 4)

@@ -192,3 +192,10 @@ def test_manager_host_mode_routes_through_the_tier(bank):
     assert torch.equal(got, backend.forward(x, ids, w, bank))
     assert manager.host.calls == 1
     manager.close()
+
+
+def test_empty_call_returns_empty_rows(bank):
+    tier = host()
+    out = tier.forward("a", bank, SignatureBackend(), torch.zeros(0, 128), torch.zeros(0, 2, dtype=torch.long),
+                       torch.zeros(0, 2))
+    assert out.shape == (0, 128) and tier.calls == 0
