@@ -35,15 +35,15 @@ def slot_order_sum(pairs, tokens, top_k):
     return total
 
 
-@pytest.mark.parametrize("mode", ["fp8", 0])
+@pytest.mark.parametrize("mode", ["fp8", 0, 1, 2, 3, 4])
 def test_host_resident_calls_match_the_resident_bank(cuda, mode):
     print_case("host residency", mode)
     g = torch.Generator().manual_seed(501)
     if mode == "fp8":
         bank, backend = random_fp8_bank(EXPERTS, HIDDEN, INTER, layout="channel", generator=g), HipExpertBackend()
     else:
-        bank = random_quantized_bank(0, EXPERTS, HIDDEN, INTER, asymmetric=True, generator=g)
-        backend = QuantizedExpertBackend(0)
+        bank = random_quantized_bank(mode, EXPERTS, HIDDEN, INTER, asymmetric=mode == 0, generator=g)
+        backend = QuantizedExpertBackend(mode)
     resident = staging.device_copy(bank, cuda)
     tier = staging.HostResidency(max_staged_experts=8, max_pair_rows=64, cache_experts=6)
     # decode tokens through the hot cache (and the pool for the overflow), then
