@@ -36,8 +36,9 @@
 // read touches spread over the banks.  The scales of each K block (activation
 // or hidden groups, weight channels or 128x128 blocks) ride in the same
 // stages.  Tile lists are XCD-aware: each XCD takes a contiguous range of
-// (column tile, expert tile) work, so the tiles of one expert that share a
-// weight tile run on the same XCD at the same time and share its L2.
+// expert-major (expert, column tile, row tile) work, so the tiles of one
+// expert, which share weight rows and activation rows, run on the same XCD at
+// about the same time and share its L2.
 #include <algorithm>
 
 #include "common.hpp"
@@ -301,9 +302,17 @@ __device__ __forceinline__ void grouped_tiles(const typename OP::Args& a) {
         const int ntc = min(kChunk, (xend - c0 + nwx - 1) / nwx);
         __syncthreads();  // the previous chunk is done with the metadata
         if (threadIdx.x < ntc) {
+            // Work item L -> (column tile, row tile), expert-major: expert e's
+            // c row tiles (the first is t0) own items [ncol t0, ncol (t0 + c)),
+            // column tile by column tile, so an expert's tiles run together on
+            // one XCD and share its weight and activation rows in that L2.
             const int L = c0 + threadIdx.x * nwx;
-            const int mt = L % nvt, e = a.tile_expert[mt], m0 = a.tile_m0[mt];
-            s.meta[threadIdx.x] = TileMeta{L / nvt, e, m0, min(a.offsets[e + 1], m0 + kGroupM)};
+            const int ncol = OP::col_tiles(a), q = L / ncol, eq = a.tile_expert[q];
+            const int t0 = q - (a.tile_m0[q] - a.offsets[eq]) / kGroupM;
+            const int c = (a.offsets[eq + 1] - a.offsets[eq] + kGroupM - 1) / kGroupM;
+            const int r = L - ncol * t0, mt = t0 + r % c;
+            const int e = a.tile_expert[mt], m0 = a.tile_m0[mt];
+            s.meta[threadIdx.x] = TileMeta{r / c, e, m0, min(a.offsets[e + 1], m0 + kGroupM)};
         }
         __syncthreads();
         for (int i = threadIdx.x; i < ntc * kGroupM; i += kGThreads)
