@@ -38,7 +38,12 @@ namespace dmoe {
 namespace {
 
 constexpr int kUpWaves = 8, kUpThreads = kUpWaves * kWave;
-constexpr int kDnWaves = 4, kDnThreads = kDnWaves * kWave;
+// Down kernel waves per workgroup: each wave walks its own batches of two
+// experts, whose pair lists, activation rows and hidden scales are dependent
+// global reads; more waves split that chain. Eight where the kernel fits 256
+// registers (two waves per SIMD), else four.
+constexpr int kDnMaxWaves = 8;
+constexpr int dn_waves(int wf, int kb2) { return kb2 >= 8 || (wf == kWfInt6 && kb2 >= 6) ? 4 : 8; }
 constexpr int kRowsPerPass = 4;  // activation rows per MFMA pass of the gate/up kernel
 
 // Pairs of active expert `ai` in ascending order into `out` (one whole wave);
@@ -223,7 +228,7 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
 
 struct DownLds {
     float wt[kMaxDecodePairs];                  // route weights of all pairs, fp32
-    int rows[kDnWaves][2][kMaxDecodePairs];     // pairs of the wave's two experts
+    int rows[kDnMaxWaves][2][kMaxDecodePairs];  // pairs of the wave's two experts
     float part[kMaxDecodePairs][8];
     alignas(16) uint8_t hq[kDownQuantBytes];    // hidden FP8 quantized here (small decode)
     float hs[kDownQuantBytes / 128];
@@ -256,7 +261,8 @@ __device__ __forceinline__ void load_down_batch(const DownArgs& a, int num_activ
 // WF = weight format; KB2 = upper bound of the 128-column K blocks of the
 // down projection (I <= 128 * KB2); the runtime count KB guards every block.
 template <int WF, int KB2>
-__global__ __launch_bounds__(kDnThreads) void fp8_down_decode_kernel(DownArgs a) {
+__global__ __launch_bounds__(dn_waves(WF, KB2) * kWave) void fp8_down_decode_kernel(DownArgs a) {
+    constexpr int kDnWaves = dn_waves(WF, KB2), kDnThreads = kDnWaves * kWave;
     __shared__ DownLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int col = lane % 16, grp = lane / 16;
@@ -394,14 +400,17 @@ void launch_gateup_format(const GateUpArgs& a, int max_active, hipStream_t strea
 
 template <int WF>
 void launch_down_format(const DownArgs& a, hipStream_t stream) {
-    const dim3 grid(a.w2.N / 8), block(kDnThreads);
+    const dim3 grid(a.w2.N / 8);
     const int kb = a.w2.K / 128;
-    if (kb <= 2) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 2>), grid, block, 0, stream, a);
-    else if (kb <= 4) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 4>), grid, block, 0, stream, a);
-    else if (kb <= 6) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 6>), grid, block, 0, stream, a);
-    else if (kb <= 8) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 8>), grid, block, 0, stream, a);
-    else if (kb <= 16) hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 16>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((fp8_down_decode_kernel<WF, 32>), grid, block, 0, stream, a);
+    auto go = [&](auto kernel, int kb2) {
+        hipLaunchKernelGGL(kernel, grid, dim3(dn_waves(WF, kb2) * kWave), 0, stream, a);
+    };
+    if (kb <= 2) go(fp8_down_decode_kernel<WF, 2>, 2);
+    else if (kb <= 4) go(fp8_down_decode_kernel<WF, 4>, 4);
+    else if (kb <= 6) go(fp8_down_decode_kernel<WF, 6>, 6);
+    else if (kb <= 8) go(fp8_down_decode_kernel<WF, 8>, 8);
+    else if (kb <= 16) go(fp8_down_decode_kernel<WF, 16>, 16);
+    else go(fp8_down_decode_kernel<WF, 32>, 32);
 }
 
 }  // namespace
