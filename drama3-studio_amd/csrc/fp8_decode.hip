@@ -46,23 +46,9 @@ constexpr int kDnMaxWaves = 8;
 constexpr int dn_waves(int wf, int kb2) { return kb2 >= 8 || (wf == kWfInt6 && kb2 >= 6) ? 4 : 8; }
 constexpr int kRowsPerPass = 4;  // activation rows per MFMA pass of the gate/up kernel
 
-// Pairs of active expert `ai` in ascending order into `out` (one whole wave);
-// returns the count.  The pair set is the grouping's bitmask.
-__device__ int wave_pairs_of(const Grouping* g, int ai, int pairs, int* out) {
-    const int lane = threadIdx.x % kWave;
-    int count = 0;
-    for (int c = 0; c < pairs; c += kWave) {
-        const int p = c + lane;
-        const bool on = p < pairs && ((g->mask[ai][p / 32] >> (p % 32)) & 1u);
-        const uint64_t bits = __ballot(on);
-        if (on) out[count + __popcll(bits & ((1ull << lane) - 1))] = p;
-        count += __popcll(bits);
-    }
-    return count;
-}
-
-// The same from the expert's mask words already in registers (8 words: up
-// to kMaxDecodePairs pairs).
+// Pairs of an active expert in ascending order into `out` (one whole wave),
+// from the expert's mask words already in registers (8 words: up to
+// kMaxDecodePairs pairs); returns the count.
 __device__ int wave_pairs_of_words(const uint32_t (&mw)[kMaxDecodePairs / 32], int pairs, int* out) {
     const int lane = threadIdx.x % kWave;
     int count = 0;
@@ -239,14 +225,22 @@ struct DownBatch {
     WRaw<WF> b[KB2];
     float sw[KB2];
     int ai0, ai1;  // active indices of the two experts (ai1 = -1: none)
+    uint32_t mw[2][kMaxDecodePairs / 32];  // the two experts' pair masks (wave-uniform loads)
 };
 
 // Batch bi = active experts 2 bi and 2 bi + 1 (if any).
 template <int WF, int KB2>
 __device__ __forceinline__ void load_down_batch(const DownArgs& a, int num_active, int bi, int n0, int col, int grp,
                                                 int KB, DownBatch<WF, KB2>& bt) {
-    bt.ai0 = 2 * bi;
-    bt.ai1 = 2 * bi + 1 < num_active ? 2 * bi + 1 : -1;
+    bt.ai0 = __builtin_amdgcn_readfirstlane(2 * bi);  // wave-uniform: the mask loads below are scalar
+    bt.ai1 = 2 * bi + 1 < num_active ? bt.ai0 + 1 : -1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint4* mp = (const uint4*)a.grouping->mask[h == 1 && bt.ai1 >= 0 ? bt.ai1 : bt.ai0];
+        const uint4 m0 = mp[0], m1 = mp[1];
+        bt.mw[h][0] = m0.x; bt.mw[h][1] = m0.y; bt.mw[h][2] = m0.z; bt.mw[h][3] = m0.w;
+        bt.mw[h][4] = m1.x; bt.mw[h][5] = m1.y; bt.mw[h][6] = m1.z; bt.mw[h][7] = m1.w;
+    }
     const int ai = col < 8 ? bt.ai0 : bt.ai1;
     const int e = ai >= 0 ? a.grouping->expert[ai] : -1;
     const int n = n0 + (col & 7);
@@ -316,8 +310,9 @@ __global__ __launch_bounds__(dn_waves(WF, KB2) * kWave) void fp8_down_decode_ker
     const float* hs = a.quantize_hidden ? s.hs : a.hs;
 
     for (int bi = wave; bi < batches; bi += kDnWaves) {
-        const int M0 = wave_pairs_of(a.grouping, cur.ai0, a.pairs, s.rows[wave][0]);
-        const int M1 = cur.ai1 >= 0 ? wave_pairs_of(a.grouping, cur.ai1, a.pairs, s.rows[wave][1]) : 0;
+        // pair lists from the masks that came with the batch's weights
+        const int M0 = wave_pairs_of_words(cur.mw[0], a.pairs, s.rows[wave][0]);
+        const int M1 = cur.ai1 >= 0 ? wave_pairs_of_words(cur.mw[1], a.pairs, s.rows[wave][1]) : 0;
         const int passes = max((M0 + 7) / 8, (M1 + 7) / 8);
         // pair of A row `row` (0..7: expert ai0, 8..15: expert ai1) in a pass
         auto a_row = [&](int pass, int row) -> int {
