@@ -201,6 +201,44 @@ def test_prefill_2048_tokens_full_shape(cuda, x_group):
     assert torch.isfinite(out.float()).all()
 
 
+@pytest.mark.parametrize("x_group", ["token", 128])
+def test_grouped_work_lists_longer_than_one_chunk(cuda, x_group):
+    """8192 tokens x top-8 over 64 experts at H 1280, I 768: both grouped GEMMs
+    have more (column tile, row tile) work items than the persistent grid
+    holds in one chunk of tile metadata per workgroup (gate/up 6 x ~1100,
+    down 5 x ~1100 items over 256 workgroups of 16-item chunks), so the
+    expert-major work order runs across chunk boundaries.  Every token within
+    the bar of the decode kernels on the same routes (32-token calls), and 32
+    spread tokens against the oracle."""
+    print_case("grouped multi-chunk", x_group)
+    experts, hidden, inter, tokens = 64, 1280, 768, 8192
+    staged = random_fp8_bank(experts, hidden, inter, layout="channel", device=cuda,
+                             generator=torch.Generator(device=cuda).manual_seed(20261204))
+    g = torch.Generator().manual_seed(20261204)
+    x = torch.randn(tokens, hidden, generator=g).bfloat16()
+    logits = zipf_logits(tokens, experts, 20261204)
+    backend = HipExpertBackend(x_group=x_group)
+    xd = x.to(cuda)
+    out, weights, ids = backend.forward_routed(xd, logits.to(cuda), 8, staged)
+    counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=experts)
+    row_tiles = int(((counts + 63) // 64).sum())
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    assert min(inter // 128, (hidden + 255) // 256) * row_tiles > 16 * (cus // 8 * 8)  # > one chunk each
+    decode = torch.cat([backend.forward(xd[t:t + 32], ids[t:t + 32], weights[t:t + 32], staged)
+                        for t in range(0, tokens, 32)])
+    torch.cuda.synchronize()
+    assert backend.status(cuda) == 0
+    got, ref = out.float(), decode.float()
+    per_token = ((got - ref).abs().amax(1) / ref.abs().amax(1).clamp_min(1e-30)).cpu().numpy()
+    assert per_token.max() < TOL, (int(per_token.argmax()), float(per_token.max()))
+    pick = np.linspace(0, tokens - 1, 32).astype(int)
+    b13, b2 = oracle_banks(staged)
+    expected = orc.fp8_moe_forward(b13, b2, x.float().numpy()[pick], ids.cpu().numpy()[pick],
+                                   weights.float().cpu().numpy()[pick],
+                                   x_group=128 if x_group == 128 else hidden)
+    assert rel_inf(out.float().cpu().numpy()[pick], expected) < TOL
+
+
 @pytest.mark.parametrize("pairs,experts,block_m,zipf", [
     (16384, 128, 64, True),    # the prefill workload's tile map (one-launch placement)
     (16384, 128, 16, True),
