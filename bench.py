@@ -294,7 +294,9 @@ def run_prefill(reps: int = 10):
                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                         "roofline_frac": round(max(tflops / FP8_PEAK_TFLOPS, gbs / HBM_PEAK_GBS), 4)}
     result.update({"tokens": PREFILL_TOKENS, "top_k": TOP_K, "experts": EXPERTS, "routing": "zipf1.1",
-                   "alg_gflop": round(flops / 1e9, 2), "alg_mb": round(nbytes / 1e6, 1)})
+                   "alg_gflop": round(flops / 1e9, 2), "alg_mb": round(nbytes / 1e6, 1),
+                   "mfma_frac_is": "algorithmic flops / measured time / FP8 dense peak",
+                   "mfma_busy_counters": prefill_mfma_busy()})
     return result
 
 
@@ -587,6 +589,26 @@ def cpu_baseline(budget_s: float = 8.0):
 
 
 TRAFFIC_SUMMARY = ROOT / "profiles" / "fp8_fused_decode_kernel_moe_layer_b1_hbm_traffic.txt"
+
+
+PREFILL_COUNTERS = ROOT / "profiles" / "fp8_grouped_prefill_2048_counters.txt"
+
+
+def prefill_mfma_busy():
+    """SQ_VALU_MFMA_BUSY_CYCLES fractions of the grouped prefill GEMMs from the
+    committed counter summary of the 2048-token layer, or None."""
+    try:
+        busy = {}
+        for text in PREFILL_COUNTERS.read_text().splitlines():
+            if text.startswith("mfma_busy_"):
+                key, value = text.split(":", 1)
+                busy[key[len("mfma_busy_"):]] = float(value)
+        if busy:
+            busy["source"] = str(PREFILL_COUNTERS.relative_to(ROOT))
+            return busy
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def measured_traffic():
