@@ -286,6 +286,9 @@ def run_prefill(reps: int = 10):
             backend.forward_routed(x, logits, TOP_K, bank, out=out)
         stop.record()
         torch.cuda.synchronize()
+        status = backend.status(device)
+        if status:
+            raise RuntimeError(f"prefill calls raised device status bits {status:#x}")
         us = start.elapsed_time(stop) * 1e3 / reps
         tflops = flops / (us * 1e-6) / 1e12
         gbs = nbytes / (us * 1e-6) / 1e9
