@@ -85,10 +85,10 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
     __shared__ GateUpLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const Grouping* gr = a.grouping;
-    if ((int)blockIdx.x >= gr->num_active) return;
-    const int e = gr->expert[blockIdx.x];
+    if ((int)blockIdx.y >= gr->num_active) return;
+    const int e = gr->expert[blockIdx.y];
     const int I = a.w13.N / 2, H = a.w13.K, KB = H / 128;
-    const int n0 = blockIdx.y * 16;
+    const int n0 = blockIdx.x * 16;
     const int col = lane % 16, grp = lane / 16;
     int* rows = s.rows[wave];
     const v4f zero = {0, 0, 0, 0};
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
     // and the activation rows follow while the weights are in flight.
     uint32_t mw[kMaxDecodePairs / 32];
     {
-        const uint4* mp = (const uint4*)gr->mask[blockIdx.x];
+        const uint4* mp = (const uint4*)gr->mask[blockIdx.y];
         const uint4 m0 = mp[0], m1 = mp[1];
         mw[0] = m0.x; mw[1] = m0.y; mw[2] = m0.z; mw[3] = m0.w;
         mw[4] = m1.x; mw[5] = m1.y; mw[6] = m1.z; mw[7] = m1.w;
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
     // The last of the 8 column tiles of this 128-group quantizes it: one
     // 16-lane row per pair, 8 values per lane, read coherently.
     const int group = n0 / 128;
-    int* counter = a.counters + (int64_t)blockIdx.x * (I / 128) + group;
+    int* counter = a.counters + (int64_t)blockIdx.y * (I / 128) + group;
     if (!arrive_last(counter, 128 / 16, &s.last)) return;
     for (int m = threadIdx.x / 16; m < M; m += kUpThreads / 16) {
         const int64_t p = s.rows[0][m];
@@ -385,7 +385,7 @@ namespace {
 
 template <int WF>
 void launch_gateup_format(const GateUpArgs& a, int max_active, hipStream_t stream) {
-    const dim3 grid(max_active, a.w13.N / 2 / 16), block(kUpThreads);
+    const dim3 grid(a.w13.N / 2 / 16, max_active), block(kUpThreads);  // experts slowest: idle ones last
     const int kbw = (a.w13.K / 128 + kUpWaves - 1) / kUpWaves;
     if (kbw <= 1) hipLaunchKernelGGL((fp8_gateup_decode_kernel<WF, 1>), grid, block, 0, stream, a);
     else if (kbw <= 2) hipLaunchKernelGGL((fp8_gateup_decode_kernel<WF, 2>), grid, block, 0, stream, a);
