@@ -49,6 +49,16 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 // Process-wide switch of the single-launch decode (dmoe_set_fused_decode).
 std::atomic<int> g_fused_decode{1};
 bool fused_enabled() { return g_fused_decode.load(std::memory_order_relaxed) != 0; }
+// FP8 calls take the single launch up to kFusedPreferPairs pairs in the
+// default mode (1): above that the three launches were measured faster on
+// this chip (1 / 2 / 3 / 4 / 8 tokens x top-8: 20.6 / 32.7 / 42.6 / 51.9 /
+// 84.7 us fused vs 23.2 / 33.9 / 41.9 / 48.6 / 78.2 us); mode 2 takes it
+// whenever it fits (<= 64 pairs).
+constexpr int kFusedPreferPairs = 16;
+bool fp8_fused_wanted(int pairs) {
+    const int mode = g_fused_decode.load(std::memory_order_relaxed);
+    return mode == 2 || (mode == 1 && pairs <= kFusedPreferPairs);
+}
 
 // Bound of the single-launch decode's hand-off wait, in ticks of the 100 MHz
 // real-time counter (dmoe_set_sync_spin_limit); 200 ms by default.
@@ -309,7 +319,7 @@ void fp8_decode_call(const BankGeom& g, Activations a, const dmoe::RouteSource& 
                  int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes, int* status,
                  hipStream_t stream) {
     const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
-    if (fused_enabled() && fp8_fused_call(g, a, route, weights, weights_dtype, pairs, top_k, gu_dtype, out,
+    if (fp8_fused_wanted(pairs) && fp8_fused_call(g, a, route, weights, weights_dtype, pairs, top_k, gu_dtype, out,
                                           out_dtype, out_row_stride, out_pairs, ws, status, stream))
         return;
     const bool in_down = down_quantizes(g, pairs);
@@ -672,7 +682,7 @@ extern "C" {
 
 int dmoe_abi_version(void) { return DMOE_ABI_VERSION; }
 
-int dmoe_set_fused_decode(int enabled) { return g_fused_decode.exchange(enabled != 0 ? 1 : 0); }
+int dmoe_set_fused_decode(int mode) { return g_fused_decode.exchange(mode <= 0 ? 0 : mode >= 2 ? 2 : 1); }
 
 uint64_t dmoe_set_sync_spin_limit(uint64_t ticks) { return g_spin_ticks.exchange(ticks); }
 

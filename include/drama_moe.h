@@ -74,12 +74,14 @@ typedef struct DmoeFp8Bank {
  * (native/include/drama_native.h:16; runtime.cpp:288). */
 DMOE_API int dmoe_abi_version(void);
 
-/* Process-wide switch of the single-launch decode (default on): decode calls
- * of at most 64 route pairs whose activation rows (rows * H <= 16 KiB) and
- * hidden (pairs * I <= 48 KiB) fit run as ONE persistent launch of one
- * workgroup per CU that routes, projects and combines with a grid-wide
- * hand-off inside; 0 selects the three-launch decode for every call (A/B
- * measurement).  Returns the previous setting.  The fused launch occupies
+/* Process-wide switch of the single-launch decode.  Mode 1 (the default):
+ * FP8 decode calls of at most 16 route pairs (above that the three launches
+ * are faster) whose activation rows (rows * H <= 16 KiB) and hidden
+ * (pairs * I <= 48 KiB) fit run as ONE persistent launch of one workgroup
+ * per CU that routes, projects and combines with a grid-wide hand-off
+ * inside; mode 2 takes that launch for every FP8 call it fits (at most 64
+ * pairs); 0 selects the three-launch decode for every call (A/B
+ * measurement).  Returns the previous mode.  The fused launch occupies
  * every CU and waits on its own workgroups: work on other streams of the
  * same device delays it, and a wait that exceeds the bound of
  * dmoe_set_sync_spin_limit (200 ms by default) gives up with
@@ -89,7 +91,7 @@ DMOE_API int dmoe_abi_version(void);
  * separate rotation, projection and combine launches.  No counterpart in the
  * reference (its decode is per-route-slot Triton launches,
  * fp8_decode.py:114-147). */
-DMOE_API int dmoe_set_fused_decode(int enabled);
+DMOE_API int dmoe_set_fused_decode(int mode);
 
 /* Process-wide bound of the single-launch decode's hand-off wait, in ticks
  * of the GPU's 100 MHz real-time counter (default 20,000,000 = 200 ms).  A

@@ -47,7 +47,7 @@ def decode_mode():
     lib = _lib.library()
 
     def set_mode(fused: bool) -> None:
-        lib.dmoe_set_fused_decode(1 if fused else 0)
+        lib.dmoe_set_fused_decode(2 if fused else 0)
 
     yield set_mode
     lib.dmoe_set_fused_decode(1)

@@ -46,7 +46,7 @@ def bank(cuda):
 def test_noalloc_layer_equals_workspace_layer(cuda, bank, fused, token_counts):
     staged, desc = bank
     lib = _lib.library()
-    previous = lib.dmoe_set_fused_decode(1 if fused else 0)
+    previous = lib.dmoe_set_fused_decode(2 if fused else 0)
     try:
         g = torch.Generator(device=cuda).manual_seed(7 + token_counts[0])
         for tokens in token_counts:
