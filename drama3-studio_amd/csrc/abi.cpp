@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <map>
 #include <mutex>
+#include <numeric>
 #include <stdexcept>
 #include <string>
 
@@ -595,15 +596,27 @@ void g128_forward(const BankGeom& g, const void* x, int x_dtype, int64_t x_row_s
                   size_t workspace_bytes, int* status, hipStream_t stream) {
     const Activations full{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, rows, row_div, g.H};
     check_activations(g, full, pairs);
-    require(out_pairs != nullptr || top_k <= dmoe::kMaxDecodePairs, "top_k above 256 for a group-128 layer call");
+    // A chunk starts at a row boundary and, for a layer combine, holds whole
+    // tokens: its pair count is a multiple of lcm(row_div, top_k) (rows of at
+    // most 256 pairs) or stays inside one row (longer rows, cut at tokens).
+    const bool combine = out_pairs == nullptr;
+    int step = row_div;
+    if (combine && row_div <= dmoe::kMaxDecodePairs) {
+        step = row_div / std::gcd(row_div, top_k) * top_k;
+        require(step <= dmoe::kMaxDecodePairs, "group-128 layer call: lcm(row_div, top_k) above 256 route pairs");
+    } else if (combine) {
+        require(top_k <= dmoe::kMaxDecodePairs && row_div % top_k == 0,
+                "group-128 layer call: pairs per row must be a multiple of top_k (at most 256)");
+    }
+    const int cap = combine ? (dmoe::kMaxDecodePairs / top_k) * top_k : dmoe::kMaxDecodePairs;
     const int gu_dtype = x_dtype;
     for (int p0 = 0; p0 < pairs;) {
         const int r0 = p0 / row_div;
         int count, div = row_div;
         if (row_div <= dmoe::kMaxDecodePairs) {
-            count = std::min(pairs - p0, (dmoe::kMaxDecodePairs / row_div) * row_div);
+            count = std::min(pairs - p0, (dmoe::kMaxDecodePairs / step) * step);
         } else {  // many pairs per row: a chunk stays inside one row
-            count = std::min({pairs - p0, dmoe::kMaxDecodePairs, (r0 + 1) * row_div - p0});
+            count = std::min({pairs - p0, cap, (r0 + 1) * row_div - p0});
             div = count;
         }
         const Activations a{static_cast<const char*>(x) + (int64_t)r0 * x_row_stride * element_size(x_dtype), x_dtype,
@@ -678,6 +691,12 @@ void* static_scratch() {
 
 }  // namespace
 
+namespace dmoe {
+// The calling thread's last-error message, for the host-only entry points of
+// the cooperative decode's CPU executor (cpu_experts.cpp).
+void set_last_error(const char* message) { g_last_error = message ? message : ""; }
+}  // namespace dmoe
+
 extern "C" {
 
 int dmoe_abi_version(void) { return DMOE_ABI_VERSION; }
@@ -689,6 +708,34 @@ uint64_t dmoe_set_sync_spin_limit(uint64_t ticks) { return g_spin_ticks.exchange
 int dmoe_debug_force_sync_timeout(int force) { return g_force_timeout.exchange(force != 0 ? 1 : 0); }
 
 const char* dmoe_last_error(void) { return g_last_error.c_str(); }
+
+int dmoe_silu_table(float* table, void* stream) {
+    return checked([&] {
+        require(table != nullptr && reinterpret_cast<uintptr_t>(table) % 4 == 0, "SiLU table buffer is required");
+        dmoe::launch_silu_table(table, as_stream(stream));
+    });
+}
+
+int dmoe_combine_slots(const float* partials, int64_t partial_row_stride, const void* ids, int ids_dtype, int experts,
+                       int tokens, int top_k, int hidden, void* out, int out_dtype, int64_t out_row_stride,
+                       void* stream) {
+    return checked([&] {
+        require(partials && ids && out, "combine buffers are required");
+        require(is_id_dtype(ids_dtype), "route ids must be int32 or int64");
+        require(is_float_dtype(out_dtype), "output must be fp32, bf16 or fp16");
+        require(experts >= 1 && top_k >= 1 && tokens >= 0 && hidden >= 8 && hidden % 8 == 0,
+                "combine: bad experts, top_k, tokens or hidden size");
+        require((int64_t)tokens * top_k <= dmoe::kMaxPermutePairs, "more than 1048576 route pairs per call");
+        require(partial_row_stride >= hidden && partial_row_stride % 4 == 0 &&
+                    reinterpret_cast<uintptr_t>(partials) % 16 == 0,
+                "partial rows must be contiguous and 16-byte aligned");
+        require(out_row_stride >= hidden, "output row stride smaller than the hidden size");
+        if (!tokens) return;
+        const dmoe::CombineArgs ca{partials, partial_row_stride, ids, ids_dtype, experts, tokens, top_k, hidden,
+                                   out, out_dtype, out_row_stride};
+        dmoe::launch_combine(ca, as_stream(stream));
+    });
+}
 
 int dmoe_decode_fp8(const uint8_t* values, float* out, int64_t count, void* stream) {
     return checked([&] {
@@ -1268,16 +1315,30 @@ int dmoe_quant_moe_layer(const DmoeQuantBank* bank, const void* x, int x_dtype, 
         require(ids_out && weights_out && is_float_dtype(weights_dtype), "routing outputs are required");
         const int pairs = checked_pairs(tokens, top_k);
         hipStream_t st = as_stream(stream);
-        if (is_g128_mode(bank->mode) && pairs <= dmoe::kMaxDecodePairs) {
-            // one decode call that routes itself (the single-launch kernel when it fits)
+        if (is_g128_mode(bank->mode)) {
             const BankGeom g = check_g128_bank(bank);
             const Activations a{x, x_dtype, x_row_stride, nullptr, nullptr, 0, 0, tokens, top_k, g.H};
             check_activations(g, a, pairs);
             check_output(g, out, out_dtype, out_row_stride, pairs, top_k);
-            const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k, renormalize != 0,
-                                          ids_out, weights_out, weights_dtype};
-            fp8_decode_call(g, a, route, weights_out, weights_dtype, pairs, top_k, x_dtype, out, out_dtype,
-                            out_row_stride, nullptr, workspace, workspace_bytes, status, st);
+            if (pairs <= dmoe::kMaxDecodePairs) {
+                // one decode call that routes itself (the single-launch kernel when it fits)
+                const dmoe::RouteSource route{nullptr, DMOE_I64, logits, logits_row_stride, top_k,
+                                              renormalize != 0, ids_out, weights_out, weights_dtype};
+                fp8_decode_call(g, a, route, weights_out, weights_dtype, pairs, top_k, x_dtype, out, out_dtype,
+                                out_row_stride, nullptr, workspace, workspace_bytes, status, st);
+                return;
+            }
+            // larger calls: the router kernel into the caller's routing outputs,
+            // then the experts over those routes as consecutive decode calls
+            const size_t need = fp8_workspace_layout(dmoe::kMaxDecodePairs, g.H, g.I, nullptr, nullptr);
+            require(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+            require(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+            const dmoe::RouteArgs ra{logits, logits_row_stride, tokens, g.experts, top_k, renormalize != 0,
+                                     ids_out, weights_out, weights_dtype};
+            dmoe::launch_route_topk(ra, st);
+            g128_forward(g, x, x_dtype, x_row_stride, tokens, top_k, ids_out, DMOE_I64, weights_out, weights_dtype,
+                         pairs, top_k, out, out_dtype, out_row_stride, nullptr, workspace, workspace_bytes, status,
+                         st);
             return;
         }
         // the experts from routes the call computes first (inside the

@@ -183,7 +183,7 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
                     g = round_through(g, a.gu_dtype);
                     u = round_through(u, a.gu_dtype);
                     float* dst = a.h32 + (int64_t)rows[m0 + r] * I + n0 + col;
-                    const float h = g / (1.0f + __expf(-g)) * u;
+                    const float h = silu_f32(g) * u;
                     if (a.quantize_hidden) store_coherent(dst, h);
                     else *dst = h;
                 }

@@ -528,7 +528,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                     }
                     g = round_through(g, a.gu_dtype);
                     up = round_through(up, a.gu_dtype);
-                    const float h = g / (1.0f + __expf(-g)) * up;
+                    const float h = silu_f32(g) * up;
                     const int p = s.plist[s.ucoord[d][1] + pass * 16 + m];
                     // column 8 a + b of a 128-group lives at word 16 b + a (see the reader)
                     const int word = (c0 / 128) * 128 + c * 16 + (c0 % 128) / 8;

@@ -109,6 +109,13 @@ __device__ __forceinline__ float absmax8(const F8& x, int* status) {
     return m;
 }
 
+// SiLU of a gate value as every FP8 decode kernel computes it: g / (1 +
+// e^-g) with the fast exponential and a correctly rounded division.  The
+// cooperative decode's CPU executor reads this function's values for every
+// bf16 gate from a table the device fills with it (dmoe_silu_table), so its
+// hidden activations match the device's bit for bit.
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+
 // The FP8 scale of a group whose max |v| is amax (reference contract):
 // max(amax, 1e-10) * fl(1/448).
 __device__ __forceinline__ float fp8_group_scale(float amax) { return fmaxf(amax, 1e-10f) * (1.0f / 448.0f); }

@@ -244,6 +244,7 @@ void launch_fp8_gateup_decode(const GateUpArgs& a, int max_active, hipStream_t s
 void launch_fp8_down_decode(const DownArgs& a, hipStream_t stream);
 void launch_fp8_quantize(const QuantArgs& a, hipStream_t stream);
 void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stream);
+void launch_silu_table(float* table, hipStream_t stream);
 void launch_route_topk(const RouteArgs& a, hipStream_t stream);
 void launch_route_quantize(const RouteArgs& r, const QuantArgs& q, hipStream_t stream);
 void launch_permute(const PermuteArgs& a, hipStream_t stream);

@@ -30,7 +30,7 @@ __device__ void quantize_unit128(const QuantArgs& a, int64_t unit) {
     if (a.silu_mul) {
         F8 g = load8(a.x, base + c0 + col * 8, a.x_dtype), u = load8(a.x, base + a.cols + c0 + col * 8, a.x_dtype);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v.v[j] = g.v[j] / (1.0f + __expf(-g.v[j])) * u.v[j];
+        for (int j = 0; j < 8; ++j) v.v[j] = silu_f32(g.v[j]) * u.v[j];
     } else {
         v = load8(a.x, base + c0 + col * 8, a.x_dtype);
     }
@@ -79,6 +79,17 @@ __global__ void fp8_decode_kernel(const uint8_t* v, float* out, int64_t n) {
 
 void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stream) {
     hipLaunchKernelGGL(fp8_decode_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, v, out, n);
+}
+
+// SiLU of every bf16 gate value, as the FP8 decode kernels compute it:
+// table[b] = silu_f32(the bf16 value with bits b), 65536 entries.
+__global__ __launch_bounds__(256) void silu_table_kernel(float* table) {
+    const int b = blockIdx.x * 256 + threadIdx.x;  // grid 256 x 256: every bit pattern once
+    table[b] = silu_f32(bf16_to_f32((uint16_t)b));
+}
+
+void launch_silu_table(float* table, hipStream_t stream) {
+    hipLaunchKernelGGL(silu_table_kernel, dim3(256), dim3(256), 0, stream, table);
 }
 
 // ------------------------------------------------------------------ router

@@ -91,6 +91,16 @@ _SIGNATURES = {
     "dmoe_moe_block_post": ([_P, _L, _I, _I, _P, _L, _I, _P, _P, _L, _P, _L, _P, _L, _P], _I),
     "dmoe_fp8_quantized_pairs": ([ctypes.POINTER(Fp8Bank), _P, _P, _L, _L, _I, _I, _I, _P, _I, _P,
                                   _I, _I, _I, _P, _P, ctypes.c_size_t, _P, _P], _I),
+    "dmoe_combine_slots": ([_P, _L, _P, _I, _I, _I, _I, _I, _P, _I, _L, _P], _I),
+    "dmoe_silu_table": ([_P, _P], _I),
+    "dmoe_cpu_executor_create": ([_I, _I, _I, _I, _I], _P),
+    "dmoe_cpu_executor_destroy": ([_P], None),
+    "dmoe_cpu_executor_isa": ([_P], _I),
+    "dmoe_cpu_executor_threads": ([_P], _I),
+    "dmoe_cpu_executor_set_guard": ([_P, _I], _I),
+    "dmoe_cpu_executor_set_silu_table": ([_P, _P], _I),
+    "dmoe_cpu_expert_pairs": ([_P, ctypes.POINTER(Fp8Bank), _P, _P, _I, _P, _P, _I, _P], _I),
+    "dmoe_cpu_partition_routes": ([_P, _I, _P, _I, _I, _I, _P, _P], _I),
 }
 
 _lib = None

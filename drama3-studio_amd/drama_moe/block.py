@@ -81,7 +81,12 @@ class MoeBlock:
         experts_out = _bf16_rows(experts_out, "experts output", self.hidden, residual.shape[0])
         if out is None:
             out = torch.empty_like(residual)
-        out = _bf16_rows(out, "output", self.hidden, residual.shape[0])
+        elif (out.dtype != torch.bfloat16 or tuple(out.shape) != tuple(residual.shape) or out.stride(1) != 1
+              or (out.stride(0) * 2) % 16 or out.data_ptr() % 16 or out.device != residual.device):
+            # the kernel writes the caller's buffer itself: a substitute copy
+            # would leave it unwritten (and allocate inside a graph capture)
+            raise ValueError(f"out must be bf16 [{residual.shape[0]}, {self.hidden}] on the input's device with "
+                             "contiguous, 16-byte aligned rows")
         if residual.shape[0] == 0:
             return out
         lib = _lib.library()

@@ -366,6 +366,7 @@ class ResidentExpertManager:
         self._banks: dict[int, tuple] = {}
         self._device_banks: dict[int, tuple] = {}
         self._packed_backends: dict[int, object] = {}
+        self.hybrid_decode = None
         self._closed = False
 
     def _require_open(self) -> None:
@@ -408,6 +409,8 @@ class ResidentExpertManager:
         if x.shape[0] == 0:
             return torch.zeros_like(x)
         backend = self._backend_for(bank)
+        if self.hybrid_decode is not None and self.hybrid_decode.eligible(module, x, topk_ids):
+            return self.hybrid_decode.forward(module, bank, x, topk_ids, topk_weights)
         if self.host is not None:
             return self.host.forward(id(module), bank, backend, x, topk_ids, topk_weights)
         if self.validate_ids:
@@ -429,7 +432,34 @@ class ResidentExpertManager:
             self._device_banks[id(module)] = cached
         return cached[1]
 
+    def configure_hybrid_decode(self, cpu_jobs: int = 0, *, threads: int = 4, device=None,
+                                synchronize_return: bool = True, guard_fp8_boundaries: bool = True):
+        """Give ``cpu_jobs`` (1-8) route slots of each eligible one-token FP8
+        decode call to host cores (drama_moe.hybrid.HybridDecodeRuntime; the
+        reference's configure_hybrid_decode, offload.py:1289-1308); 0 turns
+        the mode off.  Needs host-held FP8 banks."""
+        self._require_open()
+        if isinstance(cpu_jobs, bool) or not isinstance(cpu_jobs, int) or not 0 <= cpu_jobs <= 8:
+            raise ValueError("Hybrid CPU jobs must be an integer from 0 to 8")
+        if isinstance(threads, bool) or not isinstance(threads, int) or not 1 <= threads <= 64:
+            raise ValueError("Hybrid native threads must be an integer from 1 to 64")
+        replacement = None
+        if cpu_jobs:
+            from .hybrid import HybridDecodeRuntime
+
+            replacement = HybridDecodeRuntime(
+                self, cpu_jobs=cpu_jobs, threads=threads,
+                device=device if device is not None else torch.device("cuda", torch.cuda.current_device()),
+                synchronize_return=synchronize_return, guard_fp8_boundaries=guard_fp8_boundaries)
+        if self.hybrid_decode is not None:
+            self.hybrid_decode.close()
+        self.hybrid_decode = replacement
+        return replacement
+
     def close(self) -> None:
+        if self.hybrid_decode is not None:
+            self.hybrid_decode.close()
+            self.hybrid_decode = None
         for module in self.modules.values():
             routed = module.__dict__.get("forward")
             if isinstance(routed, _RoutedForward):

@@ -437,6 +437,88 @@ DMOE_API int dmoe_moe_block_post(const void* shared_act, int64_t act_row_stride,
                                  const void* residual, int64_t residual_row_stride, void* out,
                                  int64_t out_row_stride, void* stream);
 
+/* Slot-order combine of ordered weighted partials: out[t] = out_dtype(the
+ * fp32 sum over slots j = 0 .. top_k-1 of partials[t * top_k + j], summed in
+ * slot order); pairs whose id (ids [tokens * top_k], int32 or int64) lies
+ * outside [0, experts) contribute nothing.  partials [tokens * top_k, hidden]
+ * fp32 with 16-byte aligned rows (row stride in elements), hidden a multiple
+ * of 8.  Replaces .view(T, k, H).sum(1).to(dtype) of the manager's grouped
+ * calls (offload.py:1242-1244) and the ordered merge of the cooperative
+ * decode, ordered.sum(0).to(bfloat16) (hybrid_decode.py:303-310). */
+DMOE_API int dmoe_combine_slots(const float* partials, int64_t partial_row_stride, const void* ids, int ids_dtype,
+                                int experts, int tokens, int top_k, int hidden, void* out, int out_dtype,
+                                int64_t out_row_stride, void* stream);
+
+/* ---------------------------------------------- cooperative decode: host side
+ *
+ * The reference can give the lowest-ranked route slots of a one-token FP8
+ * decode to host cores while the GPU runs the others (HybridDecodeRuntime,
+ * src/drama_low_vram/hybrid_decode.py:33-416, over the native executor of
+ * native/src/runtime.cpp:68-335).  These entry points are that executor:
+ * host pointers (a DmoeFp8Bank here describes a bank in host memory),
+ * synchronous, thread-safe per executor (calls on one executor are
+ * serialized).  Its arithmetic is the FP8 decode kernels' own, step for step
+ * (block products rounded once from their exact value, the kernels' K order,
+ * bf16 gate/up, the device's SiLU values from dmoe_silu_table, FP8 hidden
+ * groups, down fma chain, route weight), so a slot computed here equals the
+ * device's. */
+
+/* Returned by dmoe_cpu_expert_pairs when, with the guard on, the hidden
+ * quantization of a slot landed within 4 fp32 ulps of an E4M3 rounding
+ * midpoint: `out` holds nothing usable and the caller recomputes the slots
+ * on the GPU.  Replaces the "GPU FP8 rounding boundary requires fallback"
+ * error (fp8_reference.cpp:68-86) that native_backend.py:151-152 turns into
+ * NativeQuantizationBoundary. */
+#define DMOE_CPU_GPU_RECOMPUTE 1
+
+/* Executor for banks of `hidden` x `inter` (multiples of 128) and up to
+ * `capacity` route slots per call, with a pool of `threads` host threads
+ * (the caller counts as one) and block products in vector ISA `isa` (0: the
+ * best this host has; 1 scalar, 2 AVX2 + F16C, 3 AVX-512; all give the same
+ * bits).  NULL on error (dmoe_last_error).  Replaces drama_executor_create /
+ * drama_executor_destroy (native/include/drama_native.h:40-42). */
+DMOE_API void* dmoe_cpu_executor_create(int hidden, int inter, int capacity, int threads, int isa);
+DMOE_API void dmoe_cpu_executor_destroy(void* executor);
+
+/* Vector ISA the executor's block products use: 1 scalar, 2 AVX2 + F16C,
+ * 3 AVX-512.  Replaces drama_executor_implementation (drama_native.h:43). */
+DMOE_API int dmoe_cpu_executor_isa(void* executor);
+
+/* Threads of the executor's pool. */
+DMOE_API int dmoe_cpu_executor_threads(void* executor);
+
+/* Turns the E4M3 midpoint guard on (1) or off (0).  Replaces
+ * drama_executor_set_quantization_guard (drama_native.h:52). */
+DMOE_API int dmoe_cpu_executor_set_guard(void* executor, int enabled);
+
+/* Borrows the 65536-entry host table of dmoe_silu_table (kept alive by the
+ * caller); required before the first call.  Replaces
+ * drama_executor_set_silu_table (drama_native.h:49). */
+DMOE_API int dmoe_cpu_executor_set_silu_table(void* executor, const float* table);
+
+/* Weighted fp32 partials out [jobs, hidden] of `jobs` route slots (expert
+ * ids [jobs] int64, weights [jobs] fp32) for one activation row already
+ * quantized to FP8 by the device: xq [hidden] E4M3 bytes, xs its scales
+ * ([hidden/128] for x_group 128, [1] for x_group = hidden).  Returns 0,
+ * DMOE_CPU_GPU_RECOMPUTE, or -1 (dmoe_last_error; every argument is checked
+ * before any work).  Replaces drama_executor_forward_quantized
+ * (drama_native.h:63-69). */
+DMOE_API int dmoe_cpu_expert_pairs(void* executor, const DmoeFp8Bank* bank, const uint8_t* xq, const float* xs,
+                                   int x_group, const int64_t* ids, const float* weights, int jobs, float* out);
+
+/* Route planning of the cooperative decode: cpu_jobs of the `count` route
+ * slots go to the host -- slots whose expert is not in `resident` first, each
+ * kind from the lowest-ranked slot up -- and the rest to the GPU; both lists
+ * in ascending slot order.  Replaces drama_partition_routes
+ * (drama_native.h:33-36; runtime.cpp:291-335). */
+DMOE_API int dmoe_cpu_partition_routes(const int64_t* ids, int count, const int64_t* resident, int resident_count,
+                                       int experts, int cpu_jobs, int64_t* cpu_slots, int64_t* gpu_slots);
+
+/* Device: table [65536] fp32 = the SiLU the FP8 decode kernels apply to
+ * the bf16 gate value with bit pattern i.  Replaces build_gpu_silu_table
+ * (src/drama_low_vram/fp8_decode.py:17-21). */
+DMOE_API int dmoe_silu_table(float* table, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

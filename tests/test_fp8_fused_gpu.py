@@ -73,15 +73,21 @@ def test_fused_equals_three_launch_and_oracle(cuda, decode_mode, experts, hidden
 def test_fused_router_layer_equals_three_launch(cuda, decode_mode, tokens):
     print_case("fused routed layer", tokens)
     g = torch.Generator().manual_seed(777 + tokens)
-    staged = to_device(random_fp8_bank(128, 2048, 768, layout="channel", generator=g), cuda)
+    bank = random_fp8_bank(128, 2048, 768, layout="channel", generator=g)
+    staged = to_device(bank, cuda)
     x = torch.randn(tokens, 2048, generator=g).bfloat16().to(cuda)
     logits = torch.randn(tokens, 128, generator=g).to(cuda)
     backend = HipExpertBackend()
     (fo, fw, fi), (so, sw, si) = both(decode_mode, lambda: backend.forward_routed(x, logits, 8, staged))
     assert torch.equal(fi, si) and torch.equal(fw, sw)
     assert torch.equal(fo, so)
-    eids, _ = orc.route_topk(logits.cpu().numpy(), 8)
+    eids, ew = orc.route_topk(logits.cpu().numpy(), 8)
     np.testing.assert_array_equal(fi.cpu().numpy(), eids)
+    # the full decode layer (E 128, H 2048, I 768) against the oracle on every token
+    np.testing.assert_array_equal(fw.float().cpu().numpy(), torch.from_numpy(ew).bfloat16().float().numpy())
+    b13, b2 = oracle_banks(bank)
+    expected = orc.fp8_moe_forward(b13, b2, x.float().cpu().numpy(), eids, fw.float().cpu().numpy())
+    assert rel_inf(fo.float().cpu().numpy(), expected) < TOL
 
 
 @pytest.mark.parametrize("experts,tokens,top_k", [(128, 1, 8), (100, 3, 8), (8, 2, 8), (128, 1, 5), (64, 2, 12)])

@@ -94,6 +94,71 @@ def test_activation_quant_matches_oracle_on_wide_rows(cuda, dtype, group):
     np.testing.assert_array_equal(s.cpu().numpy(), es)
 
 
+def _e4m3_tie_rows(dtype, rows=3, cols=2048, seed=11):
+    """Rows whose every 128-group (and every row) has max |x| = 448 * 2^k, so
+    that the quantizer's scale max(amax, 1e-10) * fl(1/448) is exactly 2^k
+    and x / scale lands exactly on the chosen targets: every E4M3 value,
+    every midpoint between neighbours (ties, 2^-10 and 42.0 among them) and
+    the midpoints' neighbours one fp32 ulp away (the input type's ulp for
+    bf16 / fp16, where the fp32 neighbours are not representable)."""
+    grid = np.unique(torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().abs().numpy())
+    grid = grid[np.isfinite(grid)].astype(np.float64)
+    mids = ((grid[:-1] + grid[1:]) / 2).astype(np.float32)
+    if dtype == torch.float32:
+        near = np.concatenate([np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0))])
+    else:
+        m = torch.from_numpy(mids).to(dtype)
+        step = torch.finfo(dtype).eps * m.float().abs()
+        near = np.concatenate([(m.float() + step).to(dtype).float().numpy(), (m.float() - step).to(dtype).float().numpy()])
+    targets = np.concatenate([grid.astype(np.float32), mids, near]).astype(np.float32)
+    targets = targets[(targets > 0) & (targets < 448)]
+    rng = np.random.default_rng(seed)
+    out = np.empty((rows, cols), np.float32)
+    for r, k in zip(range(rows), (-6, 0, 5)):
+        vals = np.tile(targets, -(-(cols // 128 * 127) // targets.size))[: cols // 128 * 127]
+        vals = rng.permutation(vals) * rng.choice([-1.0, 1.0], vals.size)
+        body = vals.reshape(cols // 128, 127)
+        maxcol = np.full((cols // 128, 1), 448.0) * rng.choice([-1.0, 1.0], (cols // 128, 1))
+        out[r] = (np.concatenate([maxcol, body], 1) * 2.0 ** k).reshape(-1)
+    return torch.from_numpy(out).to(dtype), mids
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("group", [128, "row"])
+def test_activation_quant_rounds_e4m3_ties_like_the_contract(cuda, dtype, group):
+    """Device FP8 quantization at exact E4M3 rounding ties and their
+    neighbours: bytes and scales bit-exact against the oracle (the reference's
+    fp8_reference.cpp:19-36, 52-93 contract; known answers 42.0 and 2^-10 of
+    test_native_backend.py:216-231 are among the ties) and against torch's
+    independent float8_e4m3fn conversion of fl(x / scale)."""
+    print_case("quantize ties", dtype, group)
+    from drama_moe import _lib
+    from drama_moe.offload import device_state
+
+    x, mids = _e4m3_tie_rows(dtype)
+    rows, cols = x.shape
+    g = 128 if group == 128 else cols
+    q = torch.empty(rows, cols, dtype=torch.uint8, device=cuda)
+    s = torch.empty(rows, cols // g, device=cuda)
+    xd = x.to(cuda)
+    _lib.check(_lib.library().dmoe_fp8_quantize(
+        _lib.ptr(xd), _lib.dtype_code(dtype), cols, rows, cols, g, _lib.ptr(q), _lib.ptr(s),
+        _lib.ptr(device_state(cuda).status), _lib.stream_handle(cuda)))
+    xf = x.float().numpy()
+    scales = s.cpu().numpy()
+    assert np.all(np.log2(scales) == np.round(np.log2(scales)))  # exact powers of two
+    normalized = (xf.reshape(rows, -1, g) / scales[:, :, None]).reshape(rows, cols).astype(np.float32)
+    on_tie = np.isin(np.abs(normalized), mids)
+    assert on_tie.sum() >= 2 * mids.size  # every row holds the ties several times over
+    assert np.isin(np.float32(42.0), np.abs(normalized)) and np.isin(np.float32(2.0 ** -10), np.abs(normalized))
+    eq, es = orc.quantize_fp8(xf, g)
+    np.testing.assert_array_equal(scales, es)
+    got = q.cpu().numpy()
+    np.testing.assert_array_equal(got, eq)
+    independent = torch.from_numpy(normalized).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(got, independent)
+
+
 def test_silu_mul_quant_matches_oracle_within_one_step(cuda):
     print_case("silu_mul_quant")
     gu = (torch.randn(9, 2 * 768, generator=torch.Generator().manual_seed(5)) * 4).bfloat16()

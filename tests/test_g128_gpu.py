@@ -166,3 +166,104 @@ def test_g128_24_layer_decode_step_in_hipgraph(cuda, mode):
         np.testing.assert_array_equal(eager[l][2].cpu().numpy(), eids)
         expected = oracle_layer(banks[l], xs[l].float().cpu().numpy(), eids, eager[l][1].float().cpu().numpy())
         assert rel_inf(eager[l][0].float().cpu().numpy(), expected) < TOL
+
+
+@pytest.mark.parametrize("mode", [4, 5])
+def test_g128_routed_layer_above_one_decode_call(cuda, mode):
+    """Router + experts of a 100-token call (800 pairs): the router kernel
+    writes the routing, the experts run as consecutive decode calls over it.
+    Routing bit-exact with the oracle on every token, outputs within 2e-2 of
+    the oracle on tokens at both sides of every decode-call boundary."""
+    print_case("g128 routed 100 tokens", mode)
+    store = bank_on(cuda, mode, 32, 1024, 256, 51 + mode)
+    g = torch.Generator().manual_seed(700 + mode)
+    tokens = 100
+    x = torch.randn(tokens, 1024, generator=g).bfloat16()
+    logits = torch.randn(tokens, 32, generator=g)
+    backend = QuantizedExpertBackend(mode)
+    backend.status(cuda)
+    out, w, ids = backend.forward_routed(x.to(cuda), logits.to(cuda), 8, store)
+    torch.cuda.synchronize()
+    assert backend.status(cuda) == 0
+    eids, ew = orc.route_topk(logits.numpy(), 8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), eids)
+    np.testing.assert_array_equal(w.float().cpu().numpy(), torch.from_numpy(ew).bfloat16().float().numpy())
+    pick = [0, 31, 32, 63, 64, 95, 96, 99]
+    expected = oracle_layer(store, x.float().numpy()[pick], eids[pick], w.float().cpu().numpy()[pick])
+    assert rel_inf(out.float().cpu().numpy()[pick], expected) < TOL
+    # the same routes through forward() give the same bytes
+    again = backend.forward(x.to(cuda), ids, w, store)
+    assert torch.equal(again, out)
+
+
+@pytest.mark.parametrize("mode", [4, 5])
+def test_g128_moe_block_prefill_size(cuda, mode):
+    """MoeBlock over a group-128 bank at 100 tokens: the routed leg takes the
+    large-call path and the block output matches the oracle's composition."""
+    from drama_moe import block
+
+    print_case("g128 moe block 100 tokens", mode)
+    g = torch.Generator().manual_seed(880 + mode)
+    hidden, experts, inter, top_k, tokens = 512, 32, 256, 8, 100
+    store = bank_on(cuda, mode, experts, hidden, inter, 60 + mode)
+
+    def mk(*shape):
+        return (torch.randn(*shape, generator=g) * 0.03).bfloat16()
+
+    rw, sw, gw, uw, dw = mk(experts, hidden), mk(1, hidden), mk(128, hidden), mk(128, hidden), mk(hidden, 128)
+    blk = block.MoeBlock(rw.to(cuda), sw.to(cuda), gw.to(cuda), uw.to(cuda), dw.to(cuda), store,
+                         QuantizedExpertBackend(mode), top_k=top_k)
+    x = torch.randn(tokens, hidden, generator=g).bfloat16()
+    # a small residual, so the bf16 rounding of the residual sum stays far
+    # below the MoE contribution the comparison measures
+    after = (torch.randn(tokens, hidden, generator=g) / 64).bfloat16()
+    out, w, ids = blk(x.to(cuda), after.to(cuda))
+    logits, _, _ = blk.pre(x.to(cuda))
+    eids, _ = orc.route_topk(logits.cpu().numpy(), top_k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), eids)
+    f = lambda t: t.float().cpu().numpy()  # noqa: E731
+    _, want_sgate, want_act = orc.block_pre(f(x), f(rw), f(sw), f(gw), f(uw))
+    experts_out = orc.bf16_round(oracle_layer(store, f(x), eids, f(w)))
+    want = orc.block_post(want_act, f(dw), want_sgate, experts_out, f(after))
+    assert rel_inf(f(out) - f(after), want - f(after)) < TOL
+    # a supplied output the kernel cannot write in place is refused, not copied
+    with pytest.raises(ValueError, match="out must be bf16"):
+        blk(x.to(cuda), after.to(cuda), out=torch.empty(hidden, tokens, dtype=torch.bfloat16, device=cuda).t())
+
+
+@pytest.mark.parametrize("mode", [4, 5])
+def test_g128_layer_combine_with_pairs_per_row_not_top_k(cuda, mode):
+    """A direct C-ABI layer call whose rows hold 2 pairs each while tokens
+    hold 3 (row_div 2, top_k 3, 600 pairs): decode calls cut at whole tokens
+    and rows, so every token equals the oracle's sum of its three pairs."""
+    import ctypes
+
+    from drama_moe.offload import device_state
+    from drama_moe.quantized import bank_struct
+
+    print_case("g128 row_div 2 top_k 3", mode)
+    store = bank_on(cuda, mode, 16, 512, 256, 90 + mode)
+    g = torch.Generator().manual_seed(31 + mode)
+    pairs, row_div, top_k = 600, 2, 3
+    rows, tokens = pairs // row_div, pairs // top_k
+    x = torch.randn(rows, 512, generator=g).bfloat16()
+    ids = torch.randint(0, 16, (pairs,), generator=g)
+    w = (torch.rand(pairs, generator=g) + 0.1).float()
+    out = torch.empty(tokens, 512, dtype=torch.float32, device=cuda)
+    xd, idd, wd = x.to(cuda), ids.to(cuda), w.to(cuda)
+    lib = _lib.library()
+    bank = bank_struct(store)
+    state = device_state(cuda)
+    ws = state.workspace_for(lib.dmoe_quant_workspace_bytes(ctypes.byref(bank), rows, pairs))
+    _lib.check(lib.dmoe_quant_moe_forward(
+        ctypes.byref(bank), _lib.ptr(xd), _lib.dtype_code(xd.dtype), xd.stride(0), rows, row_div, _lib.ptr(idd),
+        _lib.dtype_code(idd.dtype), _lib.ptr(wd), _lib.dtype_code(wd.dtype), pairs, top_k, _lib.ptr(out),
+        _lib.F32, out.stride(0), None, _lib.ptr(ws), ws.numel(), _lib.ptr(state.status),
+        _lib.stream_handle(cuda)))
+    torch.cuda.synchronize()
+    b13, b2 = oracle_banks(store)
+    xs = x.float().numpy()
+    parts = np.concatenate([orc.fp8_expert_pairs(b13, b2, xs[p // row_div], ids[p:p + 1].numpy(),
+                                                 w[p:p + 1].numpy(), x_group=512) for p in range(pairs)])
+    expected = parts.reshape(tokens, top_k, 512).sum(1)
+    assert rel_inf(out.cpu().numpy(), expected) < TOL
