@@ -189,19 +189,74 @@ def run_gpu(steps: int, warmup: int):
     }
 
 
+PMC_WORKLOADS = ("decode", "prefill", "w4a16", "decode_multi", "packed", "block")
+
+
 def pmc_pass(workload: str = "decode", rounds: int = 8, copy_mib: int = 256):
-    """Eager workload for hardware-counter runs: `rounds` passes of the
-    decode step over the layer banks (or `rounds` 2048-token FP8 prefill layer
-    calls with per-token activation scales, or `rounds` 512-token asymmetric
-    W4A16 prefill calls), then a plain fp32 copy of
+    """Eager workload for hardware-counter runs, then a plain fp32 copy of
     `copy_mib` MiB (read once, written once) whose counter readings calibrate
-    the bytes-per-count of the HBM counters."""
+    the bytes-per-count of the HBM counters.  Workloads (each `rounds` times):
+      decode        the 1-token decode step over the LAYERS layer banks;
+      prefill       a 2048-token FP8 prefill layer, per-token activation scales;
+      w4a16         a 512-token asymmetric W4A16 prefill layer;
+      decode_multi  the three-launch decode at 4, 8 and 16 tokens (one layer
+                    bank per token count, rotating over the banks);
+      packed        the 1-token decode layer of every packed format (modes 0-5),
+                    router inside, LAYERS banks per mode;
+      block         the MoE block kernels around the routed experts at 1 token
+                    (block_pre / block_post, LAYERS layers)."""
     import torch
 
     from drama_moe.offload import HipExpertBackend
 
     device = torch.device("cuda", 0)
-    if workload == "w4a16":
+    calls = rounds
+    if workload == "decode_multi":
+        banks = [make_layer_bank(layer, device) for layer in range(LAYERS)]
+        backend = HipExpertBackend()
+        for tokens in (4, 8, 16):
+            xs, logits, outs = decode_inputs(tokens, device, SEED + tokens)
+            for _ in range(rounds):
+                for i in range(LAYERS):
+                    backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
+        calls = 3 * rounds * LAYERS
+    elif workload == "packed":
+        from drama_moe.formats import random_quantized_bank
+        from drama_moe.quantized import QuantizedExpertBackend
+
+        g = torch.Generator(device=device).manual_seed(SEED + 5)
+        xs, logits, outs = decode_inputs(1, device, SEED)
+        layers = 4  # 4 banks x 6 formats stay within HBM comfortably; rotation defeats the MALL
+        for mode in range(6):
+            banks = [random_quantized_bank(mode, EXPERTS, HIDDEN, INTER, asymmetric=mode == 0, device=device,
+                                           generator=g) for _ in range(layers)]
+            backend = QuantizedExpertBackend(mode)
+            for _ in range(rounds):
+                for i in range(LAYERS):
+                    backend.forward_routed(xs[i], logits[i], TOP_K, banks[i % layers], out=outs[i])
+            del banks
+            torch.cuda.synchronize()
+        calls = 6 * rounds * LAYERS
+    elif workload == "block":
+        from drama_moe import block
+
+        g = torch.Generator(device=device).manual_seed(SEED + 77)
+
+        def w(*shape):
+            return (torch.randn(*shape, device=device, generator=g) * 0.02).bfloat16()
+
+        blocks = [block.MoeBlock(w(EXPERTS, HIDDEN), w(1, HIDDEN), w(SHARED_INTER, HIDDEN), w(SHARED_INTER, HIDDEN),
+                                 w(HIDDEN, SHARED_INTER), None, None, top_k=TOP_K) for _ in range(LAYERS)]
+        xs = torch.randn(LAYERS, 1, HIDDEN, device=device, generator=g).bfloat16()
+        after = torch.randn(LAYERS, 1, HIDDEN, device=device, generator=g).bfloat16()
+        experts_out = torch.randn(LAYERS, 1, HIDDEN, device=device, generator=g).bfloat16()
+        outs = torch.empty_like(xs)
+        for _ in range(rounds):
+            for i in range(LAYERS):
+                logits, sgate, act = blocks[i].pre(xs[i])
+                blocks[i].post(act, sgate, experts_out[i], after[i], out=outs[i])
+        calls = rounds * LAYERS
+    elif workload == "w4a16":
         from drama_moe import router
         from drama_moe.formats import random_quantized_bank
         from drama_moe.quantized import QuantizedExpertBackend
@@ -235,9 +290,48 @@ def pmc_pass(workload: str = "decode", rounds: int = 8, copy_mib: int = 256):
     for _ in range(4):
         torch.mul(src, 1.0, out=dst)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_pass": {"workload": workload, "calls": rounds * (LAYERS if workload == "decode" else 1),
+    if workload == "decode":
+        calls = rounds * LAYERS
+    print(json.dumps({"pmc_pass": {"workload": workload, "calls": calls,
                                    "copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}}),
           flush=True)
+
+
+def stream_sweep(total_mib: int = 2048, reps: int = 20):
+    """Plain streaming-read bandwidth of the device by size: for each size S,
+    ceil(total / S) distinct fp32 buffers of S bytes (so the rotation exceeds
+    the 256 MB Infinity Cache), each read once per round by a sum reduction
+    (torch.sum: a read-only pass with a few bytes written); GB/s from HIP
+    events over `reps` rounds.  The attainable fraction of the 8 TB/s peak
+    for a single pass of a given size."""
+    import math
+
+    import torch
+
+    device = torch.device("cuda", 0)
+    rows = []
+    for mb in (4, 8, 16, 32, 38, 64, 128, 256, 512):
+        n = mb * (1 << 20) // 4
+        count = max(2, math.ceil(total_mib / mb))
+        bufs = [torch.ones(n, device=device) for _ in range(count)]
+        out = torch.empty(count, device=device)
+        for i, b in enumerate(bufs):
+            torch.sum(b, out=out[i])
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            for i, b in enumerate(bufs):
+                torch.sum(b, out=out[i])
+        stop.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(stop) * 1e3 / (reps * count)
+        gbs = n * 4 / (us * 1e-6) / 1e9
+        rows.append({"mib": mb, "buffers": count, "us_per_read": round(us, 2), "gbs": round(gbs, 1),
+                     "frac_of_8tbs": round(gbs / HBM_PEAK_GBS, 4)})
+        del bufs, out
+        torch.cuda.empty_cache()
+    print(json.dumps({"stream_sweep": rows}), flush=True)
 
 
 PREFILL_TOKENS = 2048
@@ -635,9 +729,10 @@ def main():
     parser.add_argument("--no-prefill", action="store_true")
     parser.add_argument("--no-quant", action="store_true")
     parser.add_argument("--no-block", action="store_true")
-    parser.add_argument("--pmc-pass", nargs="?", const="decode", choices=("decode", "prefill", "w4a16"),
-                        help="run the eager counter-collection workload (decode, 2048-token FP8 prefill or "
-                             "512-token W4A16 prefill) instead of the benchmark")
+    parser.add_argument("--pmc-pass", nargs="?", const="decode", choices=PMC_WORKLOADS,
+                        help="run an eager counter-collection workload (see pmc_pass) instead of the benchmark")
+    parser.add_argument("--stream-sweep", action="store_true",
+                        help="measure the plain streaming-read bandwidth by size instead of the benchmark")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path is built and "
@@ -648,6 +743,9 @@ def main():
         sys.exit(2)
     if args.pmc_pass:
         pmc_pass(args.pmc_pass)
+        return
+    if args.stream_sweep:
+        stream_sweep()
         return
     steps = max(1, args.steps)
     gpu = run_gpu(steps, args.warmup)

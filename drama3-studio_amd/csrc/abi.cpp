@@ -270,12 +270,55 @@ void check_output(const BankGeom& g, void* out, int out_dtype, int64_t out_row_s
     require(top_k >= 1 && pairs % top_k == 0, "pairs must be tokens * top_k");
 }
 
+// Single-launch decodes on one device never run at the same time: each
+// persistent launch waits on its own workgroups, so two of them sharing the
+// CUs could each hold part of the device while waiting for workgroups the
+// other one keeps out (until the spin bound gives up).  A launch on a stream
+// other than the previous launch's therefore waits for that launch (an event
+// per device); the Python layer orders its calls the same way through the
+// shared workspace.  Under graph capture nothing is recorded or waited for:
+// the order of graph replays is the caller's.
+struct FusedOrder {
+    hipEvent_t done = nullptr;
+    hipStream_t stream = nullptr;
+    bool launched = false;
+};
+
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+template <class Launch>
+bool ordered_fused_launch(hipStream_t stream, Launch&& launch) {
+    if (capturing(stream)) return launch();
+    static std::mutex mu;
+    static std::map<int, FusedOrder> by_device;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) throw std::runtime_error("hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(mu);
+    FusedOrder& o = by_device[dev];
+    if (o.done == nullptr && hipEventCreateWithFlags(&o.done, hipEventDisableTiming) != hipSuccess) {
+        o.done = nullptr;
+        throw std::runtime_error("could not create the single-launch decode's ordering event");
+    }
+    if (o.launched && o.stream != stream && hipStreamWaitEvent(stream, o.done, 0) != hipSuccess)
+        throw std::runtime_error("could not order the single-launch decode after the previous one");
+    if (!launch()) return false;
+    if (hipEventRecord(o.done, stream) != hipSuccess) throw std::runtime_error("hipEventRecord failed");
+    o.stream = stream;
+    o.launched = true;
+    return true;
+}
+
 // Single-launch decode of a small call (fp8_fused.hip); false when the call
-// does not fit it (nothing enqueued).
+// does not fit it (nothing enqueued).  `order_streams` = false (the
+// no-allocation entry point, whose callers order overlapping calls
+// themselves) skips the cross-stream ordering and its event.
 bool fp8_fused_call(const BankGeom& g, const Activations& a, const dmoe::RouteSource& route, const void* weights,
                     int weights_dtype, int pairs, int top_k, int gu_dtype, void* out, int out_dtype,
                     int64_t out_row_stride, float* out_pairs, const Fp8Workspace& ws, int* status,
-                    hipStream_t stream) {
+                    hipStream_t stream, bool order_streams) {
     const int rows = (pairs - 1) / a.row_div + 1;
     const int route_k = route.logits ? route.top_k : top_k;
     const int x_esize = a.xq ? 0 : a.x_dtype == DMOE_F32 ? 4 : 2;
@@ -310,7 +353,8 @@ bool fp8_fused_call(const BankGeom& g, const Activations& a, const dmoe::RouteSo
     fa.status = status;
     fa.spin_ticks = g_spin_ticks.load(std::memory_order_relaxed);
     fa.tag_skew = g_force_timeout.load(std::memory_order_relaxed) ? 1u : 0u;
-    return dmoe::launch_fp8_fused_decode(fa, stream);
+    if (!order_streams) return dmoe::launch_fp8_fused_decode(fa, stream);
+    return ordered_fused_launch(stream, [&] { return dmoe::launch_fp8_fused_decode(fa, stream); });
 }
 
 // A whole decode FP8 call (<= 256 pairs): one fused launch when it fits,
@@ -318,10 +362,10 @@ bool fp8_fused_call(const BankGeom& g, const Activations& a, const dmoe::RouteSo
 void fp8_decode_call(const BankGeom& g, Activations a, const dmoe::RouteSource& route, const void* weights,
                  int weights_dtype, int pairs, int top_k, int gu_dtype, void* out, int out_dtype,
                  int64_t out_row_stride, float* out_pairs, void* workspace, size_t workspace_bytes, int* status,
-                 hipStream_t stream) {
+                 hipStream_t stream, bool order_streams = true) {
     const Fp8Workspace ws = take_workspace(g, pairs, workspace, workspace_bytes);
     if (fp8_fused_wanted(pairs) && fp8_fused_call(g, a, route, weights, weights_dtype, pairs, top_k, gu_dtype, out,
-                                          out_dtype, out_row_stride, out_pairs, ws, status, stream))
+                                          out_dtype, out_row_stride, out_pairs, ws, status, stream, order_streams))
         return;
     const bool in_down = down_quantizes(g, pairs);
     launch_prep(g, a, route, pairs, ws, status, stream);
@@ -1004,7 +1048,8 @@ int dmoe_fp8_moe_layer_noalloc(const DmoeFp8Bank* bank, const void* x, int x_dty
         require(need <= kStaticScratchBytes, "call needs more scratch than the 8 MiB static scratch holds");
         void* ws = static_scratch();
         fp8_decode_call(c.g, c.a, c.route, weights_out, weights_dtype, c.pairs, top_k, gu_dtype, out, out_dtype,
-                        out_row_stride, nullptr, ws, kStaticScratchBytes, status, as_stream(stream));
+                        out_row_stride, nullptr, ws, kStaticScratchBytes, status, as_stream(stream),
+                        /*order_streams=*/false);
     });
 }
 

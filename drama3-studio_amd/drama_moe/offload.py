@@ -304,6 +304,22 @@ def check_id_range(ids: Tensor, experts: int) -> None:
         raise ValueError(f"Expert IDs must be in [0, {experts})")
 
 
+def raise_device_status(device: torch.device) -> None:
+    """Read (and clear) the device status word of the expert kernels at a
+    host sync the caller already has; raise if an earlier call's outputs are
+    invalid (a single-launch decode whose hand-off wait gave up) or it met
+    expert ids outside the bank."""
+    state = device_state(device)
+    value = int(state.status.item())
+    if not value & (_lib.STATUS_SYNC_TIMEOUT | _lib.STATUS_BAD_EXPERT_ID):
+        return
+    state.status.zero_()
+    if value & _lib.STATUS_SYNC_TIMEOUT:
+        raise RuntimeError("an earlier expert call's single-launch decode gave up its hand-off wait (other work "
+                           f"held the device's CUs); its outputs are invalid (device status {value:#x})")
+    raise ValueError(f"an earlier expert call met expert ids outside the bank (device status {value:#x})")
+
+
 class _RoutedForward:
     """Forward of an attached expert module: hands ``(x, topk_ids,
     topk_weights)`` to the manager.  ``shadowed`` is the instance-level forward
@@ -338,10 +354,16 @@ class ResidentExpertManager:
     packed banks bound by a quantized loader on a QuantizedExpertBackend of
     their mode.  ``validate_ids=True`` keeps the reference's eager range check
     of the ids (one host sync per call); ``False`` leaves bad ids to the
-    device status word so calls can be captured in hipGraphs.
+    device status word so calls can be captured in hipGraphs.  At that host
+    sync, ``raise_on_status=True`` (default) also reads the device status
+    word and raises if an earlier call's single-launch decode gave up its
+    hand-off wait (outputs invalid) or met ids outside the bank; with
+    ``validate_ids=False`` there is no sync and the caller reads
+    ``backend.status()`` where it has one.
     """
 
-    def __init__(self, *, backend=None, validate_ids: bool = True, residency: str = "hbm", **staging) -> None:
+    def __init__(self, *, backend=None, validate_ids: bool = True, residency: str = "hbm",
+                 raise_on_status: bool = True, **staging) -> None:
         from .staging import RESIDENCY_MODES, HostResidency, check_staging_sizes
 
         if residency not in RESIDENCY_MODES:
@@ -358,6 +380,7 @@ class ResidentExpertManager:
                        sizes.get("cache_experts", 0), sizes.get("hot_cache_experts"))
         self.backend = backend if backend is not None else HipExpertBackend()
         self.validate_ids = validate_ids
+        self.raise_on_status = raise_on_status
         self.residency = residency
         # host mode: the staging tier; hbm mode: the sizes are checked and unused
         self.host = HostResidency(pin_memory=staging.get("pin_memory", True), **sizes) if residency == "host" else None
@@ -415,6 +438,8 @@ class ResidentExpertManager:
             return self.host.forward(id(module), bank, backend, x, topk_ids, topk_weights)
         if self.validate_ids:
             check_id_range(topk_ids, bank.count)
+            if self.raise_on_status:
+                raise_device_status(_device_of(x))
         return backend.forward(x, topk_ids, topk_weights, self._on_device(module, bank, x.device))
 
     def _on_device(self, module: nn.Module, bank, device: torch.device):

@@ -254,3 +254,89 @@ def test_decode_after_prefill_on_one_workspace(cuda, decode_mode):
     fused, staged_out = both(decode_mode, run)
     assert torch.equal(fused, staged_out)
     assert backend.status(cuda) == 0
+
+
+def test_single_launch_decodes_on_two_streams_with_own_workspaces(cuda):
+    """Direct C-ABI callers with a workspace each issue single-launch decodes
+    on two streams back to back, without ordering them: the library orders
+    the persistent launches itself (each waits for the previous one on
+    another stream), so none waits for workgroups the other keeps out --
+    every call is exact and no status bit is raised, where two concurrent
+    launches could only end in the hand-off bound."""
+    import ctypes
+
+    from drama_moe.formats import fp8_bank_struct
+
+    print_case("fused decodes on two streams")
+    lib = _lib.library()
+    g = torch.Generator().manual_seed(404)
+    staged = to_device(random_fp8_bank(128, 2048, 768, layout="channel", generator=g), cuda)
+    bank = fp8_bank_struct(staged)
+    size = lib.dmoe_fp8_workspace_bytes(ctypes.byref(bank), 8)
+    workspaces = [torch.zeros(size, dtype=torch.uint8, device=cuda) for _ in range(2)]
+    status = torch.zeros(1, dtype=torch.int32, device=cuda)
+    calls = 12
+    xs = torch.randn(calls, 1, 2048, generator=g).bfloat16().to(cuda)
+    logits = torch.randn(calls, 1, 128, generator=g).to(cuda)
+    outs = torch.empty_like(xs)
+    ids = torch.empty(calls, 1, 8, dtype=torch.int64, device=cuda)
+    weights = torch.empty(calls, 1, 8, dtype=torch.bfloat16, device=cuda)
+
+    def layer(i, stream, ws):
+        _lib.check(lib.dmoe_fp8_moe_layer(
+            ctypes.byref(bank), _lib.ptr(xs[i]), _lib.BF16, 2048, 1, _lib.ptr(logits[i]), 128, 8, 1,
+            _lib.ptr(ids[i]), _lib.ptr(weights[i]), _lib.BF16, 128, _lib.BF16, _lib.ptr(outs[i]), _lib.BF16, 2048,
+            _lib.ptr(ws), ws.numel(), _lib.ptr(status), ctypes.c_void_p(stream.cuda_stream)))
+
+    streams = [torch.cuda.Stream(cuda), torch.cuda.Stream(cuda)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(cuda))
+    for i in range(calls):
+        layer(i, streams[i % 2], workspaces[i % 2])
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    backend = HipExpertBackend()
+    for i in range(calls):
+        want, _, _ = backend.forward_routed(xs[i], logits[i], 8, staged)
+        assert torch.equal(outs[i], want), i
+
+
+def test_manager_reports_a_given_up_hand_off_at_its_sync(cuda):
+    """ResidentExpertManager(validate_ids=True) reads the device status word
+    at the host sync it already has: after a call whose hand-off wait gave
+    up (forced from the host with a 100 us bound), the next call raises
+    instead of returning with the earlier output silently invalid."""
+    from drama_moe.offload import ResidentExpertManager
+
+    print_case("manager status surfacing")
+
+    class Experts(torch.nn.Module):
+        fp8 = True
+
+        def __init__(self, bank):
+            super().__init__()
+            for name, tensor in bank.buffers().items():
+                self.register_buffer(name, tensor)
+
+    lib = _lib.library()
+    g = torch.Generator().manual_seed(505)
+    module = Experts(to_device(random_fp8_bank(16, 512, 256, layout="channel", generator=g), cuda))
+    manager = ResidentExpertManager(backend=HipExpertBackend())
+    manager.attach("0", module)
+    x = torch.randn(1, 512, generator=g).bfloat16().to(cuda)
+    ids = torch.tensor([[3, 1, 7, 2, 6, 0, 4, 5]], device=cuda)
+    w = torch.full((1, 8), 0.125, dtype=torch.bfloat16, device=cuda)
+    try:
+        good = module(x, ids, w)
+        previous = lib.dmoe_set_sync_spin_limit(10_000)
+        forced = lib.dmoe_debug_force_sync_timeout(1)
+        try:
+            module(x, ids, w)
+        finally:
+            lib.dmoe_debug_force_sync_timeout(forced)
+            lib.dmoe_set_sync_spin_limit(previous)
+        with pytest.raises(RuntimeError, match="gave up its hand-off wait"):
+            module(x, ids, w)
+        assert torch.equal(module(x, ids, w), good)  # the status was cleared; the next call is exact
+    finally:
+        manager.close()
