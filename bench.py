@@ -316,13 +316,13 @@ def stream_sweep(total_mib: int = 2048, reps: int = 20):
         bufs = [torch.ones(n, device=device) for _ in range(count)]
         out = torch.empty(count, device=device)
         for i, b in enumerate(bufs):
-            torch.sum(b, out=out[i])
+            torch.sum(b, dim=0, out=out[i])
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(reps):
             for i, b in enumerate(bufs):
-                torch.sum(b, out=out[i])
+                torch.sum(b, dim=0, out=out[i])
         stop.record()
         torch.cuda.synchronize()
         us = start.elapsed_time(stop) * 1e3 / (reps * count)
