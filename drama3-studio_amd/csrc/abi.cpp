@@ -760,6 +760,15 @@ int dmoe_silu_table(float* table, void* stream) {
     });
 }
 
+int dmoe_stream_read(const void* data, int64_t bytes, uint32_t* sink, void* stream) {
+    return checked([&] {
+        require(data != nullptr && sink != nullptr && reinterpret_cast<uintptr_t>(data) % 16 == 0,
+                "stream read: a 16-byte aligned buffer and a sink word are required");
+        require(bytes >= 16 && bytes % 16 == 0, "stream read: bytes must be a positive multiple of 16");
+        dmoe::launch_stream_read(data, bytes, sink, as_stream(stream));
+    });
+}
+
 int dmoe_combine_slots(const float* partials, int64_t partial_row_stride, const void* ids, int ids_dtype, int experts,
                        int tokens, int top_k, int hidden, void* out, int out_dtype, int64_t out_row_stride,
                        void* stream) {

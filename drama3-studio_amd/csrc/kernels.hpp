@@ -245,6 +245,10 @@ void launch_fp8_down_decode(const DownArgs& a, hipStream_t stream);
 void launch_fp8_quantize(const QuantArgs& a, hipStream_t stream);
 void launch_fp8_decode(const uint8_t* v, float* out, int64_t n, hipStream_t stream);
 void launch_silu_table(float* table, hipStream_t stream);
+
+// Streaming-read probe (measurement only).
+int stream_read_blocks(int64_t bytes);
+void launch_stream_read(const void* data, int64_t bytes, uint32_t* sink, hipStream_t stream);
 void launch_route_topk(const RouteArgs& a, hipStream_t stream);
 void launch_route_quantize(const RouteArgs& r, const QuantArgs& q, hipStream_t stream);
 void launch_permute(const PermuteArgs& a, hipStream_t stream);

@@ -520,6 +520,16 @@ DMOE_API int dmoe_cpu_partition_routes(const int64_t* ids, int count, const int6
  * (src/drama_low_vram/fp8_decode.py:17-21). */
 DMOE_API int dmoe_silu_table(float* table, void* stream);
 
+/* ---------------------------------------------------------- measurement
+ *
+ * No counterpart in the reference: a streaming read of `bytes` (a multiple
+ * of 16, 16-byte aligned) of device memory, each 16-byte word loaded once,
+ * for pricing one pass over a given number of bytes on this GPU (the figure
+ * the expert kernels' single passes over their weight rows are set against).
+ * `sink` is one device word, written only if the buffer's words XOR to a
+ * fixed unlikely value. */
+DMOE_API int dmoe_stream_read(const void* data, int64_t bytes, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

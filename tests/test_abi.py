@@ -110,3 +110,12 @@ def test_route_and_permute_validate_geometry():
     assert lib.dmoe_permute(_fake(), _lib.I64, 20000, 128, _fake(), _fake(), _fake(), _fake(), need - 4,
                             None, None) == -1
     assert "workspace too small" in lib.dmoe_last_error().decode()
+
+
+def test_stream_read_validates_before_launch():
+    lib = _lib.library()
+    assert lib.dmoe_stream_read(_fake(), 100, _fake(), None) == -1
+    assert "multiple of 16" in lib.dmoe_last_error().decode()
+    assert lib.dmoe_stream_read(_fake(0x100008), 1024, _fake(), None) == -1
+    assert "aligned" in lib.dmoe_last_error().decode()
+    assert lib.dmoe_stream_read(_fake(), 1024, None, None) == -1
