@@ -25,6 +25,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -297,40 +298,49 @@ def pmc_pass(workload: str = "decode", rounds: int = 8, copy_mib: int = 256):
           flush=True)
 
 
-def stream_sweep(total_mib: int = 2048, reps: int = 20):
-    """Plain streaming-read bandwidth of the device by size: for each size S,
-    ceil(total / S) distinct fp32 buffers of S bytes (so the rotation exceeds
-    the 256 MB Infinity Cache), each read once per round by a sum reduction
-    (torch.sum: a read-only pass with a few bytes written); GB/s from HIP
-    events over `reps` rounds.  The attainable fraction of the 8 TB/s peak
-    for a single pass of a given size."""
+# MiB one 1-token decode call reads: 8 experts x 3 x 768 x 2048 FP8 bytes plus
+# their per-channel scales (37.86 MB).
+DECODE_MB = 36.1
+
+
+def stream_sweep(total_mib: int = 2048, replays: int = 10):
+    """Plain streaming-read rate of the device by size: for each size S,
+    ceil(total / S) distinct buffers of S bytes (so the rotation exceeds the
+    256 MB Infinity Cache), each read once per round by the library's read
+    probe (dmoe_stream_read: 16-byte non-temporal loads, four per lane in
+    flight, up to 8 workgroups of 512 per CU), one launch per buffer replayed
+    from a hipGraph as the decode steps are; microseconds per launch from HIP
+    events.  The attainable fraction of the 8 TB/s peak for one pass of a
+    given size, to set the single-launch decode (DECODE_MB per call) against."""
     import math
 
     import torch
 
+    from drama_moe import _lib
+
+    lib = _lib.library()
     device = torch.device("cuda", 0)
+    stream = torch.cuda.Stream(device)
+    sink = torch.zeros(1, dtype=torch.int32, device=device)
     rows = []
-    for mb in (4, 8, 16, 32, 38, 64, 128, 256, 512):
-        n = mb * (1 << 20) // 4
+    for mb in (4, 8, 16, 24, 32, DECODE_MB, 48, 64, 128, 256, 512):
+        nbytes = int(mb * (1 << 20)) // 16 * 16
         count = max(2, math.ceil(total_mib / mb))
-        bufs = [torch.ones(n, device=device) for _ in range(count)]
-        out = torch.empty(count, device=device)
-        for i, b in enumerate(bufs):
-            torch.sum(b, dim=0, out=out[i])
-        torch.cuda.synchronize()
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            for i, b in enumerate(bufs):
-                torch.sum(b, dim=0, out=out[i])
-        stop.record()
-        torch.cuda.synchronize()
-        us = start.elapsed_time(stop) * 1e3 / (reps * count)
-        gbs = n * 4 / (us * 1e-6) / 1e9
-        rows.append({"mib": mb, "buffers": count, "us_per_read": round(us, 2), "gbs": round(gbs, 1),
-                     "frac_of_8tbs": round(gbs / HBM_PEAK_GBS, 4)})
-        del bufs, out
+        bufs = [torch.ones(nbytes // 4, device=device) for _ in range(count)]
+
+        def reads():
+            handle = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+            for b in bufs:
+                _lib.check(lib.dmoe_stream_read(_lib.ptr(b), nbytes, _lib.ptr(sink), handle))
+
+        us = _graph_time_us(reads, count, replays, stream)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"mib": mb, "buffers": count, "workgroups": min(2048, -(-nbytes // (512 * 4 * 16))),
+                     "us_per_read": round(us, 2), "gbs": round(gbs, 1), "frac_of_8tbs": round(gbs / HBM_PEAK_GBS, 4)})
+        del bufs
         torch.cuda.empty_cache()
+    if int(sink.item()) != 0:
+        raise RuntimeError("stream read probe wrote its sink")
     print(json.dumps({"stream_sweep": rows}), flush=True)
 
 
@@ -395,6 +405,89 @@ def run_prefill(reps: int = 10):
                    "mfma_frac_is": "algorithmic flops / measured time / FP8 dense peak",
                    "mfma_busy_counters": prefill_mfma_busy()})
     return result
+
+
+def run_hybrid(calls: int = 128, threads: int = 8, layers: int = 2):
+    """Cooperative decode: the lowest-ranked route slots of a 1-token FP8
+    layer call on the host cores (the library's executor, `threads` workers),
+    the others on the GPU, merged in slot order.  `layers` of the bench's
+    banks attached from host memory; eager calls (the mode waits on the host
+    for its partials), seeded inputs rotating over 16 tokens; wall-clock
+    microseconds per layer call for 1, 2 and 4 host slots, beside the same
+    calls on the GPU alone (eager, one host sync per call) and the executor
+    alone on all 8 slots of a call."""
+    import torch
+
+    from drama_moe import fp8_moe, router
+    from drama_moe.formats import EXPERT_BUFFER_NAMES, StagedExperts
+    from drama_moe.hybrid import CpuExpertExecutor, silu_table
+    from drama_moe.offload import HipExpertBackend, ResidentExpertManager
+
+    device = torch.device("cuda", 0)
+
+    class Experts(torch.nn.Module):
+        fp8 = True
+
+        def __init__(self, bank):
+            super().__init__()
+            for name in EXPERT_BUFFER_NAMES:
+                self.register_buffer(name, getattr(bank, name))
+
+    manager = ResidentExpertManager(backend=HipExpertBackend())
+    modules = []
+    for layer in range(layers):
+        bank = make_layer_bank(layer, device)
+        host = StagedExperts(*(getattr(bank, n).cpu() for n in EXPERT_BUFFER_NAMES))
+        del bank
+        module = Experts(host)
+        manager.attach(str(layer), module)
+        modules.append(module)
+    g = torch.Generator(device=device).manual_seed(SEED + 91)
+    xs = torch.randn(16, 1, HIDDEN, device=device, generator=g).bfloat16()
+    routes = [router.route_topk(torch.randn(1, EXPERTS, device=device, generator=g), TOP_K)[::-1] for _ in range(16)]  # (ids, weights)
+
+    def timed(n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(n):
+            ids, w = routes[i % 16]
+            modules[i % layers](xs[i % 16], ids, w)
+            torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e6 / n
+
+    try:
+        timed(16)  # device copies of the banks, first launches
+        result = {"gpu_only_us": round(timed(calls), 1)}
+        for jobs in (1, 2, 4):
+            hybrid = manager.configure_hybrid_decode(jobs, threads=threads)
+            with hybrid.decode():
+                timed(8)
+                us = timed(calls)
+            stats = hybrid.report()
+            result[f"cpu_jobs_{jobs}_us"] = round(us, 1)
+            result[f"cpu_jobs_{jobs}_recomputed_pairs"] = stats["boundary_recomputed_pairs"]
+        executor = CpuExpertExecutor(manager._bank_of(modules[0]), capacity=8, threads=threads,
+                                     silu_table=silu_table(device))
+        result["executor_isa"] = executor.implementation
+        q, s = fp8_moe.quantize_groups(fp8_moe.quant_kernel, xs[0], HIDDEN)
+        qh = q.view(torch.uint8).cpu().reshape(-1).contiguous()
+        sh = s.cpu().reshape(-1).contiguous()
+        ids, w = routes[0]
+        ids_h, w_h = ids.cpu().reshape(-1), w.float().cpu().reshape(-1)
+        store = manager._bank_of(modules[0])
+        for _ in range(4):
+            executor.forward_quantized_pairs(qh, sh, ids_h, w_h, store=store)
+        t0 = time.perf_counter()
+        reps = 32
+        for _ in range(reps):
+            executor.forward_quantized_pairs(qh, sh, ids_h, w_h, store=store)
+        result["executor_8_slots_us"] = round((time.perf_counter() - t0) * 1e6 / reps, 1)
+        executor.close()
+        result.update({"threads": threads, "layers": layers, "calls": calls, "guard": True,
+                       "timing": "wall clock per eager layer call"})
+        return result
+    finally:
+        manager.close()
 
 
 SHARED_INTER = 768  # the shared expert's intermediate size in the block leg
@@ -729,6 +822,7 @@ def main():
     parser.add_argument("--no-prefill", action="store_true")
     parser.add_argument("--no-quant", action="store_true")
     parser.add_argument("--no-block", action="store_true")
+    parser.add_argument("--no-hybrid", action="store_true")
     parser.add_argument("--pmc-pass", nargs="?", const="decode", choices=PMC_WORKLOADS,
                         help="run an eager counter-collection workload (see pmc_pass) instead of the benchmark")
     parser.add_argument("--stream-sweep", action="store_true",
@@ -756,6 +850,8 @@ def main():
     log("prefill", json.dumps(prefill))
     quant = None if args.no_quant else run_quant()
     log("quant", json.dumps(quant))
+    hybrid = None if args.no_hybrid else run_hybrid()
+    log("hybrid", json.dumps(hybrid))
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log("cpu", json.dumps(cpu))
@@ -791,6 +887,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill_fp8": prefill,
         "packed_banks": quant,
+        "cooperative_decode": hybrid,
     }
     print(json.dumps(line), flush=True)
 

@@ -4,8 +4,8 @@ executor behind dmoe_cpu_expert_pairs and the route planner.
 The executor follows the FP8 decode kernels' arithmetic step for step, so it
 is checked three ways here: its scalar, AVX2 and AVX-512 block products give
 the same bits; it equals, bit for bit, an independent numpy statement of that
-arithmetic (exact block products rounded once, glibc's correctly rounded
-fmaf for the block chains, the 8-wave K split of gate/up, bf16 gate/up, SiLU
+arithmetic (fp32 block products in the fixed lane order, glibc's correctly
+rounded fmaf for the block chains, the 8-wave K split of gate/up, bf16 gate/up, SiLU
 by table, E4M3 hidden groups through torch's float8 conversion); and it is
 within the path's 2e-2 bar of the oracle (the reference contract, which
 chains gate/up blocks in one sequence).  The guard's known answer: a hidden
@@ -73,8 +73,14 @@ def emulate(store: StagedExperts, xq: np.ndarray, xs: np.ndarray, ids, weights, 
     KB, KBd = H // 128, I // 128
     out = np.empty((len(ids), H), np.float32)
 
-    def dot(w, x):  # exact sum of exact products, rounded once
-        return np.float32(np.sum(w.astype(np.float64) * x))
+    def dot(w, x):  # fp32 lane l sums the (exact) products k = l, l + 16, ...; the lanes fold in halves
+        products = (w.astype(np.float32) * x.astype(np.float32)).reshape(8, 16)
+        lanes = np.zeros(16, np.float32)
+        for step in products:
+            lanes = (lanes + step).astype(np.float32)
+        for width in (8, 4, 2, 1):
+            lanes[:width] = lanes[:width] + lanes[width:2 * width]
+        return np.float32(lanes[0])
 
     for j, (e, wt) in enumerate(zip(ids, weights)):
         h = np.empty(I, np.float32)

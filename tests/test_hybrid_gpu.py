@@ -4,8 +4,8 @@ src/drama_low_vram/hybrid_decode.py:33-416, and its tests
 tests/test_hybrid_decode.py).
 
 Bars: the GPU slots are the resident path's own partials, bit for bit; the
-host slots follow the decode kernels' arithmetic with exactly rounded block
-products (the device's FP8 MFMA truncates inside groups of 8 products), so
+host slots follow the decode kernels' arithmetic with fp32 block products
+in a fixed lane order (the device's FP8 MFMA truncates inside groups of 8 products), so
 they and the layer output are within 2e-2 of the all-GPU resident call and
 of the oracle.  A call is deterministic: repeats, other streams and
 asynchronous returns give the same bits.  The boundary guard's GPU
