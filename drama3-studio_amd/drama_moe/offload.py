@@ -364,7 +364,7 @@ class ResidentExpertManager:
 
     def __init__(self, *, backend=None, validate_ids: bool = True, residency: str = "hbm",
                  raise_on_status: bool = True, **staging) -> None:
-        from .staging import RESIDENCY_MODES, HostResidency, check_staging_sizes
+        from .staging import RESIDENCY_MODES, HostResidency, OffloadStatistics, check_staging_sizes
 
         if residency not in RESIDENCY_MODES:
             raise ValueError(f"residency must be one of {RESIDENCY_MODES}, got {residency!r}")
@@ -383,7 +383,10 @@ class ResidentExpertManager:
         self.raise_on_status = raise_on_status
         self.residency = residency
         # host mode: the staging tier; hbm mode: the sizes are checked and unused
-        self.host = HostResidency(pin_memory=staging.get("pin_memory", True), **sizes) if residency == "host" else None
+        self.statistics = OffloadStatistics()
+        self.host = HostResidency(pin_memory=staging.get("pin_memory", True),
+                                  profile_transfers=staging.get("profile_transfers", False),
+                                  statistics=self.statistics, **sizes) if residency == "host" else None
         self.modules: dict[str, nn.Module] = {}
         self.forward_calls = 0
         self._banks: dict[int, tuple] = {}
@@ -391,6 +394,15 @@ class ResidentExpertManager:
         self._packed_backends: dict[int, object] = {}
         self.hybrid_decode = None
         self._closed = False
+
+    @property
+    def stats(self):
+        """Cumulative OffloadStatistics of this manager's host traffic (the
+        reference's ``manager.stats``); reading it collects the event times
+        of transfers profiled so far."""
+        if self.host is not None:
+            return self.host.collect()
+        return self.statistics
 
     def _require_open(self) -> None:
         if self._closed:
@@ -432,6 +444,8 @@ class ResidentExpertManager:
         if x.shape[0] == 0:
             return torch.zeros_like(x)
         backend = self._backend_for(bank)
+        if self.host is None:
+            self.statistics.forward_calls += 1  # the host tier counts its own calls
         if self.hybrid_decode is not None and self.hybrid_decode.eligible(module, x, topk_ids):
             return self.hybrid_decode.forward(module, bank, x, topk_ids, topk_weights)
         if self.host is not None:
@@ -446,7 +460,7 @@ class ResidentExpertManager:
         """The bank itself when it lives on ``device``, else its whole copy
         there, made on the module's first call and kept while the module
         holds the same buffers."""
-        from .staging import bank_device, bank_key, device_copy
+        from .staging import bank_buffers, bank_device, bank_key, device_copy
 
         if bank_device(bank) == device:
             return bank
@@ -455,6 +469,9 @@ class ResidentExpertManager:
         if cached is None or cached[0] != key:
             cached = (key, device_copy(bank, device))
             self._device_banks[id(module)] = cached
+            copied = bank_buffers(bank).values()
+            self.statistics.h2d_copy_calls += len(copied)
+            self.statistics.h2d_bytes += sum(t.numel() * t.element_size() for t in copied)
         return cached[1]
 
     def configure_hybrid_decode(self, cpu_jobs: int = 0, *, threads: int = 4, device=None,
@@ -503,10 +520,11 @@ class ResidentExpertManager:
 # that configure its host staging tiers.  With residency="host" the sizes
 # and pin_memory configure the staging tier of drama_moe.staging; with every
 # expert resident (the default) they are checked and have nothing to
-# configure.  profile_transfers, combined_decode_bank and packed_staging are
-# accepted for call-site compatibility: banks are always staged packed, and a
-# decode token whose experts are split between the hot cache and the pool
-# runs as grouped pair calls.
+# configure.  profile_transfers times the host tier's copies with HIP events
+# (``manager.stats.h2d_seconds``).  combined_decode_bank and packed_staging
+# are accepted for call-site compatibility: banks are always staged packed,
+# and a decode token whose experts are split between the hot cache and the
+# pool runs as grouped pair calls.
 STAGING_KEYWORDS = frozenset({"max_staged_experts", "max_pair_rows", "cache_experts", "hot_cache_experts",
                               "pin_memory", "profile_transfers", "combined_decode_bank", "packed_staging"})
 

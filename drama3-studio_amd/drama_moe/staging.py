@@ -29,6 +29,7 @@ can be.
 from __future__ import annotations
 
 import dataclasses
+import time
 
 import torch
 from torch import Tensor
@@ -36,6 +37,71 @@ from torch import Tensor
 from .formats import EXPERT_BUFFER_NAMES, QuantizedStore, StagedExperts
 
 RESIDENCY_MODES = ("hbm", "host")
+
+
+@dataclasses.dataclass
+class OffloadStatistics:
+    """Cumulative counts and timings of a manager's host traffic: the
+    reference's OffloadStatistics (offload.py:59-98) for the fields this tier
+    has.  Host banks are pinned whole, once, and their rows copied straight
+    into device slots, so there is no gather step, staging area or DMA-source
+    wait to count.  ``h2d_seconds`` is HIP-event time of the copies, collected
+    only with ``profile_transfers``; the other timings are host wall time;
+    ``h2d_copy_calls`` counts tensor copy submissions."""
+
+    forward_calls: int = 0
+    grouped_calls: int = 0
+    staging_calls: int = 0
+    h2d_copy_calls: int = 0
+    expert_loads: int = 0
+    expert_cache_hits: int = 0
+    hot_cache_hits: int = 0
+    hot_cache_loads: int = 0
+    hot_cache_bytes: int = 0
+    hot_cache_capacity_experts: int = 0
+    staged_bytes: int = 0
+    h2d_bytes: int = 0
+    host_staging_seconds: float = 0.0
+    h2d_submit_seconds: float = 0.0
+    routing_host_seconds: float = 0.0
+    h2d_seconds: float = 0.0
+    pinned_bytes: int = 0
+    device_buffer_bytes: int = 0
+    peak_staged_experts: int = 0
+
+    def as_dict(self) -> dict:
+        return dataclasses.asdict(self)
+
+
+class TransferClock:
+    """HIP-event timing of host-to-device copies: a start and a stop event
+    around each batch on the copying stream, read when the statistics are
+    asked for (no host wait on the call path)."""
+
+    def __init__(self, stats: OffloadStatistics, enabled: bool):
+        self.stats = stats
+        self.enabled = bool(enabled)
+        self._pending: list = []
+
+    def start(self, device):
+        if not self.enabled or torch.device(device).type != "cuda":
+            return None
+        event = torch.cuda.Event(enable_timing=True)
+        event.record(torch.cuda.current_stream(device))
+        return event
+
+    def stop(self, started, device) -> None:
+        if started is None:
+            return
+        event = torch.cuda.Event(enable_timing=True)
+        event.record(torch.cuda.current_stream(device))
+        self._pending.append((started, event))
+
+    def collect(self) -> None:
+        for started, stopped in self._pending:
+            stopped.synchronize()
+            self.stats.h2d_seconds += started.elapsed_time(stopped) / 1000.0
+        self._pending.clear()
 
 
 def bank_buffers(bank) -> dict:
@@ -80,6 +146,8 @@ class ExpertSlots:
         self.clock = 0
         self.loads = 0
         self.hits = 0
+        self.copy_calls = 0
+        self.copied_bytes = 0
 
     @property
     def nbytes(self) -> int:
@@ -125,6 +193,8 @@ class ExpertSlots:
                     del self.slot_of[self.holds[slot]]
                 for name, source in sources.items():
                     self.buffers[name][slot].copy_(source[expert], non_blocking=True)
+                    self.copy_calls += 1
+                    self.copied_bytes += source[expert].numel() * source.element_size()
                 self.holds[slot] = expert
                 self.slot_of[expert] = slot
                 self.loads += 1
@@ -165,7 +235,8 @@ class HostResidency:
     """Runs calls on banks held in host memory through device slots."""
 
     def __init__(self, *, max_staged_experts: int = 8, max_pair_rows: int = 64, cache_experts: int = 0,
-                 hot_cache_experts: int | None = None, pin_memory: bool = True):
+                 hot_cache_experts: int | None = None, pin_memory: bool = True, profile_transfers: bool = False,
+                 statistics: OffloadStatistics | None = None):
         cache_experts = check_staging_sizes(max_staged_experts, max_pair_rows, cache_experts, hot_cache_experts)
         self.max_pair_rows = max_pair_rows
         self.cache_experts = cache_experts
@@ -175,12 +246,50 @@ class HostResidency:
         self._host: dict = {}
         self.calls = 0
         self.grouped_calls = 0
+        self.statistics = statistics if statistics is not None else OffloadStatistics()
+        self.clock = TransferClock(self.statistics, profile_transfers)
 
     def stats(self) -> dict:
         return {"calls": self.calls, "grouped_calls": self.grouped_calls, "pool_loads": self.pool.loads,
                 "pool_bytes": self.pool.nbytes, "cache_hits": sum(c.hits for c in self.caches.values()),
                 "cache_loads": sum(c.loads for c in self.caches.values()),
                 "cache_bytes": sum(c.nbytes for c in self.caches.values())}
+
+    def collect(self) -> OffloadStatistics:
+        """The cumulative statistics, with the profiled copies' event times
+        read and the device buffer sizes refreshed."""
+        self.clock.collect()
+        st = self.statistics
+        st.hot_cache_bytes = sum(c.nbytes for c in self.caches.values())
+        st.hot_cache_capacity_experts = self.cache_experts * len(self.caches)
+        st.device_buffer_bytes = self.pool.nbytes + st.hot_cache_bytes
+        return st
+
+    def _place(self, slots: "ExpertSlots", host, experts, keep: set, *, hot: bool, device) -> dict:
+        """slots.place with its copies counted (and timed when profiling)."""
+        st = self.statistics
+        began = time.perf_counter()
+        loads, hits, calls, nbytes = slots.loads, slots.hits, slots.copy_calls, slots.copied_bytes
+        started = self.clock.start(device)
+        placed = slots.place(host, experts, keep)
+        self.clock.stop(started, device)
+        loads, hits = slots.loads - loads, slots.hits - hits
+        calls, nbytes = slots.copy_calls - calls, slots.copied_bytes - nbytes
+        st.h2d_copy_calls += calls
+        st.h2d_bytes += nbytes
+        if hot:
+            st.hot_cache_loads += loads
+            st.hot_cache_hits += hits
+        else:
+            st.staging_calls += 1 if loads else 0
+            st.expert_loads += loads
+            st.expert_cache_hits += hits
+            st.staged_bytes += nbytes
+            st.peak_staged_experts = max(st.peak_staged_experts, len(placed))
+        elapsed = time.perf_counter() - began
+        st.host_staging_seconds += elapsed
+        st.h2d_submit_seconds += elapsed if calls else 0.0
+        return placed
 
     def host_bank(self, key, bank):
         """``bank`` in page-locked host memory (copied once per bank) when
@@ -194,6 +303,7 @@ class HostResidency:
         if cached is None or cached[0] != ident:
             cached = (ident, bank_like(bank, {n: t.pin_memory() for n, t in bank_buffers(bank).items()}))
             self._host[key] = cached
+            self.statistics.pinned_bytes += sum(t.numel() * t.element_size() for t in bank_buffers(bank).values())
         return cached[1]
 
     @torch.no_grad()
@@ -207,7 +317,10 @@ class HostResidency:
             return torch.zeros_like(x)
         host = self.host_bank(key, bank)
         experts = host.w13_weight.shape[0]
+        began = time.perf_counter()
         host_ids = ids.to("cpu", torch.int64)
+        self.statistics.routing_host_seconds += time.perf_counter() - began
+        self.statistics.forward_calls += 1
         if host_ids.numel() and (int(host_ids.min()) < 0 or int(host_ids.max()) >= experts):
             raise ValueError(f"Expert IDs must be in [0, {experts})")
         self.calls += 1
@@ -223,16 +336,17 @@ class HostResidency:
                 routed = list(dict.fromkeys(host_ids[0].tolist()))
                 chosen = [e for e in routed if e in cache.slot_of] + [e for e in routed if e not in cache.slot_of]
                 chosen = chosen[:self.cache_experts]
-                cached = cache.place(host, chosen, keep=set(chosen))
+                cached = self._place(cache, host, chosen, set(chosen), hot=True, device=x.device)
             else:
                 cached = cache.lookup(unique)
+                self.statistics.hot_cache_hits += len(cached)
         cold = [e for e in unique if e not in cached]
         if top_k <= self.max_pair_rows:
             if not cold:
                 return self._whole(backend, x, host_ids, weights, cache.bank(host), cached, experts)
             if not cached and len(cold) <= self.pool.capacity:
                 self.pool.bind(host, x.device)
-                staged = self.pool.place(host, cold, keep=set(cold))
+                staged = self._place(self.pool, host, cold, set(cold), hot=False, device=x.device)
                 return self._whole(backend, x, host_ids, weights, self.pool.bank(host), staged, experts)
         return self._grouped(backend, x, host_ids, weights, host, cache, cached, cold, experts)
 
@@ -250,6 +364,7 @@ class HostResidency:
 
     def _grouped(self, backend, x, host_ids, weights, host, cache, cached: dict, cold: list, experts: int) -> Tensor:
         self.grouped_calls += 1
+        self.statistics.grouped_calls += 1
         tokens, top_k = host_ids.shape
         flat = host_ids.reshape(-1)
         pair_out = torch.empty((flat.numel(), x.shape[-1]), dtype=torch.float32, device=x.device)
@@ -262,7 +377,8 @@ class HostResidency:
 
             def stage(group=group):
                 self.pool.bind(host, x.device)
-                return self.pool.bank(host), self.pool.place(host, group, keep=set(group))
+                return self.pool.bank(host), self._place(self.pool, host, group, set(group), hot=False,
+                                                         device=x.device)
             groups.append((stage, group))
         for prepare, group in groups:
             slots_bank, slots = prepare()

@@ -194,6 +194,38 @@ def test_manager_host_mode_routes_through_the_tier(bank):
     manager.close()
 
 
+def test_statistics_count_the_host_traffic(bank):
+    """OffloadStatistics (offload.py:59-98): hot-cache and pool loads and hits,
+    the bytes and tensor copies they moved, forward calls, host timings; no
+    event time without profile_transfers, and none for copies off the GPU
+    (test_offload.py:521-531)."""
+    per_expert = sum(t[0].numel() * t.element_size() for t in staging.bank_buffers(bank).values())
+    tensors = len(staging.bank_buffers(bank))
+    backend = SignatureBackend()
+    model = nn.ModuleDict({"experts": FP8Experts(bank)})
+    manager = offload.install_expert_offload(model, backend=backend, residency="host", max_staged_experts=4,
+                                             cache_experts=3, pin_memory=False)
+    g = torch.Generator().manual_seed(12)
+    x1 = torch.randn(1, 128, generator=g).bfloat16()
+    w2 = torch.rand(1, 2, generator=g)
+    model["experts"](x1, torch.tensor([[3, 7]]), w2)   # two hot-cache loads
+    model["experts"](x1, torch.tensor([[7, 3]]), w2)   # two hot-cache hits
+    x2 = torch.randn(2, 128, generator=g).bfloat16()
+    ids = torch.tensor([[3, 5], [11, 7]])              # a prompt: 3, 7 from the cache, 5, 11 staged
+    got = model["experts"](x2, ids, torch.rand(2, 2, generator=g))
+    assert got.shape == (2, 128)
+    st = manager.stats
+    assert (st.forward_calls, st.hot_cache_loads, st.hot_cache_hits) == (3, 2, 4)
+    assert (st.expert_loads, st.staging_calls, st.peak_staged_experts, st.grouped_calls) == (2, 1, 2, 1)
+    assert st.staged_bytes == 2 * per_expert and st.h2d_bytes == 4 * per_expert
+    assert st.h2d_copy_calls == 4 * tensors
+    assert st.hot_cache_capacity_experts == 3 and st.hot_cache_bytes == 3 * per_expert
+    assert st.device_buffer_bytes == st.hot_cache_bytes + 4 * per_expert
+    assert st.routing_host_seconds > 0 and st.host_staging_seconds > 0 and st.h2d_seconds == 0
+    assert st.as_dict()["expert_loads"] == 2
+    manager.close()
+
+
 def test_empty_call_returns_empty_rows(bank):
     tier = host()
     out = tier.forward("a", bank, SignatureBackend(), torch.zeros(0, 128), torch.zeros(0, 2, dtype=torch.long),

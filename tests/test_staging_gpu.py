@@ -87,3 +87,29 @@ def test_manager_residency_modes_agree(cuda):
     torch.cuda.synchronize()
     for a, b in zip(outputs["hbm"], outputs["host"]):
         assert torch.equal(a, b)
+
+
+def test_profiled_transfers_report_event_time(cuda):
+    """profile_transfers times the host tier's copies with HIP events
+    (test_offload.py:903-947: h2d_seconds > 0 after staged calls); without it
+    the event time stays 0 and the byte counts are the same."""
+    print_case("host tier transfer profiling")
+    g = torch.Generator().manual_seed(503)
+    bank = random_fp8_bank(EXPERTS, HIDDEN, INTER, layout="channel", generator=g)
+    per_expert = sum(t[0].numel() * t.element_size() for t in staging.bank_buffers(bank).values())
+    seen = {}
+    for profile in (False, True):
+        model = nn.ModuleDict({"experts": FP8Experts(bank)})
+        manager = offload.install_expert_offload(model, residency="host", max_staged_experts=8, cache_experts=4,
+                                                 profile_transfers=profile)
+        gg = torch.Generator().manual_seed(10)
+        for tokens in (1, 1, 3):
+            model["experts"](*route(tokens, 4, gg, cuda))
+        torch.cuda.synchronize()
+        st = manager.stats
+        seen[profile] = st.h2d_bytes
+        assert st.h2d_bytes == (st.expert_loads + st.hot_cache_loads) * per_expert
+        assert st.pinned_bytes == bank.nbytes
+        assert (st.h2d_seconds > 0) == profile
+        manager.close()
+    assert seen[False] == seen[True]
