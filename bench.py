@@ -298,6 +298,90 @@ def pmc_pass(workload: str = "decode", rounds: int = 8, copy_mib: int = 256):
           flush=True)
 
 
+FUSED_PHASES = ("entry", "routed", "loads_issued", "first_gateup_batch", "gateup_done", "hidden_ready", "down_done")
+
+
+def phase_times(replays: int = 64):
+    """Phase timeline of the 1-token single-launch decode: the graph of one
+    routed decode step per rotating layer bank that the headline times, each
+    step captured with its own phase buffer (dmoe_debug_set_phase_buffer: the
+    kernel's timing instance stamps the 100 MHz real-time counter at 7 points
+    in thread 0 of every workgroup), replayed `replays` times.  Per phase, over
+    workgroups and steps, the 10th / 50th / 90th percentile of (stamp - the
+    step's earliest entry stamp) in microseconds; beside it the same graph's
+    HIP-event time per step with the ordinary kernel."""
+    import numpy as np
+    import torch
+
+    from drama_moe import _lib
+    from drama_moe.offload import HipExpertBackend
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    banks = [make_layer_bank(layer, device) for layer in range(LAYERS)]
+    backend = HipExpertBackend()
+    stream = torch.cuda.Stream(device)
+    lib = _lib.library()
+    xs, logits, outs = decode_inputs(1, device, SEED)
+    us_plain, _ = decode_graph_us(backend, xs, logits, banks, outs, stream, 16 * replays, 64)
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    per_step = cus * len(FUSED_PHASES)
+    buf = torch.zeros(LAYERS, per_step, dtype=torch.int64, device=device)
+
+    def step(i):
+        _lib.check(lib.dmoe_debug_set_phase_buffer(_lib.ptr(buf[i]), per_step))
+        backend.forward_routed(xs[i], logits[i], TOP_K, banks[i], out=outs[i])
+
+    try:
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            for i in range(LAYERS):
+                step(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(LAYERS):
+                step(i)
+    finally:
+        _lib.check(lib.dmoe_debug_set_phase_buffer(None, 0))
+    for _ in range(4):
+        graph.replay()
+    torch.cuda.synchronize()
+    rel = []
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    timed_ms = 0.0
+    for _ in range(replays):
+        buf.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            graph.replay()
+            stop.record(stream)
+        torch.cuda.synchronize()
+        timed_ms += start.elapsed_time(stop)
+        stamps = buf.view(LAYERS, cus, len(FUSED_PHASES)).cpu().numpy().astype(np.float64)
+        for layer in range(LAYERS):
+            st = stamps[layer]
+            t0 = st[:, 0][st[:, 0] > 0].min()
+            rel.append(np.where(st > 0, (st - t0) / 100.0, np.nan))  # 100 MHz ticks -> us
+    status = backend.status(device)
+    if status:
+        raise RuntimeError(f"decode steps raised device status bits {status:#x}")
+    rel = np.stack(rel)  # [steps, workgroups, phases]
+    phases = {}
+    for k, name in enumerate(FUSED_PHASES):
+        v = rel[:, :, k]
+        v = v[~np.isnan(v)]
+        phases[name] = {"p10_us": round(float(np.percentile(v, 10)), 2), "median_us": round(float(np.median(v)), 2),
+                        "p90_us": round(float(np.percentile(v, 90)), 2), "workgroups": int(v.size // rel.shape[0])}
+    last = np.nanmax(rel[:, :, -1], axis=1)
+    print(json.dumps({"phase_times": phases, "steps": int(rel.shape[0]), "workgroups_per_step": cus,
+                      "last_down_done_median_us": round(float(np.median(last)), 2),
+                      "timing_instance_us_per_step": round(timed_ms * 1e3 / (replays * LAYERS), 2),
+                      "ordinary_kernel_us_per_step": round(us_plain, 2),
+                      "clock": "s_memrealtime, 100 MHz"}), flush=True)
+
+
 # MiB one 1-token decode call reads: 8 experts x 3 x 768 x 2048 FP8 bytes plus
 # their per-channel scales (37.86 MB).
 DECODE_MB = 36.1
@@ -825,6 +909,8 @@ def main():
     parser.add_argument("--no-hybrid", action="store_true")
     parser.add_argument("--pmc-pass", nargs="?", const="decode", choices=PMC_WORKLOADS,
                         help="run an eager counter-collection workload (see pmc_pass) instead of the benchmark")
+    parser.add_argument("--phase-times", action="store_true",
+                        help="time the phases of the 1-token single-launch decode instead of the benchmark")
     parser.add_argument("--stream-sweep", action="store_true",
                         help="measure the plain streaming-read bandwidth by size instead of the benchmark")
     args = parser.parse_args()
@@ -840,6 +926,9 @@ def main():
         return
     if args.stream_sweep:
         stream_sweep()
+        return
+    if args.phase_times:
+        phase_times()
         return
     steps = max(1, args.steps)
     gpu = run_gpu(steps, args.warmup)

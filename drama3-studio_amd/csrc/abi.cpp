@@ -68,6 +68,10 @@ std::atomic<uint64_t> g_spin_ticks{kDefaultSpinTicks};
 // Diagnostic switch (dmoe_debug_force_sync_timeout): hand-off readers wait for
 // a tag no producer writes, so every wait runs to the bound.
 std::atomic<int> g_force_timeout{0};
+// Diagnostic phase stamps (dmoe_debug_set_phase_buffer): the FP8 single-launch
+// decodes launched while a buffer is set stamp each workgroup's phases into it.
+std::atomic<uint64_t*> g_phase_times{nullptr};
+std::atomic<int64_t> g_phase_entries{0};
 
 // tokens * top_k in 64 bits, checked against the per-call pair limit before
 // it is narrowed (a wrapped product could look like a small valid count).
@@ -353,6 +357,8 @@ bool fp8_fused_call(const BankGeom& g, const Activations& a, const dmoe::RouteSo
     fa.status = status;
     fa.spin_ticks = g_spin_ticks.load(std::memory_order_relaxed);
     fa.tag_skew = g_force_timeout.load(std::memory_order_relaxed) ? 1u : 0u;
+    fa.phase_times = g_phase_times.load(std::memory_order_relaxed);
+    fa.phase_entries = fa.phase_times ? g_phase_entries.load(std::memory_order_relaxed) : 0;
     if (!order_streams) return dmoe::launch_fp8_fused_decode(fa, stream);
     return ordered_fused_launch(stream, [&] { return dmoe::launch_fp8_fused_decode(fa, stream); });
 }
@@ -750,6 +756,15 @@ int dmoe_set_fused_decode(int mode) { return g_fused_decode.exchange(mode <= 0 ?
 uint64_t dmoe_set_sync_spin_limit(uint64_t ticks) { return g_spin_ticks.exchange(ticks); }
 
 int dmoe_debug_force_sync_timeout(int force) { return g_force_timeout.exchange(force != 0 ? 1 : 0); }
+
+int dmoe_debug_set_phase_buffer(uint64_t* buffer, int64_t entries) {
+    return checked([&] {
+        require(buffer == nullptr || (entries >= 0 && reinterpret_cast<uintptr_t>(buffer) % 8 == 0),
+                "phase buffer: 8-byte aligned device words and a non-negative entry count");
+        g_phase_entries.store(buffer ? entries : 0, std::memory_order_relaxed);
+        g_phase_times.store(buffer, std::memory_order_relaxed);
+    });
+}
 
 const char* dmoe_last_error(void) { return g_last_error.c_str(); }
 

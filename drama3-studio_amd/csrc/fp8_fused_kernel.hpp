@@ -122,10 +122,18 @@ __device__ __forceinline__ void wave_route_load(const RouteSource& src, int t, i
 // KBW: 128-column K blocks per wave of a gate/up unit (H <= 8 * 128 * KBW).
 // KBJ: 128-column K blocks of the down projection (I <= 128 * KBJ); one wave
 // runs the whole K chain of a down job, as the three-launch decode does.
-template <int WF, int KBW, int KBJ>
+// TIMES: the diagnostic instance that stamps the 100 MHz real-time counter at
+// each phase (thread 0 of every workgroup, into a.phase_times).
+template <int WF, int KBW, int KBJ, bool TIMES = false>
 __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDecodeArgs a) {
     constexpr int kUnitDepth = KBW >= 2 ? 3 : kMaxUnitDepth;  // gate/up units in flight per wave
     __shared__ FzLds s;
+    auto stamp = [&](int phase) {
+        if constexpr (TIMES) {
+            if (threadIdx.x == 0) a.phase_times[(int64_t)blockIdx.x * kFusedPhases + phase] = __builtin_amdgcn_s_memrealtime();
+        }
+    };
+    stamp(0);
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const int col = lane % 16, grp = lane / 16;
     const int H = a.w13.K, I = a.w13.N / 2, KB = H / 128, KBd = I / 128;
@@ -328,6 +336,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         }
     }
     lds_barrier();  // route slots and the activation group maxima
+    stamp(1);
 
     // ------------------------------------------------------- grouping
     // Every wave ranks the pairs in its registers (lane p: pair p), so it can
@@ -444,6 +453,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     }
 
     lds_barrier();  // grouping lists and activation rows
+    stamp(2);
     if (tid == kTicketThread) {
         const int n_slot = (G - eslot + kEpochSlots - 1) / kEpochSlots;  // workgroups sharing the slot
         s.epoch = (uint32_t)(ticket / (uint64_t)n_slot) + 1u;
@@ -545,7 +555,9 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         for (int pass = 1; pass < passes; ++pass) run_pass(pass);
     };
     unit_batch(0, kUnitDepth < my_units);
+    stamp(3);
     for (int j0 = kUnitDepth; j0 < my_units; j0 += kUnitDepth) unit_batch(j0, j0 + kUnitDepth < my_units);
+    stamp(4);
     // The first down job's rows go out only now, and only from waves that
     // have a job: the gate/up rows get the memory system to themselves, and
     // these stream during the hidden hand-off, which they are not needed
@@ -623,6 +635,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             timed_out = __builtin_amdgcn_s_memrealtime() - t0 > a.spin_ticks;
         }
         if (timed_out) raise_status(a.status, kSyncTimeout);
+        if (u0 == 0) stamp(5);
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int u = u0 + q * kHUnits + tid / 16;
@@ -727,6 +740,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         }
         lds_barrier();  // partials reused by the next tile
     }
+    stamp(6);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load outlives the wave
 }
 
@@ -734,6 +748,8 @@ namespace {
 
 template <int WF, int KBW, int KBJ>
 bool launch_fused_instance(const FusedDecodeArgs& a, hipStream_t stream) {
+    // The stamping instance exists for the FP8 format only, launched when a
+    // phase buffer holds one row per workgroup.
     // One workgroup per CU (every instance keeps one resident workgroup per CU
     // by its launch bounds and LDS), checked once per device.
     static std::mutex mu;
@@ -755,6 +771,13 @@ bool launch_fused_instance(const FusedDecodeArgs& a, hipStream_t stream) {
         grid = it->second;
     }
     if (grid < 1) return false;
+    if constexpr (WF == kWfFp8) {
+        if (a.phase_times != nullptr && a.phase_entries >= (int64_t)grid * kFusedPhases) {
+            hipLaunchKernelGGL((fp8_fused_decode_kernel<WF, KBW, KBJ, true>), dim3(grid), dim3(kFzThreads), 0, stream,
+                               a);
+            return true;
+        }
+    }
     hipLaunchKernelGGL((fp8_fused_decode_kernel<WF, KBW, KBJ>), dim3(grid), dim3(kFzThreads), 0, stream, a);
     return true;
 }

@@ -228,7 +228,13 @@ struct FusedDecodeArgs {
     int* status;
     uint64_t spin_ticks;        // bound of the hand-off wait (100 MHz ticks) before kSyncTimeout
     uint32_t tag_skew;          // 0; 1 makes readers wait for a tag no producer writes (diagnostic)
+    uint64_t* phase_times;      // null; else [grid, kFusedPhases] real-time stamps per workgroup (diagnostic)
+    int64_t phase_entries;      // entries of phase_times
 };
+// Phase stamps of the single-launch decode's timing instance: entry, routed,
+// weight loads issued, first gate/up batch published, gate/up done, hidden
+// ready (the hand-off wait ended), down done.
+constexpr int kFusedPhases = 7;
 
 bool fused_decode_fits(int pairs, int rows, int H, int I, int experts, int top_k, int x_esize, int routed_tokens);
 // Launches the fused decode; false (nothing enqueued) when the device cannot

@@ -94,6 +94,7 @@ _SIGNATURES = {
     "dmoe_combine_slots": ([_P, _L, _P, _I, _I, _I, _I, _I, _P, _I, _L, _P], _I),
     "dmoe_silu_table": ([_P, _P], _I),
     "dmoe_stream_read": ([_P, _L, _P, _P], _I),
+    "dmoe_debug_set_phase_buffer": ([_P, _L], _I),
     "dmoe_cpu_executor_create": ([_I, _I, _I, _I, _I], _P),
     "dmoe_cpu_executor_destroy": ([_P], None),
     "dmoe_cpu_executor_isa": ([_P], _I),

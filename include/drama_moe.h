@@ -108,6 +108,17 @@ DMOE_API uint64_t dmoe_set_sync_spin_limit(uint64_t ticks);
  * reference. */
 DMOE_API int dmoe_debug_force_sync_timeout(int force);
 
+/* Diagnostic phase timing of the single-launch FP8 decode (default off, null
+ * buffer).  While `buffer` (device, `entries` 64-bit words) is set, FP8
+ * single-launch decodes launched -- or captured -- from then on run a timing
+ * instance of the kernel whose thread 0 of every workgroup w stores the GPU's
+ * 100 MHz real-time counter at phase k into buffer[7 w + k]: 0 entry, 1 routed,
+ * 2 weight loads issued, 3 first gate/up batch published, 4 gate/up done,
+ * 5 hidden ready (the hand-off wait ended), 6 down done.  A buffer with fewer
+ * than 7 entries per workgroup (one workgroup per CU) leaves the ordinary
+ * kernel in place.  Null turns it off.  No counterpart in the reference. */
+DMOE_API int dmoe_debug_set_phase_buffer(uint64_t* buffer, int64_t entries);
+
 /* Last error message of the calling thread.  Replaces drama_native_error
  * (native/include/drama_native.h:19; runtime.cpp:290). */
 DMOE_API const char* dmoe_last_error(void);

@@ -340,3 +340,35 @@ def test_manager_reports_a_given_up_hand_off_at_its_sync(cuda):
         assert torch.equal(module(x, ids, w), good)  # the status was cleared; the next call is exact
     finally:
         manager.close()
+
+
+def test_phase_timing_instance_gives_the_same_bits_and_ordered_stamps(cuda):
+    """dmoe_debug_set_phase_buffer swaps in the kernel's timing instance: its
+    outputs equal the ordinary kernel's bit for bit, every workgroup stamps
+    its seven phases in order, and clearing the buffer restores the ordinary
+    kernel (the buffer is no longer written)."""
+    print_case("fused phase timing instance")
+    lib = _lib.library()
+    g = torch.Generator().manual_seed(606)
+    staged = to_device(random_fp8_bank(128, 2048, 768, layout="channel", generator=g), cuda)
+    x = torch.randn(1, 2048, generator=g).bfloat16().to(cuda)
+    logits = torch.randn(1, 128, generator=g).to(cuda)
+    backend = HipExpertBackend()
+    plain, _, _ = backend.forward_routed(x, logits, 8, staged)
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    buf = torch.zeros(cus * 7, dtype=torch.int64, device=cuda)
+    _lib.check(lib.dmoe_debug_set_phase_buffer(_lib.ptr(buf), buf.numel()))
+    try:
+        timed, _, _ = backend.forward_routed(x, logits, 8, staged)
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(lib.dmoe_debug_set_phase_buffer(None, 0))
+    assert torch.equal(timed, plain)
+    stamps = buf.view(cus, 7).cpu()
+    assert bool((stamps > 0).all())
+    assert bool((stamps[:, 1:] >= stamps[:, :-1]).all())
+    buf.zero_()
+    again, _, _ = backend.forward_routed(x, logits, 8, staged)
+    torch.cuda.synchronize()
+    assert torch.equal(again, plain) and int(buf.abs().sum()) == 0
+    assert int(backend.status(cuda)) == 0
