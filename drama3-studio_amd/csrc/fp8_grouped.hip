@@ -610,6 +610,13 @@ __global__ __launch_bounds__(kGThreads, 1) void fp8_grouped_down_kernel(GroupedD
 // out[t] = sum over slots j = 0 .. k-1 of partial[t * k + j] in slot order,
 // fp32, then the output type; invalid pairs contribute 0.  Reference:
 // offload.py:1242-1244 (view(T, k, H).sum(1).to(dtype)).
+// One thread per (token, 8 columns): out = the token's valid pair rows summed
+// in router slot order (the first slot assigns, so a lone -0 stays -0).  Up
+// to kCombineSlots slots every id and partial load goes out before the sum
+// (clamped, in bounds; invalid slots are masked after the load); 16-byte
+// stores when a 16-bit output row is aligned.
+constexpr int kCombineSlots = 8;
+
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int chunks = a.H / 8;
@@ -617,29 +624,52 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int t = (int)(i / chunks), c = (int)(i % chunks) * 8;
     float acc[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-    for (int j = 0; j < a.top_k; ++j) {
-        const int64_t p = (int64_t)t * a.top_k + j;
-        const int64_t id = load_id(a.ids, p, a.ids_dtype);
-        if (id < 0 || id >= a.experts) continue;
-        const float* src = a.partial + p * a.partial_row_stride + c;
-        const v4f x0 = *(const v4f*)src, x1 = *(const v4f*)(src + 4);
-        if (j == 0) {
+    for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+    auto add = [&](int j, const v4f& x0, const v4f& x1) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                acc[q] = x0[q];
-                acc[4 + q] = x1[q];
-            }
-        } else {
+        for (int q = 0; q < 4; ++q) {
+            acc[q] = j == 0 ? x0[q] : acc[q] + x0[q];
+            acc[4 + q] = j == 0 ? x1[q] : acc[4 + q] + x1[q];
+        }
+    };
+    if (a.top_k <= kCombineSlots) {
+        bool ok[kCombineSlots];
+        v4f x0[kCombineSlots], x1[kCombineSlots];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                acc[q] += x0[q];
-                acc[4 + q] += x1[q];
-            }
+        for (int j = 0; j < kCombineSlots; ++j) {
+            const int64_t p = (int64_t)t * a.top_k + min(j, a.top_k - 1);
+            const int64_t id = load_id(a.ids, p, a.ids_dtype);
+            ok[j] = j < a.top_k && id >= 0 && id < a.experts;
+            const float* src = a.partial + p * a.partial_row_stride + c;
+            x0[j] = *(const v4f*)src;
+            x1[j] = *(const v4f*)(src + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < kCombineSlots; ++j)
+            if (ok[j]) add(j, x0[j], x1[j]);
+    } else {
+        for (int j = 0; j < a.top_k; ++j) {
+            const int64_t p = (int64_t)t * a.top_k + j;
+            const int64_t id = load_id(a.ids, p, a.ids_dtype);
+            if (id < 0 || id >= a.experts) continue;
+            const float* src = a.partial + p * a.partial_row_stride + c;
+            add(j, *(const v4f*)src, *(const v4f*)(src + 4));
         }
     }
+    const int64_t o = (int64_t)t * a.out_row_stride + c;
+    if (a.out_dtype != kF32 && reinterpret_cast<uintptr_t>((uint16_t*)a.out + o) % 16 == 0) {
+        v4i packed;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) store_from_f32(a.out, (int64_t)t * a.out_row_stride + c + q, a.out_dtype, acc[q]);
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = a.out_dtype == kBF16 ? f32_to_bf16(acc[2 * q]) : f32_to_f16(acc[2 * q]);
+            const uint32_t hi = a.out_dtype == kBF16 ? f32_to_bf16(acc[2 * q + 1]) : f32_to_f16(acc[2 * q + 1]);
+            packed[q] = (int)(lo | (hi << 16));
+        }
+        *(v4i*)((uint16_t*)a.out + o) = packed;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) store_from_f32(a.out, o + q, a.out_dtype, acc[q]);
+    }
 }
 
 // Partial rows of pairs with an invalid expert id are zero (the grouped GEMMs
