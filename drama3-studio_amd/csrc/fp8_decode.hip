@@ -113,6 +113,8 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
 #pragma unroll
     for (int i = 0; i < KBW; ++i) {
         const int kb = wave + i * kUpWaves;
+        bg[i] = bu[i] = zero_wraw<WF>();  // blocks past K: defined operands, masked at use
+        swg[i] = swu[i] = 0.0f;
         if (kb < KB) {
             bg[i] = load_wraw<WF>(wg, H, kb, grp);
             bu[i] = load_wraw<WF>(wu, H, kb, grp);
@@ -131,6 +133,9 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
 #pragma unroll
         for (int i = 0; i < KBW; ++i) {
             const int kb = wave + i * kUpWaves;
+            af[i] = zero8i;  // blocks past K: defined operands, masked at use
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sx[i][r] = 0.0f;
             if (kb < KB) {
                 af[i] = live ? load32(a.xq + row * a.xq_row_stride + kb * 128 + grp * 32) : zero8i;
 #pragma unroll
@@ -154,15 +159,17 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
         v4f acc_g = zero, acc_u = zero;
 #pragma unroll
         for (int i = 0; i < KBW; ++i) {
-            const int kb = wave + i * kUpWaves;
-            if (kb < KB) {
-                const v8i ap = a_operand<WF>(af[i]);
-                const v4f dg = mfma_w<WF>(ap, bg[i], zero), du = mfma_w<WF>(ap, bu[i], zero);
+            // a block past K (clamped operands) is masked by selects, not a
+            // branch, so the MFMAs of all blocks stay in one basic block
+            const bool in = wave + i * kUpWaves < KB;
+            const v8i ap = a_operand<WF>(af[i]);
+            const v4f dg = mfma_w<WF>(ap, bg[i], zero), du = mfma_w<WF>(ap, bu[i], zero);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc_g[r] = fmaf(dg[r] * sx[i][r], swg[i], acc_g[r]);
-                    acc_u[r] = fmaf(du[r] * sx[i][r], swu[i], acc_u[r]);
-                }
+            for (int r = 0; r < 4; ++r) {
+                const float tg = fmaf(dg[r] * sx[i][r], swg[i], acc_g[r]);
+                const float tu = fmaf(du[r] * sx[i][r], swu[i], acc_u[r]);
+                acc_g[r] = in ? tg : acc_g[r];
+                acc_u[r] = in ? tu : acc_u[r];
             }
         }
 #pragma unroll

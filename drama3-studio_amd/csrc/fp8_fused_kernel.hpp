@@ -24,11 +24,13 @@
 //      registers, so the whole layer is in flight;
 //   2. quantizes the activation rows to FP8 in LDS while the weights land,
 //      reduces each unit's per-wave partials in LDS and publishes every value
-//      h = silu(gate) * up as one 64-bit word (fp32 bits | call epoch << 32)
-//      with an L2-coherent store;
+//      h = silu(gate) * up as one 32-bit word (fp32 bits ^ kHandoffXor, never
+//      0) with an agent-coherent store, into the hand-off buffer of the call's
+//      epoch parity, and clears its share of the other buffer for the next
+//      call;
 //   3. reads all of h with coherent loads, each lane re-reading until its
-//      words carry this call's epoch (the data is its own ready flag: no
-//      counter, no separate flag round trip), quantizes it per (pair,
+//      words are non-zero (the data is its own ready flag: no counter, no
+//      separate flag round trip), quantizes it per (pair,
 //      128-group) to FP8 in LDS, runs its down rows with the weights already
 //      in registers, and sums the route-weighted partials of each token in
 //      router slot order before one store -- deterministic, no atomics on the
@@ -100,8 +102,29 @@ __device__ __forceinline__ v8i lds32(const uint8_t* p) {
     return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-__device__ __forceinline__ uint64_t load_coherent_u64(const uint64_t* p) {
-    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Hand-off words: fp32 h bits ^ kHandoffXor.  A cleared word (0) decodes to
+// the signalling-NaN bits kHandoffXor, which no arithmetic result carries
+// (NaN results are quiet); an h with exactly those bits is published as a
+// quiet NaN, so a published word is never 0.
+constexpr uint32_t kHandoffXor = 0x7F800001u;
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+constexpr v4i zero4i = {0, 0, 0, 0};
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 family
+constexpr int kCpolSc1 = 16;              // the cache policy of an agent-scope atomic access
+
+__device__ __forceinline__ uint32_t handoff_encode(float h) {
+    const uint32_t b = __float_as_uint(h);
+    return (b == kHandoffXor ? 0x7FC00001u : b) ^ kHandoffXor;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t handoff_buffer(uint32_t* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, kHandoffWords * 4, kBufferWord3);
+}
+
+// 16 bytes of hand-off words with the agent-scope load's cache policy (no
+// stale copy from a non-coherent cache); each 4-byte word is read whole.
+__device__ __forceinline__ v4i load_handoff16(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, kCpolSc1));
 }
 
 constexpr int kRouteJ = kRouteLaneSlots;  // logits per lane (experts l + 64 j)
@@ -506,14 +529,17 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
 #pragma unroll
                 for (int i = 0; i < KBW; ++i) {
                     const int kb = wave + i * kFzWaves;
-                    if (kb < KB) {
-                        const v8i ar = a_operand<WF>(lds32(&s.xq[arow * H + kb * 128 + grp * 32]));
-                        const v4f dq = mfma_w<WF>(live ? ar : zero8i, ub[d][i], zero);
+                    // a block past K (clamped rows, as loaded) is masked by
+                    // selects, not a branch, so the MFMAs stay in one block
+                    const bool in = kb < KB;
+                    const int kbc = min(kb, KB - 1);
+                    const v8i ar = a_operand<WF>(lds32(&s.xq[arow * H + kbc * 128 + grp * 32]));
+                    const v4f dq = mfma_w<WF>(live ? ar : zero8i, ub[d][i], zero);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float sx = cl[r] ? s.xs[crow[r] * gpr + kb] : 0.0f;
-                            acc[r] = fmaf(dq[r] * sx, us[d][i], acc[r]);
-                        }
+                    for (int r = 0; r < 4; ++r) {
+                        const float sx = cl[r] ? s.xs[crow[r] * gpr + kbc] : 0.0f;
+                        const float t = fmaf(dq[r] * sx, us[d][i], acc[r]);
+                        acc[r] = in ? t : acc[r];
                     }
                 }
 #pragma unroll
@@ -540,10 +566,10 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                     up = round_through(up, a.gu_dtype);
                     const float h = silu_f32(g) * up;
                     const int p = s.plist[s.ucoord[d][1] + pass * 16 + m];
-                    // column 8 a + b of a 128-group lives at word 16 b + a (see the reader)
-                    const int word = (c0 / 128) * 128 + c * 16 + (c0 % 128) / 8;
-                    __hip_atomic_store(a.ht + (int64_t)p * I + word, ((uint64_t)epoch << 32) | __float_as_uint(h),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    // column 8 a + b of a 128-group lives at word 64 (b / 4) + 4 a + b % 4 (see the reader)
+                    const int word = (c0 / 128) * 128 + 64 * (c >> 2) + 4 * ((c0 % 128) / 8) + (c & 3);
+                    __hip_atomic_store(a.ht + (int64_t)(epoch & 1) * kHandoffWords + (int64_t)p * I + word,
+                                       handoff_encode(h), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
             lds_barrier();  // partials and coordinates read before they are overwritten
@@ -564,7 +590,20 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     // before.
     if (B < tiles && my_jobs > 0) load_job(B, wave);
     if (my_units == 0) lds_barrier();  // no gate/up barrier ran: order the epoch's LDS write
-    epoch = s.epoch;
+    epoch = __builtin_amdgcn_readfirstlane(s.epoch);
+    {
+        // The next call polls the other buffer: every workgroup clears its
+        // share of it (all kHandoffWords words, whatever this call's size), 16
+        // bytes per lane, while its own hand-off wait is still ahead.  Calls
+        // on one workspace never overlap, so nothing reads that buffer now.
+        const __amdgpu_buffer_rsrc_t next = handoff_buffer(a.ht + (int64_t)((epoch + 1) & 1) * kHandoffWords);
+        const int share = (kHandoffWords / 4 + G - 1) / G * 4;  // words per workgroup, a multiple of 4
+        for (int i = tid * 4; i < share; i += kFzThreads * 4) {
+            const int word = B * share + i;
+            if (word < kHandoffWords)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, zero4i), next, word * 4, 0, kCpolSc1);
+        }
+    }
     if (B >= tiles) {  // no down rows for this workgroup
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load outlives the wave
         return;
@@ -589,47 +628,48 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
 
     // ---------------------------------------- hidden: wait + quantize
     // One (pair, 128-group) per 16 lanes, two groups per lane in flight.
-    // Column 8 a + b of a group is stored at word 16 b + a, so word j of
-    // lane `col` (column 8 col + j) sits at 16 j + col: every load of the 16
-    // lanes reads 128 contiguous bytes, and each lane ends with its 8
-    // consecutive columns (one producer unit).
+    // Column 8 a + b of a group is stored at word 64 (b / 4) + 4 a + b % 4,
+    // so lane `col` finds its columns 8 col + 4 i .. + 3 at words 64 i +
+    // 4 col: each 16-byte load of the 16 lanes reads 256 contiguous bytes,
+    // and each lane ends with its 8 consecutive columns (one producer unit).
     constexpr int kHUnits = kFzThreads / 16;
+    const __amdgpu_buffer_rsrc_t hbuf = handoff_buffer(a.ht + (int64_t)(epoch & 1) * kHandoffWords);
     for (int u0 = 0; u0 < P * KBd; u0 += 2 * kHUnits) {
-        uint64_t w[2][8];
+        v4i w[2][2];
         bool want[2];
-        const uint64_t* hsrc[2];
+        int hoff[2];  // byte offset of the lane's first word
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int u = u0 + q * kHUnits + tid / 16;
             want[q] = u < P * KBd && s.sid[min(u, P * KBd - 1) / KBd] >= 0;
-            hsrc[q] = a.ht + (int64_t)(want[q] ? u / KBd : 0) * I + (want[q] ? u % KBd : 0) * 128 + col;
+            hoff[q] = ((want[q] ? u / KBd : 0) * I + (want[q] ? u % KBd : 0) * 128 + 4 * col) * 4;
         }
-        // the tag a ready word carries: this call's epoch (tag_skew = 1 only in
-        // the diagnostic mode that forces every wait to run to its bound)
-        const uint32_t tag = epoch + a.tag_skew;
-        auto ok = [&](uint64_t word) { return (uint32_t)(word >> 32) == tag; };
+        // a word is ready once non-zero (tag_skew = 1 only in the diagnostic
+        // mode that forces every wait to run to its bound)
+        const bool skew = a.tag_skew != 0;
+        auto ok = [&](int q, v4i v) { return !want[q] || (!skew && v[0] != 0 && v[1] != 0 && v[2] != 0 && v[3] != 0); };
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         bool timed_out = false;
-        // all 16 words at once (one round trip when the producers are done),
-        // then re-read only the words that still carry an older epoch
+        // all four 16-byte loads at once (one round trip when the producers
+        // are done), then re-read only the ones still holding a cleared word
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) w[q][j] = want[q] ? load_coherent_u64(hsrc[q] + 16 * j) : ((uint64_t)tag << 32);
+            for (int i = 0; i < 2; ++i) w[q][i] = want[q] ? load_handoff16(hbuf, hoff[q] + 256 * i) : zero4i;
         bool ready = true;
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ready = ready && ok(w[q][j]);
+            for (int i = 0; i < 2; ++i) ready = ready && ok(q, w[q][i]);
         while (!ready && !timed_out) {
             __builtin_amdgcn_s_sleep(1);
             ready = true;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    if (!ok(w[q][j])) w[q][j] = load_coherent_u64(hsrc[q] + 16 * j);
-                    ready = ready && ok(w[q][j]);
+                for (int i = 0; i < 2; ++i) {
+                    if (!ok(q, w[q][i])) w[q][i] = load_handoff16(hbuf, hoff[q] + 256 * i);
+                    ready = ready && ok(q, w[q][i]);
                 }
             }
             timed_out = __builtin_amdgcn_s_memrealtime() - t0 > a.spin_ticks;
@@ -643,7 +683,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 const int p = u / KBd, g = u % KBd;
                 F8 h;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) h.v[j] = __uint_as_float((uint32_t)w[q][j]);
+                for (int j = 0; j < 8; ++j) h.v[j] = __uint_as_float((uint32_t)w[q][j / 4][j % 4] ^ kHandoffXor);
                 const float scale = fp8_group_scale(row_max(absmax8(h, B == 0 ? a.status : nullptr)));
                 *(uint64_t*)&s.h.q[p * I + g * 128 + col * 8] = encode8(h, scale);
                 if (col == 0) s.h.s[u] = scale;
@@ -693,12 +733,21 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 for (int i = 0; i < kChunk; ++i)
                     dq[i] = mfma_w<WF>(ar >= 0 ? a_operand<WF>(af[i]) : zero8i,
                                        live_col ? db[k0 + i] : zero_wraw<WF>(), zero);
+                // the block chain by selects, not branches: a branch per block
+                // pulls each MFMA into its block and serializes them (kept where
+                // the grouped MFMAs do not fit the registers: 6-bit blocks are
+                // two MFMAs each, and I > 768 holds more rows)
+                constexpr bool kSelects = WF != kWfInt6 && KBJ <= 6;
 #pragma unroll
                 for (int i = 0; i < kChunk; ++i) {
-                    if (k0 + i < KBd) {
+                    const bool in = k0 + i < KBd;
+                    if constexpr (!kSelects) {
+                        if (!in) continue;
+                    }
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[r] = fmaf(dq[i][r] * (crow[r] >= 0 ? sh[i][r] : 0.0f), dsw[k0 + i], acc[r]);
+                    for (int r = 0; r < 4; ++r) {
+                        const float t = fmaf(dq[i][r] * (crow[r] >= 0 ? sh[i][r] : 0.0f), dsw[k0 + i], acc[r]);
+                        acc[r] = in ? t : acc[r];
                     }
                 }
             }

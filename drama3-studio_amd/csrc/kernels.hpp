@@ -219,7 +219,7 @@ struct FusedDecodeArgs {
     int64_t xq_row_stride, xs_row_stride;
     int rows, x_group;
     int gu_dtype;
-    uint64_t* ht;               // [pairs, I] hand-off words: fp32 h bits | call epoch << 32
+    uint32_t* ht;               // 2 hand-off buffers of kHandoffWords: fp32 h bits ^ kHandoffXor, 0 = not ready
     int* sync;                  // 32 64-bit call counters, 256 bytes apart, zero at first use
     void* out;                  // [pairs / top_k, H] layer output ...
     int out_dtype;
@@ -227,7 +227,7 @@ struct FusedDecodeArgs {
     float* out_pairs;           // ... or [pairs, H] ordered fp32 partials when non-null
     int* status;
     uint64_t spin_ticks;        // bound of the hand-off wait (100 MHz ticks) before kSyncTimeout
-    uint32_t tag_skew;          // 0; 1 makes readers wait for a tag no producer writes (diagnostic)
+    uint32_t tag_skew;          // 0; 1 makes readers treat every word as not ready (diagnostic)
     uint64_t* phase_times;      // null; else [grid, kFusedPhases] real-time stamps per workgroup (diagnostic)
     int64_t phase_entries;      // entries of phase_times
 };

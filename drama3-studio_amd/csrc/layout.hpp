@@ -10,11 +10,14 @@
 //   call counters     kEpochSlots 64-bit counters, kEpochStride bytes apart,
 //                     of the single-launch decode; they only grow (a call's
 //                     epoch is derived from them);
-//   hand-off words    [kFusedMaxPairs * kFusedMaxI] uint64 of the
-//                     single-launch decode: fp32 h bits | call epoch << 32.
+//   hand-off words    2 x [kFusedMaxPairs * kFusedMaxI] uint32 of the
+//                     single-launch decode: buffer (call epoch & 1) holds
+//                     this call's h values (fp32 bits ^ kHandoffXor, so a
+//                     ready word is never 0); the call zero-fills the other
+//                     buffer for the next one.
 // Only the decode kernels touch the head.  A hand-off word is accepted when
-// it carries the current call's epoch, so no other region may ever alias it:
-// values written there by another path could look like a tag.
+// it is non-zero, so no other region may ever alias it: values written there
+// by another path would look ready.
 #pragma once
 
 #include <stddef.h>
@@ -28,7 +31,8 @@ constexpr int kEpochSlots = 32;     // call counters, spread over memory channel
 constexpr int kEpochStride = 256;   // bytes between two call counters
 constexpr size_t kArrivalBytes = (size_t)kMaxDecodePairs * (kMaxInter / 128) * 4;
 constexpr size_t kEpochBytes = (size_t)kEpochSlots * kEpochStride;
-constexpr size_t kHandoffBytes = (size_t)kFusedMaxPairs * kFusedMaxI * 8;
+constexpr int kHandoffWords = kFusedMaxPairs * kFusedMaxI;  // words of one hand-off buffer
+constexpr size_t kHandoffBytes = 2 * (size_t)kHandoffWords * 4;
 
 // A named byte range of a workspace.
 struct Region {
@@ -65,14 +69,14 @@ class Carver {
 struct Head {
     int* arrival;
     int* epochs;
-    uint64_t* handoff;
+    uint32_t* handoff;
 };
 
 inline Head carve_head(Carver& c) {
     Head h{};
     h.arrival = c.take<int>("arrival counters", kArrivalBytes);
     h.epochs = c.take<int>("call counters", kEpochBytes);
-    h.handoff = c.take<uint64_t>("hand-off words", kHandoffBytes);
+    h.handoff = c.take<uint32_t>("hand-off words", kHandoffBytes);
     return h;
 }
 
