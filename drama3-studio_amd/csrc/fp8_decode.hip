@@ -71,6 +71,7 @@ __device__ int wave_pairs_of_words(const uint32_t (&mw)[kMaxDecodePairs / 32], i
 // ---------------------------------------------------------------- gate / up
 
 struct GateUpLds {
+    alignas(16) v4i stage[kUpWaves][2][128];    // each wave's gate / up block on its way into the MFMA layout
     int rows[kUpWaves][kMaxDecodePairs];        // each wave's copy of the expert's pairs
     float red[kUpWaves][kWave][8];              // cross-wave gate/up reduction
     int last;
@@ -108,6 +109,9 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
     asm volatile("" ::: "memory");
     const uint8_t* wg = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)(n0 + col) * a.w13.w_sn;
     const uint8_t* wu = wg + (int64_t)I * a.w13.w_sn;
+    const uint8_t* g0 = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)n0 * a.w13.w_sn;  // the tile's first gate row
+    const uint8_t* u0 = g0 + (int64_t)I * a.w13.w_sn;
+    const int64_t r8 = 8 * a.w13.w_sn;
     WRaw<WF> bg[KBW], bu[KBW];
     float swg[KBW], swu[KBW];
 #pragma unroll
@@ -116,8 +120,13 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
         bg[i] = bu[i] = zero_wraw<WF>();  // blocks past K: defined operands, masked at use
         swg[i] = swu[i] = 0.0f;
         if (kb < KB) {
-            bg[i] = load_wraw<WF>(wg, H, kb, grp);
-            bu[i] = load_wraw<WF>(wu, H, kb, grp);
+            if constexpr (WF == kWfFp8) {  // whole 128-byte row segments; into the MFMA layout below
+                bg[i].v = load_block_linear(g0, g0 + r8, a.w13.w_sn, kb * 128);
+                bu[i].v = load_block_linear(u0, u0 + r8, a.w13.w_sn, kb * 128);
+            } else {
+                bg[i] = load_wraw<WF>(wg, H, kb, grp);
+                bu[i] = load_wraw<WF>(wu, H, kb, grp);
+            }
             swg[i] = proj_scale<WF>(a.w13, e, n0 + col, kb);
             swu[i] = proj_scale<WF>(a.w13, e, I + n0 + col, kb);
         }
@@ -152,6 +161,13 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
     v8i af[KBW];
     float sx[KBW][4];
     load_a(0, min(kRowsPerPass, M), af, sx);
+    if constexpr (WF == kWfFp8) {  // linearly loaded blocks into the MFMA layout, once for every pass
+#pragma unroll
+        for (int i = 0; i < KBW; ++i) {
+            bg[i].v = stage_block(bg[i].v, s.stage[wave][0]);
+            bu[i].v = stage_block(bu[i].v, s.stage[wave][1]);
+        }
+    }
 
     for (int m0 = 0; m0 < M; m0 += kRowsPerPass) {
         const int mc = min(kRowsPerPass, M - m0);
@@ -220,6 +236,7 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
 // ---------------------------------------------------------------------- down
 
 struct DownLds {
+    alignas(16) v4i stage[kDnMaxWaves][2][128];  // each wave's weight blocks on their way into the MFMA layout
     float wt[kMaxDecodePairs];                  // route weights of all pairs, fp32
     int rows[kDnMaxWaves][2][kMaxDecodePairs];  // pairs of the wave's two experts
     float part[kMaxDecodePairs][8];
@@ -252,9 +269,17 @@ __device__ __forceinline__ void load_down_batch(const DownArgs& a, int num_activ
     const int e = ai >= 0 ? a.grouping->expert[ai] : -1;
     const int n = n0 + (col & 7);
     const uint8_t* wrow = a.w2.w + (int64_t)(e < 0 ? 0 : e) * a.w2.w_se + (int64_t)n * a.w2.w_sn;
+    // FP8: rows n0.. of the first expert, then of the second (the first again
+    // when there is none: zeroed after staging), whole 128-byte row segments
+    const int e0 = a.grouping->expert[bt.ai0], e1 = bt.ai1 >= 0 ? a.grouping->expert[bt.ai1] : e0;
+    const uint8_t* lo = a.w2.w + (int64_t)e0 * a.w2.w_se + (int64_t)n0 * a.w2.w_sn;
+    const uint8_t* hi = a.w2.w + (int64_t)e1 * a.w2.w_se + (int64_t)n0 * a.w2.w_sn;
 #pragma unroll
     for (int kb = 0; kb < KB2; ++kb) {
-        bt.b[kb] = (e >= 0 && kb < KB) ? load_wraw<WF>(wrow, a.w2.K, kb, grp) : zero_wraw<WF>();
+        if constexpr (WF == kWfFp8)
+            bt.b[kb].v = kb < KB ? load_block_linear(lo, hi, a.w2.w_sn, kb * 128) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+        else
+            bt.b[kb] = (e >= 0 && kb < KB) ? load_wraw<WF>(wrow, a.w2.K, kb, grp) : zero_wraw<WF>();
         bt.sw[kb] = (e >= 0 && kb < KB) ? proj_scale<WF>(a.w2, e, n, kb) : 0.0f;
     }
 }
@@ -336,6 +361,14 @@ __global__ __launch_bounds__(dn_waves(WF, KB2) * kWave) void fp8_down_decode_ker
         DownBatch<WF, KB2> nxt;
         const bool more = bi + kDnWaves < batches;
         if (more) load_down_batch<WF, KB2>(a, num_active, bi + kDnWaves, n0, col, grp, KB, nxt);
+        if constexpr (WF == kWfFp8) {  // this batch's linearly loaded blocks into the MFMA layout
+            const bool live = col < 8 || cur.ai1 >= 0;
+#pragma unroll
+            for (int kb = 0; kb < KB2; ++kb) {
+                const v8i b = stage_block(cur.b[kb].v, s.stage[wave][kb & 1]);
+                cur.b[kb].v = live ? b : zero8i;
+            }
+        }
         for (int pass = 0; pass < passes; ++pass) {
             if (pass > 0) {
                 const int ar = a_row(pass, col);

@@ -91,6 +91,7 @@ struct FzLds {
         alignas(16) uint8_t q[kFusedHBytes];                     // FP8 hidden [pairs, I]
         float s[kFusedHBytes / 128];                             // its scale per (pair, 128-group)
     } h;
+    alignas(16) v4i stage[kFzWaves][2][128];  // each wave's two 2 KB slots: FP8 blocks into the MFMA layout
     union alignas(16) {
         float red[kMaxUnitDepth][kFzWaves][kWave][4];            // gate/up per-wave partials
         float part[kFusedMaxPairs][kTileRows];                   // down projection of each pair
@@ -429,10 +430,14 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         const int e = active_of(real ? ai : num_active);
         const int n = col < 8 ? c0 + col : I + c0 + col - 8;
         const uint8_t* wrow = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)n * a.w13.w_sn;
+        const uint8_t* gate0 = a.w13.w + (int64_t)e * a.w13.w_se + (int64_t)c0 * a.w13.w_sn;
 #pragma unroll
         for (int i = 0; i < KBW; ++i) {
             const int kb = min(wave + i * kFzWaves, KB - 1);
-            ub[slot][i] = load_wraw<WF>(wrow, H, kb, grp);
+            if constexpr (WF == kWfFp8)  // gate rows c0.. then up rows I + c0.., staged at use
+                ub[slot][i].v = load_block_linear(gate0, gate0 + (int64_t)I * a.w13.w_sn, a.w13.w_sn, kb * 128);
+            else
+                ub[slot][i] = load_wraw<WF>(wrow, H, kb, grp);
             us[slot][i] = proj_scale<WF>(a.w13, e, n, kb);
         }
     };
@@ -452,10 +457,15 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         const int e = col >= 8 ? e1 : e0;
         const int n = min(rt, tiles - 1) * kTileRows + (col & 7);
         const uint8_t* wrow = a.w2.w + (int64_t)e * a.w2.w_se + (int64_t)n * a.w2.w_sn;
+        const int64_t r0 = (int64_t)min(rt, tiles - 1) * kTileRows * a.w2.w_sn;
 #pragma unroll
         for (int kb = 0; kb < KBJ; ++kb) {
             const int kbc = min(kb, KBd - 1);
-            db[kb] = load_wraw<WF>(wrow, I, kbc, grp);
+            if constexpr (WF == kWfFp8)  // expert 2 j's rows, then 2 j + 1's, staged at use
+                db[kb].v = load_block_linear(a.w2.w + (int64_t)e0 * a.w2.w_se + r0, a.w2.w + (int64_t)e1 * a.w2.w_se + r0,
+                                             a.w2.w_sn, kbc * 128);
+            else
+                db[kb] = load_wraw<WF>(wrow, I, kbc, grp);
             dsw[kb] = proj_scale<WF>(a.w2, e, n, kbc);
         }
     };
@@ -534,7 +544,9 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                     const bool in = kb < KB;
                     const int kbc = min(kb, KB - 1);
                     const v8i ar = a_operand<WF>(lds32(&s.xq[arow * H + kbc * 128 + grp * 32]));
-                    const v4f dq = mfma_w<WF>(live ? ar : zero8i, ub[d][i], zero);
+                    WRaw<WF> wb = ub[d][i];
+                    if constexpr (WF == kWfFp8) wb.v = stage_block(wb.v, s.stage[wave][(d * KBW + i) & 1]);
+                    const v4f dq = mfma_w<WF>(live ? ar : zero8i, wb, zero);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float sx = cl[r] ? s.xs[crow[r] * gpr + kbc] : 0.0f;
@@ -730,9 +742,11 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 }
                 v4f dq[kChunk];
 #pragma unroll
-                for (int i = 0; i < kChunk; ++i)
-                    dq[i] = mfma_w<WF>(ar >= 0 ? a_operand<WF>(af[i]) : zero8i,
-                                       live_col ? db[k0 + i] : zero_wraw<WF>(), zero);
+                for (int i = 0; i < kChunk; ++i) {
+                    WRaw<WF> wb = db[k0 + i];
+                    if constexpr (WF == kWfFp8) wb.v = stage_block(wb.v, s.stage[wave][(k0 + i) & 1]);
+                    dq[i] = mfma_w<WF>(ar >= 0 ? a_operand<WF>(af[i]) : zero8i, live_col ? wb : zero_wraw<WF>(), zero);
+                }
                 // the block chain by selects, not branches: a branch per block
                 // pulls each MFMA into its block and serializes them (kept where
                 // the grouped MFMAs do not fit the registers: 6-bit blocks are

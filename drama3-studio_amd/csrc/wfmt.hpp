@@ -60,6 +60,37 @@ __device__ __forceinline__ WRaw<WF> load_wraw(const uint8_t* row, int K, int kb,
     return r;
 }
 
+// One 16-row x 128-byte FP8 weight block, rows 0..7 from lo_row and 8..15
+// from hi_row (`stride` bytes apart), bytes off .. off + 127, loaded
+// linearly: load h, lane l reads row 8 h + l / 8, bytes 16 (l % 8) .. + 15,
+// so each load covers 8 whole 128-byte row segments.  (A load in the MFMA
+// operand layout half-covers 16 rows; a single pass over weights in that
+// layout was measured about a fifth slower.)  Non-temporal: read once.
+__device__ __forceinline__ v8i load_block_linear(const uint8_t* lo_row, const uint8_t* hi_row, int64_t stride,
+                                                 int off) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t o = (int64_t)(lane / 8) * stride + off + (lane % 8) * 16;
+    const v4i lo = __builtin_nontemporal_load((const v4i*)(lo_row + o));
+    const v4i hi = __builtin_nontemporal_load((const v4i*)(hi_row + o));
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// A linearly loaded block into the MFMA operand layout (lane (col, grp):
+// row col, bytes 32 grp .. + 31) through a 2 KB LDS slot of the wave: the
+// 16-byte chunk c of row r sits at chunk c ^ (r % 8), so neither the writes
+// nor the reads share banks.  The wave's LDS operations run in issue order;
+// the empty asm statements keep the compiler from reordering them.
+__device__ __forceinline__ v8i stage_block(const v8i& raw, v4i* slot) {
+    const int lane = threadIdx.x % kWave, r = lane / 8, j = lane % 8, col = lane % 16, grp = lane / 16;
+    asm volatile("" ::: "memory");
+    slot[r * 8 + (j ^ r)] = v4i{raw[0], raw[1], raw[2], raw[3]};
+    slot[(r + 8) * 8 + (j ^ r)] = v4i{raw[4], raw[5], raw[6], raw[7]};
+    asm volatile("" ::: "memory");
+    const v4i a0 = slot[col * 8 + ((2 * grp) ^ (col % 8))], a1 = slot[col * 8 + ((2 * grp + 1) ^ (col % 8))];
+    asm volatile("" ::: "memory");
+    return v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+}
+
 template <int WF>
 __device__ __forceinline__ WRaw<WF> zero_wraw() {
     WRaw<WF> r;
