@@ -110,9 +110,12 @@ DMOE_API int dmoe_debug_force_sync_timeout(int force);
 
 /* Diagnostic phase timing of the single-launch FP8 decode (default off, null
  * buffer).  While `buffer` (device, `entries` 64-bit words) is set, FP8
- * single-launch decodes launched -- or captured -- from then on run a timing
- * instance of the kernel whose thread 0 of every workgroup w stores the GPU's
- * 100 MHz real-time counter at phase k into buffer[7 w + k]: 0 entry, 1 routed,
+ * single-launch decodes launched -- or captured -- from then on that route
+ * from logits (at most 128 experts, top_k <= 8), take bf16 / fp16 activation
+ * rows with 128-group scales and write the layer output run a timing instance
+ * of the kernel whose thread 0 of every workgroup w records the GPU's 100 MHz
+ * real-time counter at phase k and stores it, when the workgroup ends, into
+ * buffer[7 w + k]: 0 entry, 1 routed,
  * 2 weight loads issued, 3 first gate/up batch published, 4 gate/up done,
  * 5 hidden ready (the hand-off wait ended), 6 down done.  A buffer with fewer
  * than 7 entries per workgroup (one workgroup per CU) leaves the ordinary
