@@ -148,10 +148,10 @@ __device__ __forceinline__ void wave_route_load(const RouteSource& src, int t, i
 // runs the whole K chain of a down job, as the three-launch decode does.
 // LEAN: the layer call every decode step makes, compiled alone (lean_call):
 // routing from logits with E <= 128 and top_k <= 8, 16-bit activation rows
-// quantized per 128-group here, the layer output.  Other calls take the
-// general instance.  The lean code is about a third smaller, and the kernel
-// runs measurably faster when less of its code competes for the instruction
-// cache.
+// quantized here (128-group or per-token scales), the layer output.  Other
+// calls take the general instance.  Without the paths this call never takes
+// (other routers, fp32 or caller-quantized activations, per-pair outputs) the
+// kernel was measured 1 us faster per 1-token layer, outputs unchanged.
 // TIMES: the diagnostic instance that stamps the 100 MHz real-time counter at
 // each phase (thread 0 of every workgroup, into a.phase_times).
 template <int WF, int KBW, int KBJ, bool LEAN, bool TIMES = false>
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         if (u < xunits) {
             const F8 v = unpack8(xr[q][0], !LEAN && a.x_dtype == kF32 ? xr[q][1] : xr[q][0], a.x_dtype);
             xamax[q] = row_max(absmax8(v, B == 0 ? a.status : nullptr));
-            if (LEAN || a.x_group == 128) {
+            if (a.x_group == 128) {
                 const float scale = fp8_group_scale(xamax[q]);
                 *(uint64_t*)&s.xq[(u / gpr) * H + (u % gpr) * 128 + col * 8] = encode8(v, scale);
                 if (col == 0) s.xs[u] = scale;
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             dsw[kb] = proj_scale<WF>(a.w2, e, n, kbc);
         }
     };
-    if (!LEAN && a.x_group != 128) {  // per-row scale: the maximum of the row's group maxima
+    if (a.x_group != 128) {  // per-row scale: the maximum of the row's group maxima
 #pragma unroll
         for (int q = 0; q < kQuantPerGroup; ++q) {
             const int u = qgroup + q * (kFzThreads / 16);
@@ -831,7 +831,7 @@ namespace {
 // The call the lean instance is compiled for (see the kernel's LEAN).
 inline bool lean_call(const FusedDecodeArgs& a) {
     return a.route.logits != nullptr && a.experts <= 2 * kWave && a.route.top_k <= 8 && a.xq == nullptr &&
-           (a.x_dtype == kBF16 || a.x_dtype == kF16) && a.x_group == 128 && a.out_pairs == nullptr;
+           (a.x_dtype == kBF16 || a.x_dtype == kF16) && a.out_pairs == nullptr;
 }
 
 template <int WF, int KBW, int KBJ, bool LEAN>
