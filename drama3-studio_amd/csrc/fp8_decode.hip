@@ -71,17 +71,18 @@ __device__ int wave_pairs_of_words(const uint32_t (&mw)[kMaxDecodePairs / 32], i
 // ---------------------------------------------------------------- gate / up
 
 struct GateUpLds {
-    alignas(16) v4i stage[kUpWaves][2][128];    // each wave's gate / up block on its way into the MFMA layout
+    alignas(16) v4i stage[kUpWaves][128];       // each wave's gate / up block on its way into the MFMA layout
     int rows[kUpWaves][kMaxDecodePairs];        // each wave's copy of the expert's pairs
     float red[kUpWaves][kWave][8];              // cross-wave gate/up reduction
     int last;
 };
 
 // WF = weight format (wfmt.hpp); KBW = 128-column K blocks per wave
-// (H <= 8 * 128 * KBW).  Occupancy target: 4 workgroups per CU, 2 for larger
-// K or 6-bit weights (their expansion needs the registers).
+// (H <= 8 * 128 * KBW).  Occupancy target: 3 workgroups per CU (6 waves per
+// SIMD: at most 80 registers), 2 for larger K or 6-bit weights (their
+// expansion needs the registers).
 template <int WF, int KBW>
-__global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) void fp8_gateup_decode_kernel(
+__global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 6 : 2)) void fp8_gateup_decode_kernel(
     GateUpArgs a) {
     __shared__ GateUpLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -164,8 +165,8 @@ __global__ __launch_bounds__(kUpThreads, (KBW <= 2 && WF != kWfInt6 ? 4 : 2)) vo
     if constexpr (WF == kWfFp8) {  // linearly loaded blocks into the MFMA layout, once for every pass
 #pragma unroll
         for (int i = 0; i < KBW; ++i) {
-            bg[i].v = stage_block(bg[i].v, s.stage[wave][0]);
-            bu[i].v = stage_block(bu[i].v, s.stage[wave][1]);
+            bg[i].v = stage_block(bg[i].v, s.stage[wave]);
+            bu[i].v = stage_block(bu[i].v, s.stage[wave]);
         }
     }
 
