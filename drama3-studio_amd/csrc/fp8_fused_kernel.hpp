@@ -579,8 +579,10 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             lds_barrier();
             epoch = s.epoch;
             {
-                const int d = tid / (16 * kUnitCols), m = (tid / kUnitCols) % 16, c = tid % kUnitCols;
-                if (d < kUnitDepth && j0 + d < my_units && pass * 16 + m < s.ucoord[d][2]) {
+                // thread (m, d, c): row-major over the units' rows, so a call
+                // with few pairs per unit publishes from wave 0 alone
+                const int d = (tid / kUnitCols) % kUnitDepth, m = tid / (kUnitCols * kUnitDepth), c = tid % kUnitCols;
+                if (m < 16 && j0 + d < my_units && pass * 16 + m < s.ucoord[d][2]) {
                     const int c0 = s.ucoord[d][0];
                     const int gl = (m / 4) * 16 + c, ul = gl + 8, r = m % 4;
                     float g = s.v.red[d][0][gl][r], up = s.v.red[d][0][ul][r];
@@ -657,58 +659,66 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     }
 
     // ---------------------------------------- hidden: wait + quantize
-    // One (pair, 128-group) per 16 lanes, two groups per lane in flight.
-    // Column 8 a + b of a group is stored at word 64 (b / 4) + 4 a + b % 4,
-    // so lane `col` finds its columns 8 col + 4 i .. + 3 at words 64 i +
-    // 4 col: each 16-byte load of the 16 lanes reads 256 contiguous bytes,
-    // and each lane ends with its 8 consecutive columns (one producer unit).
-    constexpr int kHUnits = kFzThreads / 16;
+    // One (pair, 128-group) unit per 16 lanes.  Column 8 a + b of a group is
+    // stored at word 64 (b / 4) + 4 a + b % 4, so lane `col` finds its
+    // columns 8 col + 4 i .. + 3 at words 64 i + 4 col: each 16-byte load of
+    // the 16 lanes reads 256 contiguous bytes, and each lane ends with its 8
+    // consecutive columns (one producer unit).  Two units per 16 lanes per
+    // round: units u0 + q kHGroups + (tid / 16), q < 2.  (A wave with a down
+    // job sees its polls return behind its down rows, which its MFMAs wait
+    // for anyway; the waves without one poll with nothing else outstanding.)
+    constexpr int kHGroups = kFzThreads / 16, UPG = 2;
     const __amdgpu_buffer_rsrc_t hbuf = handoff_buffer(a.ht + (int64_t)(epoch & 1) * kHandoffWords);
-    for (int u0 = 0; u0 < P * KBd; u0 += 2 * kHUnits) {
-        v4i w[2][2];
-        bool want[2];
-        int hoff[2];  // byte offset of the lane's first word
+    for (int u0 = 0; u0 < P * KBd; u0 += UPG * kHGroups) {
+        v4i w[UPG][2];
+        bool want[UPG];
+        int hoff[UPG];  // byte offset of the lane's first word
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int u = u0 + q * kHUnits + tid / 16;
+        for (int q = 0; q < UPG; ++q) {
+            const int u = u0 + q * kHGroups + tid / 16;
             want[q] = u < P * KBd && s.sid[min(u, P * KBd - 1) / KBd] >= 0;
             hoff[q] = ((want[q] ? u / KBd : 0) * I + (want[q] ? u % KBd : 0) * 128 + 4 * col) * 4;
         }
         // a word is ready once non-zero (tag_skew = 1 only in the diagnostic
         // mode that forces every wait to run to its bound)
         const bool skew = a.tag_skew != 0;
-        auto ok = [&](int q, v4i v) { return !want[q] || (!skew && v[0] != 0 && v[1] != 0 && v[2] != 0 && v[3] != 0); };
+        // (bitwise, not short-circuit: every word is checked, so no path
+        // leaves a load unwaited for the compiler to wait on later)
+        auto ok = [&](int q, v4i v) {
+            return !want[q] | (!skew & (v[0] != 0) & (v[1] != 0) & (v[2] != 0) & (v[3] != 0));
+        };
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         bool timed_out = false;
-        // all four 16-byte loads at once (one round trip when the producers
-        // are done), then re-read only the ones still holding a cleared word
+        // every 16-byte word of the round read at once, then all of them again
+        // until all are ready: one round trip per try (a lane without a unit
+        // reads its clamped offset and ignores it; a ready word stays ready)
+        auto read_all = [&]() {
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+            for (int q = 0; q < UPG; ++q)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) w[q][i] = want[q] ? load_handoff16(hbuf, hoff[q] + 256 * i) : zero4i;
-        bool ready = true;
+                for (int i = 0; i < 2; ++i) w[q][i] = load_handoff16(hbuf, hoff[q] + 256 * i);
+        };
+        auto all_ok = [&]() {
+            bool r = true;
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+            for (int q = 0; q < UPG; ++q)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) ready = ready && ok(q, w[q][i]);
+                for (int i = 0; i < 2; ++i) r = r & ok(q, w[q][i]);
+            return __builtin_amdgcn_ballot_w64(!r) == 0;  // the wave's branch, uniform
+        };
+        read_all();
+        bool ready = all_ok();
         while (!ready && !timed_out) {
             __builtin_amdgcn_s_sleep(1);
-            ready = true;
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    if (!ok(q, w[q][i])) w[q][i] = load_handoff16(hbuf, hoff[q] + 256 * i);
-                    ready = ready && ok(q, w[q][i]);
-                }
-            }
+            read_all();
+            ready = all_ok();
             timed_out = __builtin_amdgcn_s_memrealtime() - t0 > a.spin_ticks;
         }
         if (timed_out) raise_status(a.status, kSyncTimeout);
         if (u0 == 0) stamp(5);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int u = u0 + q * kHUnits + tid / 16;
+        for (int q = 0; q < UPG; ++q) {
+            const int u = u0 + q * kHGroups + tid / 16;
             if (want[q]) {
                 const int p = u / KBd, g = u % KBd;
                 F8 h;
