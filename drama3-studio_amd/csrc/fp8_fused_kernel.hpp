@@ -179,7 +179,6 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     const int P = a.pairs, E = a.experts, G = gridDim.x, B = blockIdx.x;
     const int gpr = H / 128;
     const v4f zero = {0, 0, 0, 0};
-    const v8i zero8i = {0, 0, 0, 0, 0, 0, 0, 0};
 
     // ------------------------------------------------ phase 0: entry loads
     // Everything the first phase reads goes out together: this workgroup's
@@ -538,18 +537,16 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
         auto run_pass = [&](int pass) {
 #pragma unroll
             for (int d = 0; d < kUnitDepth; ++d) {
-                // branch-free operand reads (clamped rows, values selected after the read)
+                // branch-free operand reads from clamped rows: a row past
+                // the unit's pairs multiplies a real pair's values, and its
+                // result is never read (the reducers take rows < the pair
+                // count), so no select masks it
                 const int* pr = s.prow + ust[d] + pass * 16;
                 const int mc = min(16, um[d] - pass * 16);
-                const bool live = col < mc;
                 const int arow = pr[min(col, max(mc - 1, 0))];
-                bool cl[4];
                 int crow[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    cl[r] = grp * 4 + r < mc;
-                    crow[r] = pr[min(grp * 4 + r, max(mc - 1, 0))];
-                }
+                for (int r = 0; r < 4; ++r) crow[r] = pr[min(grp * 4 + r, max(mc - 1, 0))];
                 v4f acc = zero;
 #pragma unroll
                 for (int i = 0; i < KBW; ++i) {
@@ -561,10 +558,10 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                     const v8i ar = a_operand<WF>(lds32(&s.xq[arow * H + kbc * 128 + grp * 32]));
                     WRaw<WF> wb = ub[d][i];
                     if constexpr (WF == kWfFp8) wb.v = stage_block(wb.v, s.stage[wave][(d * KBW + i) & 1]);
-                    const v4f dq = mfma_w<WF>(live ? ar : zero8i, wb, zero);
+                    const v4f dq = mfma_w<WF>(ar, wb, zero);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float sx = cl[r] ? s.xs[crow[r] * gpr + kbc] : 0.0f;
+                        const float sx = s.xs[crow[r] * gpr + kbc];
                         const float t = fmaf(dq[r] * sx, us[d][i], acc[r]);
                         acc[r] = in ? t : acc[r];
                     }
@@ -734,7 +731,6 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     // ------------------------------------------------- down + combine
     auto compute_job = [&](int j) {
         const int ai0 = 2 * j, ai1 = 2 * j + 1;
-        const bool live_col = (col < 8 ? ai0 : ai1) < num_active;
         const int M0 = s.start[ai0 + 1] - s.start[ai0];
         const int M1 = ai1 < num_active ? s.start[ai1 + 1] - s.start[ai1] : 0;
         const int passes = (max(M0, M1) + 7) / 8;
@@ -749,7 +745,11 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                               : ((m < 8) == (col < 8)) ? a_pair(m < 8 ? ai0 : ai1, pass * 8 + (m & 7)) : -1;
             }
             // branch-free operand reads: every LDS read issued up front, the
-            // MFMAs back to back, then the per-block fma chain in block order
+            // MFMAs back to back, then the per-block fma chain in block order.
+            // Operands are not masked: a row without a pair reads pair 0's
+            // hidden row, columns of a missing expert hold expert 0's weights
+            // (all finite), and the results of those rows and columns, like
+            // the off-diagonal blocks, are never stored (crow < 0).
             const int arc = max(ar, 0);
             int crc[4];
 #pragma unroll
@@ -773,7 +773,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 for (int i = 0; i < kChunk; ++i) {
                     WRaw<WF> wb = db[k0 + i];
                     if constexpr (WF == kWfFp8) wb.v = stage_block(wb.v, s.stage[wave][(k0 + i) & 1]);
-                    dq[i] = mfma_w<WF>(ar >= 0 ? a_operand<WF>(af[i]) : zero8i, live_col ? wb : zero_wraw<WF>(), zero);
+                    dq[i] = mfma_w<WF>(a_operand<WF>(af[i]), wb, zero);
                 }
                 // the block chain by selects, not branches: a branch per block
                 // pulls each MFMA into its block and serializes them (kept where
@@ -788,7 +788,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float t = fmaf(dq[i][r] * (crow[r] >= 0 ? sh[i][r] : 0.0f), dsw[k0 + i], acc[r]);
+                        const float t = fmaf(dq[i][r] * sh[i][r], dsw[k0 + i], acc[r]);
                         acc[r] = in ? t : acc[r];
                     }
                 }
