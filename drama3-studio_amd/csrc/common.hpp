@@ -70,6 +70,26 @@ __device__ __forceinline__ int64_t load_id(const void* p, int64_t i, int dtype) 
     return dtype == kI64 ? ((const int64_t*)p)[i] : (int64_t)((const int32_t*)p)[i];
 }
 
+// v / scale correctly rounded, from y = RN(1 / scale) (one true division per
+// group instead of one per value): q0 = RN(v y), then twice the residual
+// correction q <- RN(q + r y) with r = v - q scale formed exactly by an fma.
+// The first correction leaves q within one ulp of v / scale; from there, with
+// y correctly rounded, the second gives the correctly rounded quotient
+// (Markstein's theorem, as in the IA-64 division sequences).  Needs scale
+// and 1 / scale normal (an FP8 group scale lies in [1e-10 / 448, FLT_MAX /
+// 448], an INT8 row scale in [1e-12 / 127, FLT_MAX / 127]); quotients below
+// 2^-126 may differ from the true division in their last bits but are far
+// below the smallest E4M3 subnormal and below 1/2, so the encoded byte is the
+// same.  Only a zero quotient can carry the wrong sign (v = -0 gives
+// +0): callers take the sign from v.  A NaN v gives a NaN, as the division
+// does; an infinite scale (a group holding an inf) gives NaN where the
+// division gives 0 (the INT8 quantizers divide such rows truly).
+__device__ __forceinline__ float quotient_by_scale(float v, float scale, float y) {
+    const float q0 = __fmul_rn(v, y);
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, scale, v), y, q0);
+    return __builtin_fmaf(__builtin_fmaf(-q1, scale, v), y, q1);
+}
+
 // OCP E4M3 (finite "fn" variant) encode: saturate to +-448, round to nearest
 // even.  Normal range: drop 20 fp32 mantissa bits with ties-to-even and
 // rebias 127 -> 7.  Subnormal range (|v| < 2^-6): RNE of |v| * 2^9.

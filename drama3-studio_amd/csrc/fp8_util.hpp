@@ -79,29 +79,16 @@ __device__ __forceinline__ F8 load8(const void* x, int64_t i, int dtype) {
     return unpack8(w, w, dtype);
 }
 
-// v / scale correctly rounded, from y = RN(1 / scale) (one true division per
-// group instead of one per value): q0 = RN(v y), then twice the residual
-// correction q <- RN(q + r y) with r = v - q scale formed exactly by an fma.
-// The first correction leaves q within one ulp of v / scale; from there, with
-// y correctly rounded, the second gives the correctly rounded quotient
-// (Markstein's theorem, as in the IA-64 division sequences).  Needs scale
-// and 1 / scale normal (a group scale lies in [1e-10 / 448, FLT_MAX / 448]);
-// quotients below 2^-126 may differ from the true division in their last
-// bits but are far below the smallest E4M3 subnormal, so the encoded byte is
-// the same.  Only a zero quotient can carry the wrong sign (v = -0 gives
-// +0): callers take the sign from v.
-__device__ __forceinline__ float quotient_by_scale(float v, float scale, float y) {
-    const float q0 = __fmul_rn(v, y);
-    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, scale, v), y, q0);
-    return __builtin_fmaf(__builtin_fmaf(-q1, scale, v), y, q1);
-}
-
 // E4M3 bytes of v / scale (correctly rounded quotient), packed little-endian:
 // |v / scale| saturated to 448 (NaN -> 448 with its sign, as fp8_encode does),
 // then the hardware round-to-nearest-even conversion, which equals fp8_encode
 // for every fp32 value of magnitude <= 448 (the device FP8 tie tests pin it).
 __device__ __forceinline__ float fp8_saturate(float v) { return copysignf(fminf(fabsf(v), 448.0f), v); }
 
+// A group holding an inf (infinite scale, DMOE_STATUS_NON_FINITE raised by
+// absmax8) encodes its finite values as 448 with their sign where the true
+// division gives 0: the outputs after that status are unspecified, and the
+// fast path carries no branch for it.
 __device__ __forceinline__ uint64_t encode8(const F8& x, float scale) {
     const float y = 1.0f / scale;
     float q[8];

@@ -137,9 +137,11 @@ __device__ __forceinline__ void rotate_blocks(const float (&in)[N][4], float (&v
     }
 }
 
-// INT8 of one rotated value: clamp(rint(v / s), +-127).
-__device__ __forceinline__ uint32_t quant_byte(float v, float sc) {
-    const float t = fminf(fmaxf(__builtin_rintf(v / sc), -127.0f), 127.0f);
+// INT8 of one rotated value: clamp(rint(v / s), +-127).  With a finite row
+// scale the quotient comes from the row's y = RN(1 / s) (quotient_by_scale:
+// the IEEE quotient bit for bit); a row holding an inf divides truly.
+__device__ __forceinline__ uint32_t quant_byte(float q) {
+    const float t = fminf(fmaxf(__builtin_rintf(q), -127.0f), 127.0f);
     return (uint32_t)(uint8_t)(int8_t)(int)t;
 }
 
@@ -172,14 +174,16 @@ __global__ __launch_bounds__(256) void rotate_quant_kernel(RotateArgs a) {
     if (lane == 0) red[wave] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float sc = fmaxf(amax, 1e-12f) / 127.0f;
+    const float sc = fmaxf(amax, 1e-12f) / 127.0f, y = 1.0f / sc;
+    const bool fast = __builtin_isfinite(sc);
 #pragma unroll
     for (int b = 0; b < kBlocksPerWave; ++b) {
         const int c = wave + 4 * b;
         if (c >= chunks) continue;
         uint32_t packed = 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) packed |= quant_byte(v[b][r], sc) << (8 * r);
+        for (int r = 0; r < 4; ++r)
+            packed |= quant_byte(fast ? quotient_by_scale(v[b][r], sc, y) : v[b][r] / sc) << (8 * r);
         *(uint32_t*)(a.q + (int64_t)row * a.q_row_stride + c * 256 + 4 * lane) = packed;
     }
     if (threadIdx.x == 0) a.scales[row] = sc;
@@ -790,10 +794,15 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
         lds_barrier();
         if (busy && my_u < units) {  // INT8 bytes at positions 16 i + m of the block
             const int row = my_u / nb, c = my_u % nb, m = lane % 16;
-            const float sc = fmaxf(__uint_as_float(s.rmax[row]), 1e-12f) / 127.0f;
+            const float sc = fmaxf(__uint_as_float(s.rmax[row]), 1e-12f) / 127.0f, y = 1.0f / sc;
             int8_t* dst = s.x.q + row * H + c * 256 + m;
+            if (__builtin_isfinite(sc)) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) dst[16 * i] = (int8_t)quant_byte(v[i], sc);
+                for (int i = 0; i < 16; ++i) dst[16 * i] = (int8_t)quant_byte(quotient_by_scale(v[i], sc, y));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) dst[16 * i] = (int8_t)quant_byte(v[i] / sc);
+            }
             if (c == 0 && m == 0) s.sa[row] = sc;
         }
     }
@@ -1119,10 +1128,15 @@ __global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDown
             if (4 * (wave + kQdWaves * q) >= units) break;
             if (u >= units) continue;
             const int row = u / nb, c = u % nb, m = lane % 16;
-            const float sc = fmaxf(__uint_as_float(s.rmax[row]), 1e-12f) / 127.0f;
+            const float sc = fmaxf(__uint_as_float(s.rmax[row]), 1e-12f) / 127.0f, y = 1.0f / sc;
             int8_t* dst = s.act.q + row * I + c * 256 + m;
+            if (__builtin_isfinite(sc)) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) dst[16 * i] = (int8_t)quant_byte(v[q][i], sc);
+                for (int i = 0; i < 16; ++i) dst[16 * i] = (int8_t)quant_byte(quotient_by_scale(v[q][i], sc, y));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) dst[16 * i] = (int8_t)quant_byte(v[q][i] / sc);
+            }
             if (c == 0 && m == 0) s.sa[row] = sc;
         }
         lds_barrier();

@@ -1,10 +1,12 @@
-/* The FP8 encoders' quotient v / scale (csrc/fp8_util.hpp quotient_by_scale)
+/* The quantizers' quotient v / scale (csrc/common.hpp quotient_by_scale)
  * restated in C and compared bit for bit with IEEE division: y = RN(1 /
  * scale), q0 = RN(v y), then twice q <- RN(q + (v - q scale) y) with both
- * products fused (fmaf).  Cases: random group maxima over 24 decades and
- * values in the group, values within a few ulps of scale times every E4M3
- * value and midpoint up to 448, exact products with short-mantissa scales,
- * zeros, subnormals.  Prints "ok <cases>" or the first mismatches.
+ * products fused (fmaf).  Cases, for the FP8 group scales max(amax, 1e-10)
+ * * fl(1/448) and the INT8 row scales max(amax, 1e-12) / 127: random maxima
+ * over 24 decades and values in the group, values within a few ulps of scale
+ * times every E4M3 value and midpoint up to 448 and every half-integer up to
+ * 127, exact products with short-mantissa scales, zeros, subnormals.  Prints
+ * "ok <cases>" or the first mismatches.
  * Built with -ffp-contract=off so no product is fused behind our back. */
 #include <math.h>
 #include <stdint.h>
@@ -64,6 +66,14 @@ int main(int argc, char** argv) {
         const int steps = (int)(next() % 7) - 3;
         for (int s = 0; s < abs(steps); ++s) v = nextafterf(v, steps > 0 ? INFINITY : 0.0f);
         check((next() & 1) ? -v : v, scale);
+        /* INT8 rows: rint boundaries at half-integers */
+        const float sc8 = fmaxf(amax, 1e-12f) / 127.0f;
+        check((unit() * 2.0f - 1.0f) * amax, sc8);
+        float h = ((float)(next() % 127) + 0.5f) * sc8;
+        const int steps8 = (int)(next() % 7) - 3;
+        for (int s = 0; s < abs(steps8); ++s) h = nextafterf(h, steps8 > 0 ? INFINITY : 0.0f);
+        check((next() & 1) ? -h : h, sc8);
+        check(((float)(next() % 128)) * sc8, sc8);
         const float short_scale = ldexpf((float)(1 + next() % 64), (int)(next() % 40) - 60);
         const float exact = target * short_scale;
         check(exact, short_scale);

@@ -1,8 +1,9 @@
-"""The FP8 encoders divide by the group scale through one correctly rounded
-reciprocal per group and two fused residual corrections per value
-(drama3-studio_amd/csrc/fp8_util.hpp quotient_by_scale).  That quotient must
-be the IEEE quotient bit for bit, or encoded bytes drift from the reference's
-true division (native/src/fp8_reference.cpp:19-36).  The method is restated
+"""The FP8 encoders and the INT8 row quantizers divide by the scale through
+one correctly rounded reciprocal per group or row and two fused residual
+corrections per value (drama3-studio_amd/csrc/common.hpp quotient_by_scale).
+That quotient must be the IEEE quotient bit for bit, or encoded bytes drift
+from the reference's true division (native/src/fp8_reference.cpp:19-36,
+quantized_kernels.py:15-45).  The method is restated
 in C (tests/quotient_check.c) and compared with IEEE division on the CPU over
 random groups and adversarial values next to every E4M3 value and midpoint."""
 import shutil
