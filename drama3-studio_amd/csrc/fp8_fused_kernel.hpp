@@ -84,11 +84,11 @@ struct FzLds {
     float rp[kFusedMaxPairs];         // softmax probability of each routed slot
     int num_active;
     uint32_t epoch;
-    alignas(16) uint8_t xq[kFusedXBytes];   // FP8 activation rows [rows, H]
+    alignas(16) uint8_t xq[kFusedXBytes];   // FP8 activation rows [rows, H] (8-byte chunks in a_operand's order)
     float xs[kFusedXBytes / 128];           // their scale per (row, 128-group)
     float gmax[kFusedXBytes / 128];         // max |x| per (row, 128-group)
     struct {
-        alignas(16) uint8_t q[kFusedHBytes];                     // FP8 hidden [pairs, I]
+        alignas(16) uint8_t q[kFusedHBytes];                     // FP8 hidden [pairs, I] (as xq)
         float s[kFusedHBytes / 128];                             // its scale per (pair, 128-group)
     } h;
     alignas(16) v4i stage[kFzWaves][2][128];  // each wave's two 2 KB slots: FP8 blocks into the MFMA layout
@@ -222,7 +222,10 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
     if (!LEAN && a.xq) {  // caller-quantized rows
         for (int i = tid; i < a.rows * (H / 16); i += kFzThreads) {
             const int r = i / (H / 16), c = (i % (H / 16)) * 16;
-            *(v4i*)&s.xq[r * H + c] = *(const v4i*)(a.xq + (int64_t)r * a.xq_row_stride + c);
+            const v4i q = *(const v4i*)(a.xq + (int64_t)r * a.xq_row_stride + c);
+            const uint64_t q0 = a_bytes8<WF>((uint32_t)q[0] | ((uint64_t)(uint32_t)q[1] << 32));
+            const uint64_t q1 = a_bytes8<WF>((uint32_t)q[2] | ((uint64_t)(uint32_t)q[3] << 32));
+            *(v4i*)&s.xq[r * H + c] = v4i{(int)(uint32_t)q0, (int)(q0 >> 32), (int)(uint32_t)q1, (int)(q1 >> 32)};
         }
         for (int i = tid; i < a.rows * gpr; i += kFzThreads) {
             const int r = i / gpr, g = i % gpr;
@@ -366,7 +369,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
             xamax[q] = row_max(absmax8(v, B == 0 ? a.status : nullptr));
             if (a.x_group == 128) {
                 const float scale = fp8_group_scale(xamax[q]);
-                *(uint64_t*)&s.xq[(u / gpr) * H + (u % gpr) * 128 + col * 8] = encode8(v, scale);
+                *(uint64_t*)&s.xq[(u / gpr) * H + (u % gpr) * 128 + col * 8] = a_bytes8<WF>(encode8(v, scale));
                 if (col == 0) s.xs[u] = scale;
             } else if (col == 0) {
                 s.gmax[u] = xamax[q];
@@ -493,7 +496,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 for (int g = 0; g < gpr; ++g) amax = fmaxf(amax, s.gmax[r * gpr + g]);
                 const float scale = fp8_group_scale(amax);
                 const F8 v = unpack8(xr[q][0], !LEAN && a.x_dtype == kF32 ? xr[q][1] : xr[q][0], a.x_dtype);
-                *(uint64_t*)&s.xq[r * H + (u % gpr) * 128 + col * 8] = encode8(v, scale);
+                *(uint64_t*)&s.xq[r * H + (u % gpr) * 128 + col * 8] = a_bytes8<WF>(encode8(v, scale));
                 if (col == 0) s.xs[u] = scale;
             }
         }
@@ -555,7 +558,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                     // selects, not a branch, so the MFMAs stay in one block
                     const bool in = kb < KB;
                     const int kbc = min(kb, KB - 1);
-                    const v8i ar = a_operand<WF>(lds32(&s.xq[arow * H + kbc * 128 + grp * 32]));
+                    const v8i ar = lds32(&s.xq[arow * H + kbc * 128 + grp * 32]);  // in a_operand's order
                     WRaw<WF> wb = ub[d][i];
                     if constexpr (WF == kWfFp8) wb.v = stage_block(wb.v, s.stage[wave][(d * KBW + i) & 1]);
                     const v4f dq = mfma_w<WF>(ar, wb, zero);
@@ -722,7 +725,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
 #pragma unroll
                 for (int j = 0; j < 8; ++j) h.v[j] = __uint_as_float((uint32_t)w[q][j / 4][j % 4] ^ kHandoffXor);
                 const float scale = fp8_group_scale(row_max(absmax8(h, B == 0 ? a.status : nullptr)));
-                *(uint64_t*)&s.h.q[p * I + g * 128 + col * 8] = encode8(h, scale);
+                *(uint64_t*)&s.h.q[p * I + g * 128 + col * 8] = a_bytes8<WF>(encode8(h, scale));
                 if (col == 0) s.h.s[u] = scale;
             }
         }
@@ -773,7 +776,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fp8_fused_decode_kernel(FusedDe
                 for (int i = 0; i < kChunk; ++i) {
                     WRaw<WF> wb = db[k0 + i];
                     if constexpr (WF == kWfFp8) wb.v = stage_block(wb.v, s.stage[wave][(k0 + i) & 1]);
-                    dq[i] = mfma_w<WF>(a_operand<WF>(af[i]), wb, zero);
+                    dq[i] = mfma_w<WF>(af[i], wb, zero);  // af in a_operand's order
                 }
                 // the block chain by selects, not branches: a branch per block
                 // pulls each MFMA into its block and serializes them (kept where

@@ -107,12 +107,14 @@ __device__ __forceinline__ WRaw<WF> zero_wraw() {
 
 // Four codes (one per byte, values 0..15) through a 16-entry byte table held
 // in four dwords (t0: codes 0-3, t1: 4-7, t2: 8-11, t3: 12-15).
+// Only bits 0-3 of each byte of `codes` are read.  Entries 0-7 and 8-15 are
+// looked up by two byte permutes, and a third picks each byte from one or the
+// other by bit 3 of its code (selector i or 4 + i).
 __device__ __forceinline__ uint32_t lut16(uint32_t codes, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
     const uint32_t sel = codes & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
     const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
-    const uint32_t m = ((codes >> 3) & 0x01010101u) * 0xFFu;
-    return (lo & ~m) | (hi & m);
+    return __builtin_amdgcn_perm(hi, lo, ((codes >> 1) & 0x04040404u) | 0x03020100u);
 }
 
 // E4M3 bytes of code - 8 for codes 0..15: -8 .. 7.
@@ -126,7 +128,7 @@ constexpr uint32_t kHighT = 0x5800D8E0u;
 // bytes: {[k0, k2, k4, k6], [k1, k3, k5, k7]}.
 template <uint32_t T0, uint32_t T1, uint32_t T2, uint32_t T3>
 __device__ __forceinline__ v2i expand_nibbles(uint32_t w) {
-    return v2i{(int)lut16(w & 0x0F0F0F0Fu, T0, T1, T2, T3), (int)lut16((w >> 4) & 0x0F0F0F0Fu, T0, T1, T2, T3)};
+    return v2i{(int)lut16(w, T0, T1, T2, T3), (int)lut16(w >> 4, T0, T1, T2, T3)};
 }
 
 // 2-bit high parts of 8 consecutive K values (16 bits, LSB first) -> two
@@ -155,6 +157,20 @@ __device__ __forceinline__ v8i a_operand(const v8i& a) {
             r[2 * i + 1] = (int)__builtin_amdgcn_perm(d1, d0, 0x07050301u);
         }
         return r;
+    }
+}
+
+// a_operand's byte order applied to 8 activation bytes once, where they are
+// stored (the single-launch decode keeps its LDS rows in this order for the
+// integer formats, so its MFMAs read the A operand as it lies).
+template <int WF>
+__device__ __forceinline__ uint64_t a_bytes8(uint64_t v) {
+    if constexpr (WF == kWfFp8) {
+        return v;
+    } else {
+        const uint32_t d0 = (uint32_t)v, d1 = (uint32_t)(v >> 32);
+        return (uint64_t)__builtin_amdgcn_perm(d1, d0, 0x06040200u) |
+               ((uint64_t)__builtin_amdgcn_perm(d1, d0, 0x07050301u) << 32);
     }
 }
 
