@@ -1283,6 +1283,25 @@ static void quant_forward_impl(const DmoeQuantBank* bank, const void* x, int x_d
         const bool small_dn = fused_enabled() && dmoe::quant_down_decode_fits(mode, pairs, H, I);
         const bool self_routed = route != nullptr && small_up && small_dn &&
                                  dmoe::quant_gateup_decode_routes(E, route->top_k);
+        if (self_routed && out_pairs == nullptr &&
+            dmoe::quant_fused_decode_fits(mode, pairs, rows, E, H, I, x_dtype)) {  // one persistent launch
+            dmoe::QuantFusedArgs fa{};
+            fa.up = dmoe::QuantGateUpArgs{up, x, x_dtype, x_row_stride, rows, row_div, ids, ids_dtype, E, pairs,
+                                          ws.act, status};
+            fa.up.logits = route->logits;
+            fa.up.logits_row_stride = route->logits_row_stride;
+            fa.up.renormalize = route->renormalize;
+            fa.up.ids_out = route->ids_out;
+            fa.up.weights_out = route->weights_out;
+            fa.up.w_dtype = route->w_dtype;
+            fa.dn = dmoe::QuantDownArgs{dn, ws.act, weights, weights_dtype, ids, ids_dtype, E, pairs,
+                                        top_k, out, out_dtype, out_row_stride, nullptr, status};
+            fa.ht = ws.head.handoff;
+            fa.sync = ws.head.epochs;
+            fa.spin_ticks = g_spin_ticks.load(std::memory_order_relaxed);
+            fa.tag_skew = g_force_timeout.load(std::memory_order_relaxed) ? 1u : 0u;
+            if (ordered_fused_launch(st, [&] { return dmoe::launch_quant_fused_decode(fa, st); })) return;
+        }
         if (route != nullptr && !self_routed) {
             const dmoe::RouteArgs ra{route->logits, route->logits_row_stride, rows, E, route->top_k,
                                      route->renormalize != 0, route->ids_out, route->weights_out, route->w_dtype};

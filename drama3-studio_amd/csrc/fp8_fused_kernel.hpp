@@ -51,6 +51,7 @@
 
 #include "common.hpp"
 #include "fp8_util.hpp"
+#include "handoff.hpp"
 #include "kernels.hpp"
 #include "layout.hpp"
 #include "route.hpp"
@@ -108,25 +109,13 @@ __device__ __forceinline__ v8i lds32(const uint8_t* p) {
 // (NaN results are quiet); an h with exactly those bits is published as a
 // quiet NaN, so a published word is never 0.
 constexpr uint32_t kHandoffXor = 0x7F800001u;
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 constexpr v4i zero4i = {0, 0, 0, 0};
-constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 family
-constexpr int kCpolSc1 = 16;              // the cache policy of an agent-scope atomic access
 
 __device__ __forceinline__ uint32_t handoff_encode(float h) {
     const uint32_t b = __float_as_uint(h);
     return (b == kHandoffXor ? 0x7FC00001u : b) ^ kHandoffXor;
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t handoff_buffer(uint32_t* base) {
-    return __builtin_amdgcn_make_buffer_rsrc(base, 0, kHandoffWords * 4, kBufferWord3);
-}
-
-// 16 bytes of hand-off words with the agent-scope load's cache policy (no
-// stale copy from a non-coherent cache); each 4-byte word is read whole.
-__device__ __forceinline__ v4i load_handoff16(__amdgpu_buffer_rsrc_t r, int byte_offset) {
-    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, kCpolSc1));
-}
 
 constexpr int kRouteJ = kRouteLaneSlots;  // logits per lane (experts l + 64 j)
 

@@ -425,4 +425,24 @@ struct QuantDownArgs {
 bool quant_down_decode_fits(int mode, int pairs, int H, int I);
 void launch_quant_down_decode(const QuantDownArgs& a, hipStream_t stream);
 
+// Both small-call kernels as one persistent launch (one workgroup per CU):
+// every workgroup routes, runs one gate/up work item and publishes its
+// activation values as hand-off words (0x10000 | bf16 bits) into the
+// workspace head's buffer of the call's epoch, clears its share of the other
+// buffer, then runs one down tile, its first weight loads issued before it
+// polls the hidden words it needs.  Same bits as the two launches.
+struct QuantFusedArgs {
+    QuantGateUpArgs up;   // with logits (the call routes in the kernel)
+    QuantDownArgs dn;     // act unused; ids / weights: the routing's outputs
+    uint32_t* ht;         // the head's 2 hand-off buffers of kHandoffWords
+    int* sync;            // the head's call counters
+    uint64_t spin_ticks;  // bound of the hand-off wait (100 MHz ticks) before kSyncTimeout
+    uint32_t tag_skew;    // 0; 1 makes readers treat every word as not ready (diagnostic)
+};
+// Calls the two small kernels take, routed in the kernel, whose gate/up work
+// items and down tiles each fit one per CU (modes 0-2, bf16 rows, H <= 2048).
+bool quant_fused_decode_fits(int mode, int pairs, int rows, int experts, int H, int I, int x_dtype);
+// false when the device cannot hold one workgroup per CU (nothing launched)
+bool launch_quant_fused_decode(const QuantFusedArgs& a, hipStream_t stream);
+
 }  // namespace dmoe

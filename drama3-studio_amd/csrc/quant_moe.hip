@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "handoff.hpp"
 #include "kernels.hpp"
 #include "route.hpp"
 
@@ -655,6 +656,7 @@ struct QGateUpLds {
     uint32_t rmax[kQgMaxRows];  // row maxima (non-negative float bits)
     float book[16];
     int rid[kSmallPairs];               // routed in the kernel: expert of each pair
+    float rw[kSmallPairs];              // and its route weight (w_dtype-rounded, as stored)
     alignas(16) int8_t qtab[256 * 16];  // mode 3: INT8 weight of (scale byte, code)
     union {
         float tb[kQWaves][kRotWaveDwords];  // rotation transposes
@@ -666,16 +668,19 @@ struct QGateUpLds {
 // workgroup; 3: 24 + 24, the third tile holding gate columns 16-23 (MFMA
 // columns 0-7) and up columns 16-23 (8-15), so that 8 active experts of a
 // 768-column expert make one workgroup per CU instead of 1.5.
-template <int MODE, int XT, int KBW, int NT>
-__global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGateUpArgs a) {
+// The workgroup body, for work item (ai = active index, cg = column group);
+// each activation value h of pair p, column c goes to sink(p * I + c, bf16
+// bits of h).  A workgroup whose ai is past the active experts returns early.
+template <int MODE, int XT, int KBW, int NT, class Sink, class Pre>
+__device__ __forceinline__ void quant_gateup_body(const QuantGateUpArgs& a, QGateUpLds& s, int wai, int cg,
+                                                  Sink&& sink, Pre&& before_publish) {
     constexpr bool F16 = XT == kF16;
     constexpr int NX = NT == 3 ? KBW : 1;  // third-tile registers
-    __shared__ QGateUpLds s;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int col = lane % 16, grp = lane / 16;
     const QuantProjArgs& w = a.w13;
     const int H = w.K, I = w.N / 2, KB = H / 128, P = a.pairs, rows = a.rows;
-    const int n0 = blockIdx.y * (NT == 3 ? 24 : 16);
+    const int n0 = cg * (NT == 3 ? 24 : 16);
 
     // loads are issued unconditionally (clamped indexes): a load merged with
     // a constant on another path is waited for at the merge.  Two words per
@@ -710,10 +715,13 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
             const int i = min((int)threadIdx.x + j * kQThreads, chunks - 1);
             c16[j] = *(const v4i*)((const uint16_t*)a.x + (i / cpr) * a.x_row_stride + (i % cpr) * 8);
         }
+        // every load is stored (a clamped one again over the last chunk, the
+        // same bytes): a load left unread on some path is waited for at the
+        // next reuse of its registers, by then behind every store of the wave
 #pragma unroll
         for (int j = 0; j < kChunks; ++j) {
-            const int i = threadIdx.x + j * kQThreads;
-            if (i < chunks) *(v4i*)(s.x.h + (i / cpr) * H + (i % cpr) * 8) = c16[j];
+            const int i = min((int)threadIdx.x + j * kQThreads, chunks - 1);
+            *(v4i*)(s.x.h + (i / cpr) * H + (i % cpr) * 8) = c16[j];
         }
     }
     if (a.logits) {
@@ -731,7 +739,8 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
             wave_route_small(l, a.experts, top_k, a.renormalize, id, wgt);
             if (lane < top_k) {
                 s.rid[wave * top_k + lane] = id;
-                if (blockIdx.x == 0 && blockIdx.y == 0) {
+                s.rw[wave * top_k + lane] = round_through(wgt, a.w_dtype);
+                if (wai == 0 && cg == 0) {
                     a.ids_out[wave * top_k + lane] = id;
                     store_from_f32(a.weights_out, wave * top_k + lane, a.w_dtype, wgt);
                 }
@@ -741,15 +750,20 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
         if (wave == 0) group_pairs(lane < P ? s.rid[lane] : -1, lane, s.g);
     } else if (wave == 0) {
         const int pe = lane < P ? id_expert(idb, a.ids_dtype, a.experts) : -1;
-        if (lane < P && pe < 0 && blockIdx.x == 0 && blockIdx.y == 0) raise_status(a.status, kBadExpertId);
+        if (lane < P && pe < 0 && wai == 0 && cg == 0) raise_status(a.status, kBadExpertId);
         group_pairs(pe, lane, s.g);
     }
+    // the route words are read on every path: a load left unread is waited
+    // for at the next reuse of its registers, by then behind the wave's stores
+    asm volatile("" ::"v"(idb.x), "v"(idb.y));
     lds_barrier();
-    if ((int)blockIdx.x >= s.g.num_active) {  // uniform: fewer distinct experts than the grid assumed
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (wai >= s.g.num_active) {  // uniform: fewer distinct experts than the grid assumed
+        // every load out of the way (by the builtin, which the compiler's own
+        // wait bookkeeping sees: after an inlined body it need not wait again)
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), gfx9 encoding
         return;
     }
-    const int ai = blockIdx.x;
+    const int ai = wai;
     const int e = s.g.active[ai], pbeg = s.g.start[ai], pend = s.g.start[ai + 1];
     const int ng = n0 + col, nu = I + n0 + col;
     const int nxg = n0 + 16 + (col & 7), nxu = I + nxg, nx = col < 8 ? nxg : nxu;  // third tile (NT 3)
@@ -830,6 +844,7 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
         }
     }
 
+    before_publish();  // all threads, ahead of the first reduction barrier
     for (int m0 = pbeg; m0 < pend; m0 += 16) {
         const int mc = min(16, pend - m0);
         const bool live = col < mc;
@@ -909,7 +924,7 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
                 yg = bf16_round(yg);
                 yu = bf16_round(yu);
                 const float act = bf16_round(bf16_round(yg / (1.0f + expf(-yg))) * yu);
-                a.act[(int64_t)p * I + n0 + col] = __builtin_bit_cast(uint16_t, (__bf16)act);
+                sink((int64_t)p * I + n0 + col, __builtin_bit_cast(uint16_t, (__bf16)act));
                 if constexpr (NT == 3) {
                     if (col < 8) {  // gate column n0 + 16 + col here, its up column in lane + 8
                         float xg, xu;
@@ -933,13 +948,20 @@ __global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGat
                         xg = bf16_round(xg);
                         xu = bf16_round(xu);
                         const float xact = bf16_round(bf16_round(xg / (1.0f + expf(-xg))) * xu);
-                        a.act[(int64_t)p * I + nxg] = __builtin_bit_cast(uint16_t, (__bf16)xact);
+                        sink((int64_t)p * I + nxg, __builtin_bit_cast(uint16_t, (__bf16)xact));
                     }
                 }
             }
         }
         lds_barrier();
     }
+}
+
+template <int MODE, int XT, int KBW, int NT>
+__global__ __launch_bounds__(kQThreads) void quant_gateup_decode_kernel(QuantGateUpArgs a) {
+    __shared__ QGateUpLds s;
+    quant_gateup_body<MODE, XT, KBW, NT>(
+        a, s, blockIdx.x, blockIdx.y, [&](int64_t i, uint16_t bits) { a.act[i] = bits; }, [] {});
 }
 
 bool quant_gateup_decode_fits(int mode, int pairs, int rows, int H, int I, const void* x, int x_dtype,
@@ -1014,12 +1036,13 @@ void launch_quant_gateup_decode(const QuantGateUpArgs& a, hipStream_t stream) {
 constexpr int kQdWaves = 4, kQdThreads = kQdWaves * kWave;
 constexpr int kQdGroups = 3;  // rotation groups (4 blocks, 16 lanes each) per wave: pairs * I / 256 <= 48
 
-struct QDownLds {
+template <int QDW>
+struct QDownLdsT {
     SmallGroups g;
     union {
         struct {
             alignas(16) int8_t q[kQdMaxRotRows * kQdMaxI];  // modes 1-3: rotated INT8 hidden rows
-            float tb[kQdWaves][kRotWaveDwords];             // and the rotation transposes
+            float tb[QDW][kRotWaveDwords];                  // and the rotation transposes
         };
         alignas(16) uint16_t h[kQdMaxBf16];  // mode 0: bf16 hidden rows
     } act;
@@ -1028,77 +1051,218 @@ struct QDownLds {
     float wt[kSmallPairs];
     int valid[kSmallPairs];
     float part[kSmallPairs][8];
-    float book[kQdWaves][2][16];  // mode 3 codebooks of the wave's two experts
+    float book[QDW][2][16];  // mode 3 codebooks of the wave's two experts
+};
+using QDownLds = QDownLdsT<kQdWaves>;
+
+// Where the single-launch packed decode's down phase reads the hidden rows:
+// word p * I + c of `ht` holds 0x10000 | the bf16 bits of h (never 0, so a
+// cleared word is not ready), published by the gate/up phase of the call.
+struct PackedHidden {
+    const uint32_t* ht;
+    uint64_t spin_ticks;  // bound of the wait (100 MHz ticks) before kSyncTimeout
+    uint32_t tag_skew;    // 1: every word reads as not ready (diagnostic)
 };
 
+// One down batch of a wave: active experts 2 bi (MFMA columns 0-7) and
+// 2 bi + 1 (8-15) of output rows n0.. (lane column n), their weight rows
+// loaded (unconditionally: a missing second expert reads the first's rows)
+// and scales.
+template <int KB2>
+struct DownBatch {
+    int e0, e1, e, ec;
+    WRaw raw[KB2];
+    float sch, bk;
+};
 template <int MODE, int KB2>
-__global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDownArgs a) {
-    __shared__ QDownLds s;
+__device__ __forceinline__ void fetch_down_batch(const QuantProjArgs& w, const SmallGroups& g, int bi, int n,
+                                                 DownBatch<KB2>& d) {
+    const int lane = threadIdx.x % kWave, col = lane % 16, grp = lane / 16;
+    const int I = w.K, KB = I / 128, num_active = g.num_active;
+    d.e0 = num_active > 0 ? g.active[2 * bi] : 0;
+    d.e1 = 2 * bi + 1 < num_active ? g.active[2 * bi + 1] : -1;
+    d.e = col < 8 ? d.e0 : d.e1;
+    d.ec = d.e >= 0 ? d.e : d.e0;
+#pragma unroll
+    for (int kb = 0; kb < KB2; ++kb) d.raw[kb] = fetch_wrow<MODE>(w, d.ec, n, min(kb, KB - 1), grp);
+    d.sch = 1.0f;
+    d.bk = 0.0f;
+    if constexpr (MODE != 0) d.sch = channel_scale<MODE>(w, d.ec, n);
+    if constexpr (MODE == 3) {  // lanes 0-15: codebook of e0, 16-31: of e1
+        const int eb = (lane & 16) && d.e1 >= 0 ? d.e1 : d.e0;
+        d.bk = *(const float*)(w.s + (int64_t)eb * w.s_se + (int64_t)(lane % 16) * w.s_sn + I / 16 + 4);
+    }
+}
+
+// The down workgroup body for output tile `tile` with QDW waves.  FUSED:
+// the grouping `fg` comes from the call's in-kernel routing (visible to every
+// wave), prep() (all threads, before the body's first barrier) fills s.wt /
+// s.valid, and hidden() (after it) gives the hand-off the hidden rows are
+// polled from.  Otherwise the workgroup reads ids, weights and a.act itself.
+template <int MODE, int KB2, int QDW, bool FUSED, class Prep, class Hidden>
+__device__ __forceinline__ void quant_down_body(const QuantDownArgs& a, QDownLdsT<QDW>& s, int tile,
+                                                const SmallGroups& fg, Prep&& prep, Hidden&& hidden) {
+    constexpr int QDT = QDW * kWave;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int col = lane % 16, grp = lane / 16;
     const QuantProjArgs& w = a.w2;
     const int I = w.K, H = w.N, KB = I / 128, P = a.pairs;
-    const int n0 = blockIdx.x * 8;
+    const int n0 = tile * 8;
 
     const bool pl = wave == 0 && lane < P;  // lane p of wave 0 holds pair p
     // loads are issued unconditionally (clamped indexes): a load merged with
     // a constant on another path is waited for at the merge
-    const uint2 idb = load_id_bits(a.ids, min(lane, P - 1), a.ids_dtype);
-    const uint32_t wbits = load_bits(a.weights, min(lane, P - 1), a.w_dtype);  // used at the end
+    uint2 idb = {0u, 0u};
+    uint32_t wbits = 0u;  // used at the end
+    if constexpr (!FUSED) {
+        idb = load_id_bits(a.ids, min(lane, P - 1), a.ids_dtype);
+        wbits = load_bits(a.weights, min(lane, P - 1), a.w_dtype);
+    }
     // hidden rows: every load issued now (clamped to the last unit)
     const int nb = I / 256, units = P * nb;
-    Raw16<kBF16> hin[kQdGroups];  // group q of wave w: blocks 4 (w + 4 q) .. +3, 16 lanes each
+    Raw16<kBF16> hin[kQdGroups];  // group q of wave w: blocks 4 (w + QDW q) .. +3, 16 lanes each
     if constexpr (MODE != 0) {
+        if constexpr (!FUSED) {
 #pragma unroll
-        for (int q = 0; q < kQdGroups; ++q) {
-            const int u = min(4 * (wave + kQdWaves * q) + lane / 16, units - 1);
-            hin[q] = load_raw16<kBF16>(a.act, (int64_t)(u / nb) * I + (u % nb) * 256 + 16 * (lane % 16));
+            for (int q = 0; q < kQdGroups; ++q) {
+                const int u = min(4 * (wave + QDW * q) + lane / 16, units - 1);
+                hin[q] = load_raw16<kBF16>(a.act, (int64_t)(u / nb) * I + (u % nb) * 256 + 16 * (lane % 16));
+            }
         }
-        for (int r = threadIdx.x; r < P; r += kQdThreads) s.rmax[r] = 0u;
+        for (int r = threadIdx.x; r < P; r += QDT) s.rmax[r] = 0u;
     }
     // mode 0: the bf16 hidden rows, stored to LDS once the weight loads are out
-    constexpr int kChunks = MODE == 0 ? kQdMaxBf16 / 8 / kQdThreads : 1;  // 16-byte chunks per thread
+    constexpr int kChunks = MODE == 0 ? kQdMaxBf16 / 8 / QDT : 1;  // 16-byte chunks per thread
     const int chunks = P * I / 8;
     v4i c16[kChunks];
-    if constexpr (MODE == 0) {
+    if constexpr (MODE == 0 && !FUSED) {
 #pragma unroll
         for (int j = 0; j < kChunks; ++j)
-            c16[j] = *(const v4i*)(a.act + (int64_t)min((int)threadIdx.x + j * kQdThreads, chunks - 1) * 8);
+            c16[j] = *(const v4i*)(a.act + (int64_t)min((int)threadIdx.x + j * QDT, chunks - 1) * 8);
     }
-    for (int i = threadIdx.x; i < P * 8; i += kQdThreads) s.part[i / 8][i % 8] = 0.0f;
-    const int pe = pl ? id_expert(idb, a.ids_dtype, a.experts) : -1;
-    if (wave == 0) {
-        if (pl && pe < 0 && blockIdx.x == 0) raise_status(a.status, kBadExpertId);
-        group_pairs(pe, lane, s.g);
+    const SmallGroups& g = FUSED ? fg : s.g;
+    int pe = -1;
+    if constexpr (!FUSED) {
+        for (int i = threadIdx.x; i < P * 8; i += QDT) s.part[i / 8][i % 8] = 0.0f;
+        pe = pl ? id_expert(idb, a.ids_dtype, a.experts) : -1;
+        if (wave == 0) {
+            if (pl && pe < 0 && tile == 0) raise_status(a.status, kBadExpertId);
+            group_pairs(pe, lane, s.g);
+        }
+        lds_barrier();
     }
-    lds_barrier();
 
-    const int num_active = s.g.num_active;
+    const int num_active = g.num_active;
     const int batches = (num_active + 1) / 2;
     // batch bi = active experts 2 bi (columns 0-7) and 2 bi + 1 (8-15)
-    int e0 = 0, e1 = -1, e = 0, ec = 0;
-    WRaw raw[KB2];
-    float sch = 1.0f, bk = 0.0f;
     const int n = n0 + (col & 7);
-    auto fetch_batch = [&](int bi) {  // loads unconditional (see above)
-        e0 = num_active > 0 ? s.g.active[2 * bi] : 0;
-        e1 = 2 * bi + 1 < num_active ? s.g.active[2 * bi + 1] : -1;
-        e = col < 8 ? e0 : e1;
-        ec = e >= 0 ? e : e0;
-#pragma unroll
-        for (int kb = 0; kb < KB2; ++kb) raw[kb] = fetch_wrow<MODE>(w, ec, n, min(kb, KB - 1), grp);
-        if constexpr (MODE != 0) sch = channel_scale<MODE>(w, ec, n);
-        if constexpr (MODE == 3) {  // lanes 0-15: codebook of e0, 16-31: of e1
-            const int eb = (lane & 16) && e1 >= 0 ? e1 : e0;
-            bk = *(const float*)(w.s + (int64_t)eb * w.s_se + (int64_t)(lane % 16) * w.s_sn + I / 16 + 4);
+    DownBatch<KB2> cur;
+    auto fetch_batch = [&](int bi) { fetch_down_batch<MODE, KB2>(w, g, bi, n, cur); };
+    WRow b[KB2];
+    auto decode_batch = [&]() {
+        if constexpr (MODE == 3) {
+            if (lane < 32) s.book[wave][lane / 16][lane % 16] = cur.bk;  // read back by this wave only
         }
+#pragma unroll
+        for (int kb = 0; kb < KB2; ++kb) decode_wrow<MODE, false>(cur.raw[kb], n, s.book[wave][col < 8 ? 0 : 1], b[kb]);
     };
-    fetch_batch(min(wave, max(batches - 1, 0)));  // waves without a batch: loaded, never used
+    // FUSED: wave 0 published the workgroup's h words and its memory counter
+    // holds their stores, so the batches go to waves 1.. (a wait for the rows
+    // there would also wait for those stores).  Every wave issues the fetch
+    // (wave 0's, and those past the last batch, are never used): a load on
+    // one path only is waited for where the paths merge.
+    constexpr int W0 = FUSED ? 1 : 0;
+    // FUSED, up to 6 blocks: the first batch is decoded while the hidden
+    // rows are polled (8 blocks of decoded rows held there would spill)
+    constexpr bool kEarly = FUSED && KB2 <= 6;
+    const bool has_batch = wave >= W0 && wave - W0 < batches;  // wave-uniform
+    fetch_batch(min(max(wave - W0, 0), max(batches - 1, 0)));
+
+    if constexpr (FUSED) {
+        for (int i = threadIdx.x; i < P * 8; i += QDT) s.part[i / 8][i % 8] = 0.0f;
+        prep();
+        lds_barrier();
+        const PackedHidden hs = hidden();
+        // The hidden words: this lane's 16 values of each of its rotation
+        // units (modes 1-3) or its 8-value chunks (mode 0), clamped to real
+        // ones as the loads above are, every 16-byte read at once, then all
+        // of them again until every word is non-zero: one round trip per try.
+        // (Only real units or chunks are read: these loads bypass the
+        // caches, and clamped duplicates would all hit the same words.)
+        constexpr int kReads = MODE == 0 ? 2 * kChunks : 4 * kQdGroups;
+        const __amdgpu_buffer_rsrc_t hb = handoff_buffer(const_cast<uint32_t*>(hs.ht));
+        int off[kReads];  // byte offsets
+        bool want[kReads];
+#pragma unroll
+        for (int q = 0; q < kReads; ++q) {
+            if constexpr (MODE == 0) {
+                const int i = (int)threadIdx.x + (q / 2) * QDT;
+                want[q] = i < chunks;
+                off[q] = (min(i, chunks - 1) * 8 + 4 * (q % 2)) * 4;
+            } else {
+                const int u = 4 * (wave + QDW * (q / 4)) + lane / 16;
+                want[q] = u < units;
+                const int uc = min(u, units - 1);
+                off[q] = ((uc / nb) * I + (uc % nb) * 256 + 16 * (lane % 16) + 4 * (q % 4)) * 4;
+            }
+        }
+        v4i hw[kReads];
+#pragma unroll
+        for (int q = 0; q < kReads; ++q) hw[q] = v4i{0, 0, 0, 0};
+        auto read_all = [&]() {
+#pragma unroll
+            for (int q = 0; q < kReads; ++q)
+                if (want[q]) hw[q] = load_handoff16(hb, off[q]);
+        };
+        auto all_ok = [&]() {
+            bool r = !hs.tag_skew;
+#pragma unroll
+            for (int q = 0; q < kReads; ++q)
+                r = r & (!want[q] | ((hw[q][0] != 0) & (hw[q][1] != 0) & (hw[q][2] != 0) & (hw[q][3] != 0)));
+            return __builtin_amdgcn_ballot_w64(!r) == 0;  // the wave's branch, uniform
+        };
+        // The first check waits for every load, the batch's weight rows too:
+        // (kEarly) the wave decodes them while its second read is out.
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        read_all();
+        bool ready = all_ok(), timed_out = false;
+        if (!ready) {
+            __builtin_amdgcn_s_sleep(1);
+            read_all();
+        }
+        if (kEarly && has_batch) decode_batch();
+        if (!ready) {
+            ready = all_ok();
+            timed_out = !ready && __builtin_amdgcn_s_memrealtime() - t0 > hs.spin_ticks;
+            while (!ready && !timed_out) {
+                __builtin_amdgcn_s_sleep(1);
+                read_all();
+                ready = all_ok();
+                timed_out = __builtin_amdgcn_s_memrealtime() - t0 > hs.spin_ticks;
+            }
+        }
+        if (timed_out) raise_status(a.status, kSyncTimeout);
+        // the bf16 bits (low halves), two per dword, as the loads from a.act give them
+        auto pack = [](v4i v, int k) {
+            return ((uint32_t)v[2 * k] & 0xFFFFu) | ((uint32_t)v[2 * k + 1] << 16);
+        };
+        if constexpr (MODE == 0) {
+#pragma unroll
+            for (int j = 0; j < kChunks; ++j)
+                c16[j] = v4i{(int)pack(hw[2 * j], 0), (int)pack(hw[2 * j], 1), (int)pack(hw[2 * j + 1], 0),
+                             (int)pack(hw[2 * j + 1], 1)};
+        } else {
+#pragma unroll
+            for (int q = 0; q < kQdGroups; ++q)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) hin[q].w[k] = pack(hw[4 * q + k / 2], k % 2);
+        }
+    }
 
     if constexpr (MODE == 0) {
 #pragma unroll
         for (int j = 0; j < kChunks; ++j) {
-            const int i = threadIdx.x + j * kQdThreads;
+            const int i = threadIdx.x + j * QDT;
             if (i < chunks) *(v4i*)(s.act.h + i * 8) = c16[j];
         }
         lds_barrier();
@@ -1108,8 +1272,8 @@ __global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDown
         float v[kQdGroups][16];
 #pragma unroll
         for (int q = 0; q < kQdGroups; ++q) {
-            const int u = 4 * (wave + kQdWaves * q) + lane / 16;
-            if (4 * (wave + kQdWaves * q) >= units) break;  // wave-uniform
+            const int u = 4 * (wave + QDW * q) + lane / 16;
+            if (4 * (wave + QDW * q) >= units) break;  // wave-uniform
             convert16(hin[q], v[q]);
             rotate16(v[q], s.act.tb[wave], lane);  // lanes past the last block: duplicates, never stored
             float amax = 0.0f;
@@ -1124,8 +1288,8 @@ __global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDown
         lds_barrier();
 #pragma unroll
         for (int q = 0; q < kQdGroups; ++q) {  // INT8 bytes at positions 16 i + m of each block
-            const int u = 4 * (wave + kQdWaves * q) + lane / 16;
-            if (4 * (wave + kQdWaves * q) >= units) break;
+            const int u = 4 * (wave + QDW * q) + lane / 16;
+            if (4 * (wave + QDW * q) >= units) break;
             if (u >= units) continue;
             const int row = u / nb, c = u % nb, m = lane % 16;
             const float sc = fmaxf(__uint_as_float(s.rmax[row]), 1e-12f) / 127.0f, y = 1.0f / sc;
@@ -1142,43 +1306,46 @@ __global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDown
         lds_barrier();
     }
 
-    for (int bi = wave; bi < batches; bi += kQdWaves) {
-        if (bi != wave) fetch_batch(bi);
-        if constexpr (MODE == 3) {
-            if (lane < 32) s.book[wave][lane / 16][lane % 16] = bk;  // read back by this wave only
-        }
-        WRow b[KB2];
-#pragma unroll
-        for (int kb = 0; kb < KB2; ++kb) decode_wrow<MODE, false>(raw[kb], n, s.book[wave][col < 8 ? 0 : 1], b[kb]);
-        const int s0 = s.g.start[2 * bi], M0 = s.g.start[2 * bi + 1] - s0;
-        const int s1 = e1 >= 0 ? s.g.start[2 * bi + 1] : 0, M1 = e1 >= 0 ? s.g.start[2 * bi + 2] - s1 : 0;
+    for (int bi = wave - W0; bi < batches; bi += QDW - W0) {
+        if (bi < 0) break;  // wave 0 of a FUSED body
+        if (bi != wave - W0) fetch_batch(bi);
+        if (!kEarly || bi != wave - W0) decode_batch();  // kEarly: the first was decoded while polling
+        const int s0 = g.start[2 * bi], M0 = g.start[2 * bi + 1] - s0;
+        const int s1 = cur.e1 >= 0 ? g.start[2 * bi + 1] : 0, M1 = cur.e1 >= 0 ? g.start[2 * bi + 2] - s1 : 0;
         auto a_row = [&](int pass, int row) -> int {  // pair of A row `row` in a pass (-1: none)
             const int m = pass * 8 + (row & 7);
-            if (row < 8) return m < M0 ? s.g.plist[s0 + m] : -1;
-            return m < M1 ? s.g.plist[s1 + m] : -1;
+            if (row < 8) return m < M0 ? g.plist[s0 + m] : -1;
+            return m < M1 ? g.plist[s1 + m] : -1;
         };
         const int passes = (max(M0, M1) + 7) / 8;
         for (int pass = 0; pass < passes; ++pass) {
+            // A rows without a pair read row 0 (their results are never
+            // stored; an MFMA output row depends on its A row alone); the A
+            // reads of block kb + 1 are issued before the products of kb
             const int ar = a_row(pass, col);
             const int arc = ar >= 0 ? ar : 0;
             v4f fa = {0, 0, 0, 0};
             v4i ia = {0, 0, 0, 0};
+            constexpr int kT = MODE == 0 ? 4 : 2;  // 16-byte A reads per block
+            const uint8_t* xr = MODE == 0 ? (const uint8_t*)(s.act.h + arc * I + grp * 32)
+                                          : (const uint8_t*)(s.act.q + arc * I + grp * 32);
+            constexpr int kBlockBytes = MODE == 0 ? 256 : 128;
+            v4i av[2][kT];
+#pragma unroll
+            for (int t = 0; t < kT; ++t) av[0][t] = *(const v4i*)(xr + 16 * t);
 #pragma unroll
             for (int kb = 0; kb < KB2; ++kb) {
                 if (kb >= KB) continue;
-                if constexpr (MODE == 0) {
-                    const uint16_t* xr = s.act.h + arc * I + kb * 128 + grp * 32;
+                if (kb + 1 < KB2 && kb + 1 < KB) {
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const v4i av = ar >= 0 ? *(const v4i*)(xr + 8 * t) : v4i{0, 0, 0, 0};
-                        fa = mfma_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, b[kb].r[t]), fa);
-                    }
-                } else {
-                    const int8_t* xr = s.act.q + arc * I + kb * 128 + grp * 32;
-                    const v4i a0 = ar >= 0 ? *(const v4i*)xr : v4i{0, 0, 0, 0};
-                    const v4i a1 = ar >= 0 ? *(const v4i*)(xr + 16) : v4i{0, 0, 0, 0};
-                    ia = mfma_i8(a0, b[kb].r[0], ia);
-                    ia = mfma_i8(a1, b[kb].r[1], ia);
+                    for (int t = 0; t < kT; ++t) av[(kb + 1) & 1][t] = *(const v4i*)(xr + (kb + 1) * kBlockBytes + 16 * t);
+                }
+#pragma unroll
+                for (int t = 0; t < kT; ++t) {
+                    if constexpr (MODE == 0)
+                        fa = mfma_bf16(__builtin_bit_cast(v8bf, av[kb & 1][t]), __builtin_bit_cast(v8bf, b[kb].r[t]), fa);
+                    else
+                        ia = mfma_i8(av[kb & 1][t], b[kb].r[t], ia);
                 }
             }
 #pragma unroll
@@ -1186,26 +1353,28 @@ __global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDown
                 const int row = grp * 4 + r;
                 // keep the diagonal blocks: A row half == B column half
                 const int pr = ((row < 8) == (col < 8)) ? a_row(pass, row) : -1;
-                if (pr < 0 || e < 0) continue;
-                const float y = MODE == 0 ? fa[r] : (float)ia[r] * s.sa[pr] * sch;
+                if (pr < 0 || cur.e < 0) continue;
+                const float y = MODE == 0 ? fa[r] : (float)ia[r] * s.sa[pr] * cur.sch;
                 s.part[pr][col & 7] = bf16_round(y);
             }
         }
     }
-    if (pl) {
-        s.wt[lane] = bits_to_f32(wbits, a.w_dtype);
-        s.valid[lane] = pe >= 0;
+    if constexpr (!FUSED) {
+        if (pl) {
+            s.wt[lane] = bits_to_f32(wbits, a.w_dtype);
+            s.valid[lane] = pe >= 0;
+        }
     }
     lds_barrier();
     // pair partial = bf16(y) * route weight (fp32)
     if (a.out_pairs) {  // ordered fp32 partials, one row per pair (invalid pairs 0)
-        for (int i = threadIdx.x; i < P * 8; i += kQdThreads) {
+        for (int i = threadIdx.x; i < P * 8; i += QDT) {
             const int p = i / 8, c = i % 8;
             a.out_pairs[(int64_t)p * H + n0 + c] = s.valid[p] ? s.part[p][c] * s.wt[p] : 0.0f;
         }
     } else {  // layer output: fp32 sum of each token's valid partials in router slot order
         const int tokens = P / a.top_k;
-        for (int i = threadIdx.x; i < tokens * 8; i += kQdThreads) {
+        for (int i = threadIdx.x; i < tokens * 8; i += QDT) {
             const int t = i / 8, c = i % 8;
             float acc = 0.0f;
             for (int j = 0; j < a.top_k; ++j) {
@@ -1217,6 +1386,13 @@ __global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDown
             store_from_f32(a.out, (int64_t)t * a.out_row_stride + n0 + c, a.out_dtype, acc);
         }
     }
+}
+
+template <int MODE, int KB2>
+__global__ __launch_bounds__(kQdThreads) void quant_down_decode_kernel(QuantDownArgs a) {
+    __shared__ QDownLds s;
+    quant_down_body<MODE, KB2, kQdWaves, false>(a, s, blockIdx.x, s.g, [] {},
+                                                [] { return PackedHidden{}; });
 }
 
 bool quant_down_decode_fits(int mode, int pairs, int H, int I) {
@@ -1242,6 +1418,122 @@ void launch_quant_down_decode(const QuantDownArgs& a, hipStream_t stream) {
         case 2: by_kb(std::integral_constant<int, 2>{}); break;
         default: by_kb(std::integral_constant<int, 3>{}); break;
     }
+}
+
+// ------------------------------------- small call as one persistent launch
+
+template <int MODE, int XT, int KBW, int NT, int KB2>
+__global__ __launch_bounds__(kQThreads, 1) void quant_fused_decode_kernel(QuantFusedArgs a) {
+    __shared__ QGateUpLds su;
+    __shared__ QDownLdsT<kQWaves> sd;
+    __shared__ uint32_t s_epoch;
+    const int B = blockIdx.x, G = gridDim.x, tid = threadIdx.x;
+    const int I = a.up.w13.N / 2, P = a.up.pairs;
+    const int cgs = I / (NT == 3 ? 24 : 16), items = min(a.up.pairs, a.up.experts) * cgs;
+    // the call ticket from the last wave (it has no routing to do), read
+    // once the gate/up work is out
+    constexpr int kTicketThread = kQThreads - kWave;
+    const uint64_t ticket = tid == kTicketThread ? take_call_ticket(a.sync, B) : 0;
+    auto set_epoch = [&]() {  // a branch of the ticket thread's wave only: no other wave waits for the atomic
+        if (__builtin_amdgcn_readfirstlane(tid / kWave) == kTicketThread / kWave && tid == kTicketThread)
+            s_epoch = call_epoch(ticket, B, G);
+    };
+    const int tiles = a.dn.w2.N / 8;
+    if (B < items) {
+        uint32_t* hbuf = nullptr;
+        // wave 0 publishes after the body's reduction barrier, so the epoch
+        // written just before the pass loop is in LDS by then
+        quant_gateup_body<MODE, XT, KBW, NT>(
+            a.up, su, B % min(a.up.pairs, a.up.experts), B / min(a.up.pairs, a.up.experts),
+            [&](int64_t i, uint16_t bits) {
+                if (hbuf == nullptr) hbuf = a.ht + (int64_t)(s_epoch & 1) * kHandoffWords;
+                __hip_atomic_store(hbuf + i, 0x10000u | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            },
+            set_epoch);
+    } else {
+        // no gate/up item: route and group like the others
+        quant_gateup_body<MODE, XT, KBW, NT>(a.up, su, min(a.up.pairs, a.up.experts), 0,
+                                             [&](int64_t, uint16_t) {}, set_epoch);
+    }
+    // down: the route weights, the epoch (the ticket thread's wave alone waits
+    // for its atomic) and the clear of the next buffer, then the polls
+    auto prep = [&]() {
+        for (int i = tid; i < kSmallPairs; i += kQThreads) {
+            sd.wt[i] = su.rw[min(i, P - 1)];
+            sd.valid[i] = 1;
+        }
+        set_epoch();
+    };
+    auto hidden = [&]() {
+        const uint32_t epoch = __builtin_amdgcn_readfirstlane(s_epoch);
+        clear_next_handoff(a.ht, epoch, B, G, tid, kQThreads);
+        return PackedHidden{a.ht + (int64_t)(epoch & 1) * kHandoffWords, a.spin_ticks, a.tag_skew};
+    };
+    if (B < tiles) {
+        quant_down_body<MODE, KB2, kQWaves, true>(a.dn, sd, B, su.g, prep, hidden);
+        for (int t = B + G; t < tiles; t += G) {
+            lds_barrier();  // the previous tile's partials are read
+            quant_down_body<MODE, KB2, kQWaves, true>(a.dn, sd, t, su.g, prep, hidden);
+        }
+    } else {  // no down tile: the epoch and the clear still
+        prep();
+        lds_barrier();
+        hidden();
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load outlives the wave
+}
+
+// Instances: modes 0-2 (mode 3's table lookups need more registers than one
+// workgroup per CU leaves), bf16 activation rows, H <= 16 K blocks per wave pair.
+bool quant_fused_decode_fits(int mode, int pairs, int rows, int experts, int H, int I, int x_dtype) {
+    if (mode < 0 || mode > 2 || x_dtype != kBF16 || (H / 128 + kQWaves - 1) / kQWaves > 2) return false;
+    if (mode == 0 && I / 128 > 6) return false;  // 8 blocks of bf16 rows spill there
+    if (!quant_down_decode_fits(mode, pairs, H, I) || !quant_gateup_decode_routes(experts, pairs / max(rows, 1)))
+        return false;
+    const int cus = device_cus();
+    const int max_active = std::min(pairs, experts);
+    const bool wide = I % 24 == 0 && max_active * (I / 16) > cus;
+    return max_active * (I / (wide ? 24 : 16)) <= cus && H / 8 <= cus && (int64_t)pairs * I <= kHandoffWords;
+}
+
+bool launch_quant_fused_decode(const QuantFusedArgs& a, hipStream_t stream) {
+    const int I = a.up.w13.N / 2, max_active = std::min(a.up.pairs, a.up.experts), cus = device_cus();
+    const bool wide = I % 24 == 0 && max_active * (I / 16) > cus;
+    const int kbw = (a.up.w13.K / 128 + kQWaves - 1) / kQWaves, kb = a.dn.w2.K / 128;
+    bool ok = true;
+    auto go = [&](auto kernel) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kQThreads, 0) != hipSuccess || per_cu < 1) {
+            ok = false;
+            return;
+        }
+        hipLaunchKernelGGL(kernel, dim3(cus), dim3(kQThreads), 0, stream, a);
+    };
+    auto by_kb = [&](auto m, auto xt, auto kw, auto nt) {
+        constexpr int M = decltype(m)::value, X = decltype(xt)::value, K = decltype(kw)::value,
+                      N = decltype(nt)::value;
+        if (kb <= 2) go(quant_fused_decode_kernel<M, X, K, N, 2>);
+        else if (kb <= 4) go(quant_fused_decode_kernel<M, X, K, N, 4>);
+        else if (kb <= 6) go(quant_fused_decode_kernel<M, X, K, N, 6>);
+        else if constexpr (M != 0) go(quant_fused_decode_kernel<M, X, K, N, 8>);
+        else ok = false;  // not taken: the fit check refuses mode 0 past 6 blocks
+    };
+    auto by_nt = [&](auto m, auto xt, auto kw) {
+        if (wide) by_kb(m, xt, kw, std::integral_constant<int, 3>{});
+        else by_kb(m, xt, kw, std::integral_constant<int, 2>{});
+    };
+    auto by_kbw = [&](auto m) {
+        if (kbw <= 1) by_nt(m, std::integral_constant<int, kBF16>{}, std::integral_constant<int, 1>{});
+        else by_nt(m, std::integral_constant<int, kBF16>{}, std::integral_constant<int, 2>{});
+    };
+    if (a.up.x_dtype != kBF16 || kbw > 2) return false;
+    switch (a.up.w13.mode) {
+        case 0: by_kbw(std::integral_constant<int, 0>{}); break;
+        case 1: by_kbw(std::integral_constant<int, 1>{}); break;
+        case 2: by_kbw(std::integral_constant<int, 2>{}); break;
+        default: return false;
+    }
+    return ok;
 }
 
 template <int MODE, bool GATEUP, bool F16>

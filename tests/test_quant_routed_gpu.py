@@ -3,7 +3,9 @@ dmoe_quant_moe_layer) for modes 0-3: the routes it returns are the router
 kernel's bits (dmoe_route_topk), and its output is bit-for-bit the expert
 call on those routes -- whether the small-call gate/up kernel routes the call
 itself (decode sizes, up to 128 experts and top-8) or the router kernel runs
-first (larger calls, more experts, the separate launches)."""
+first (larger calls, more experts, the separate launches).  At decode sizes
+that give one workgroup per CU (modes 0-2, bf16 rows) the routed call is one
+persistent launch, checked against the two small-call launches."""
 from __future__ import annotations
 
 import pytest
@@ -78,3 +80,71 @@ def test_routed_layer_in_hipgraph(cuda):
         torch.cuda.synchronize()
         assert torch.equal(i_g, i_e) and torch.equal(w_g, w_e), step
         assert torch.equal(out, expected), step
+
+
+_BANKS = {}
+
+
+def model_bank(mode, hidden, inter, device):
+    key = (mode, hidden, inter)
+    if key not in _BANKS:
+        g = torch.Generator().manual_seed(7900 + 10 * mode + inter)
+        _BANKS[key] = to_device(random_quantized_bank(mode, 128, hidden, inter, asymmetric=mode == 0, generator=g),
+                                device)
+    return _BANKS[key]
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("hidden,inter", [(2048, 768), (2048, 512)])
+def test_routed_decode_at_model_sizes(cuda, launches, mode, hidden, inter):
+    """One token over 128 experts at top-8, at the 30B-A3B expert shape and
+    a narrower one: the routed small call runs as one persistent launch there
+    (its gate/up workgroups publish the hidden rows as hand-off words, its
+    down workgroups poll them), and it equals the expert call on the same
+    routes (the two small-call launches) bit for bit, over several calls in a
+    row (the hand-off buffers alternate between calls)."""
+    print_case("packed routed decode, model sizes", mode, hidden, inter)
+    launches(True)
+    bank = model_bank(mode, hidden, inter, cuda)
+    backend = QuantizedExpertBackend(mode)
+    g = torch.Generator().manual_seed(7950 + mode + inter)
+    for call in range(3):
+        x = torch.randn(1, hidden, generator=g).bfloat16().to(cuda)
+        logits = torch.randn(1, 128, generator=g).to(cuda)
+        out, weights, ids = backend.forward_routed(x, logits, 8, bank)
+        want = backend.forward(x, ids, weights, bank)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), call
+    assert backend.status(cuda) == 0
+
+
+def test_routed_decode_sync_timeout_is_reported(cuda, launches):
+    """The host forces the persistent packed decode's bounded hand-off wait
+    to give up (its readers wait for a tag no producer writes, up to a 100 us
+    bound): the status word carries DMOE_STATUS_SYNC_TIMEOUT, every launch
+    completes, and with the switch off the next call is exact again."""
+    print_case("packed routed decode, forced sync timeout")
+    launches(True)
+    lib = _lib.library()
+    bank = model_bank(0, 2048, 768, cuda)
+    backend = QuantizedExpertBackend(0)
+    g = torch.Generator().manual_seed(7990)
+    x = torch.randn(1, 2048, generator=g).bfloat16().to(cuda)
+    logits = torch.randn(1, 128, generator=g).to(cuda)
+    expected, _, _ = backend.forward_routed(x, logits, 8, bank)
+    torch.cuda.synchronize()
+    assert backend.status(cuda) == 0
+    previous = lib.dmoe_set_sync_spin_limit(10_000)  # 100 us of the 100 MHz counter
+    forced = lib.dmoe_debug_force_sync_timeout(1)
+    try:
+        for _ in range(2):
+            backend.forward_routed(x, logits, 8, bank)
+        torch.cuda.synchronize()
+    finally:
+        lib.dmoe_debug_force_sync_timeout(forced)
+        lib.dmoe_set_sync_spin_limit(previous)
+    assert backend.status(cuda) & _lib.STATUS_SYNC_TIMEOUT
+    again, _, _ = backend.forward_routed(x, logits, 8, bank)
+    torch.cuda.synchronize()
+    assert backend.status(cuda) == 0
+    assert torch.equal(again, expected)
