@@ -78,16 +78,15 @@ __device__ __forceinline__ v8i load_block_linear(const uint8_t* lo_row, const ui
 // A linearly loaded block into the MFMA operand layout (lane (col, grp):
 // row col, bytes 32 grp .. + 31) through a 2 KB LDS slot of the wave: the
 // 16-byte chunk c of row r sits at chunk c ^ (r % 8), so neither the writes
-// nor the reads share banks.  The wave's LDS operations run in issue order;
-// the empty asm statements keep the compiler from reordering them.
+// nor the reads share banks.  The wave's LDS operations run in issue order,
+// and the compiler keeps each read after the writes and each later write
+// after the reads (the lanes' slot addresses may coincide), free to
+// interleave consecutive blocks' staging with their MFMAs.
 __device__ __forceinline__ v8i stage_block(const v8i& raw, v4i* slot) {
     const int lane = threadIdx.x % kWave, r = lane / 8, j = lane % 8, col = lane % 16, grp = lane / 16;
-    asm volatile("" ::: "memory");
     slot[r * 8 + (j ^ r)] = v4i{raw[0], raw[1], raw[2], raw[3]};
     slot[(r + 8) * 8 + (j ^ r)] = v4i{raw[4], raw[5], raw[6], raw[7]};
-    asm volatile("" ::: "memory");
     const v4i a0 = slot[col * 8 + ((2 * grp) ^ (col % 8))], a1 = slot[col * 8 + ((2 * grp + 1) ^ (col % 8))];
-    asm volatile("" ::: "memory");
     return v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
 }
 
