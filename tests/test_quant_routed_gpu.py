@@ -26,8 +26,9 @@ def to_device(store, device):
 
 
 @pytest.fixture
-def launches():
+def launches(cuda):
     lib = _lib.library()
+    QuantizedExpertBackend.status(cuda)  # start from a clear status word (earlier tests raise bits on purpose)
     yield lambda small: lib.dmoe_set_fused_decode(1 if small else 0)
     lib.dmoe_set_fused_decode(1)
 
